@@ -1,0 +1,466 @@
+"""Pin the C oracle against the reference's own test formulas, closed forms and
+brute force. CPU only.
+
+Each test names the reference test or kernel whose behaviour it checks.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+
+BF = oracle.f32_to_bf16
+F = oracle.bf16_to_f32
+
+
+def kron_rotation() -> np.ndarray:
+    """The radix-4 stage is the 4x4 matrix below on one base-4 digit of the
+    index; four stages give its 4-fold Kronecker power
+    (kernels/prepare_integer_single.loom:109-116)."""
+    m4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=np.float64)
+    h = m4
+    for _ in range(3):
+        h = np.kron(h, m4)
+    return h
+
+
+# ---------------------------------------------------------------- rotation
+
+def test_rotation_is_kronecker_power_and_orthogonal():
+    h = kron_rotation()
+    assert np.array_equal(h @ h.T, 256.0 * np.eye(256))
+    for i in range(256):
+        e = np.zeros(256, dtype=np.float32)
+        e[i] = 1.0
+        assert np.array_equal(oracle.rotate256(e), h[:, i].astype(np.float32)), i
+
+
+def test_rotation_exact_on_representable_inputs():
+    # multiples of 2^-8 bounded by 4: every partial sum fits in 24 bits, so the
+    # f32 radix-4 result equals the float64 matrix product exactly.
+    rng = np.random.default_rng(7)
+    h = kron_rotation()
+    for _ in range(20):
+        x = (rng.integers(-1024, 1024, size=256) / 256.0).astype(np.float32)
+        assert np.array_equal(oracle.rotate256(x).astype(np.float64), h @ x.astype(np.float64))
+
+
+def test_rotation_preserves_inner_product():
+    """src/quantized.rs:858-876."""
+    a = F(BF(np.array([((i * 17 % 71) - 35.0) / 64.0 for i in range(512)], dtype=np.float32)))
+    b = F(BF(np.array([((i * 31 % 59) - 29.0) / 64.0 for i in range(512)], dtype=np.float32)))
+    expected = float(np.dot(a.astype(np.float64), b.astype(np.float64)))
+    ra = np.concatenate([oracle.rotate256(a[:256]), oracle.rotate256(a[256:])])
+    rb = np.concatenate([oracle.rotate256(b[:256]), oracle.rotate256(b[256:])])
+    actual = float(np.sum(ra.astype(np.float64) * rb.astype(np.float64) / 256.0))
+    assert abs(actual - expected) < 1e-8
+
+
+# ---------------------------------------------------------------- Q1
+
+def decode_codes(words: np.ndarray, width: int, bits: int = 4) -> np.ndarray:
+    per = 32 // bits
+    w = words[:, : width // per].astype(np.uint64)
+    shifts = (np.arange(per, dtype=np.uint64) * bits)
+    vals = ((w[:, :, None] >> shifts) & ((1 << bits) - 1)).astype(np.int64)
+    vals = np.where(vals >= (1 << (bits - 1)), vals - (1 << bits), vals)
+    return vals.reshape(words.shape[0], width)
+
+
+def reference_test_quantize(row_f32: np.ndarray, bits: int):
+    """The reference test oracle, src/quantized.rs:1094-1113 (f32 numpy)."""
+    width = row_f32.shape[0]
+    rot = np.concatenate([oracle.rotate256(row_f32[g:g + 256]) for g in range(0, width, 256)])
+    max_code = np.float32((1 << (bits - 1)) - 1)
+    m = np.float32(np.max(np.abs(rot))) if width else np.float32(0)
+    scale = np.float32(max(np.float32(m / np.float32(16.0)), np.float32(1e-30)) / max_code)
+    inv = np.float32(np.float32(0.0625) / scale)
+    codes = np.clip(np.rint((rot * inv).astype(np.float32)), -max_code, max_code).astype(np.int64)
+    return codes, scale
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("width", [256, 768, 1280, 2048, 5120, 6144, 8192, 17408])
+def test_prepare_matches_reference_test_oracle(bits, width):
+    """rotated_packing_cpu_oracle inputs: zero row, e_0, ((i*37%257)-128)/91
+    (src/quantized.rs:1074-1129)."""
+    vals = np.zeros((3, width), dtype=np.float32)
+    vals[1, 0] = 1.0
+    vals[2] = [((i * 37 % 257) - 128.0) / 91.0 for i in range(width)]
+    x = BF(vals)
+    stride = width + 512 // bits
+    codes, scales, _ = oracle.prepare(x, stride, bits)
+    for row in range(3):
+        want_codes, want_scale = reference_test_quantize(F(x[row]), bits)
+        assert scales[row] == want_scale, (row, scales[row], want_scale)
+        got = decode_codes(codes[row:row + 1], width, bits)[0]
+        assert np.array_equal(got, want_codes), row
+
+
+def test_prepare_closed_forms():
+    h = kron_rotation()
+    width = 256
+    x = np.zeros((4, width), dtype=np.float32)
+    x[0, 0] = 1.0          # e_0: rotated row is column 0 of H, all +-1
+    x[1, :] = 2.0          # constant: H.1 = 16.1, so every code is +7
+    x[2, 5] = -0.5
+    x[3, :] = 0.0          # zero row: scale = 1e-30/7, codes 0
+    codes, scales, _ = oracle.prepare(BF(x), 384, 4)
+    c = decode_codes(codes, width)
+    s7 = np.float32(np.float32(0.0625) / np.float32(7.0))
+    assert scales[0] == s7 and np.array_equal(c[0], 7 * h[:, 0].astype(np.int64))
+    assert scales[1] == np.float32(np.float32(2.0) / np.float32(7.0)) and np.all(c[1] == 7)
+    assert np.array_equal(c[2], -7 * h[:, 5].astype(np.int64))
+    assert scales[3] == np.float32(np.float32(1e-30) / np.float32(7.0)) and np.all(c[3] == 0)
+
+
+def exceptional_rows(width: int) -> np.ndarray:
+    """The seven rows of register_packing_matches_reference
+    (src/quantized.rs:1138-1150): 0, 1, ((c*37%257)-128)/91, -0.5 with NaN at
+    column 259, -0.5 with +inf at column 515, bf16::MAX, bf16 denormal."""
+    x = np.full((7, width), BF(np.float32(-0.5)), dtype=np.uint16)
+    x[0, :] = 0
+    x[1, :] = BF(np.float32(1.0))
+    x[2, :] = BF(np.array([((c * 37 % 257) - 128.0) / 91.0 for c in range(width)], np.float32))
+    x[3, 259] = 0x7FC0
+    x[4, 515] = 0x7F80
+    x[5, :] = 0x7F7F
+    x[6, :] = 0x0001
+    return x
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("width", [768, 5120, 6144, 17408])
+def test_prepare_exceptional_rows(bits, width):
+    """NaN or Inf anywhere in a row (or an overflowing rotation, as for a row of
+    bf16::MAX) -> scale +inf and all-zero codes; the other rows follow the
+    reference test oracle."""
+    x = exceptional_rows(width)
+    codes, scales, _ = oracle.prepare(x, width + 512 // bits, bits)
+    c = decode_codes(codes, width, bits)
+    for r in (3, 4, 5):
+        assert np.isinf(scales[r]) and scales[r] > 0 and np.all(c[r] == 0), r
+    for r in (0, 1, 2, 6):
+        assert np.isfinite(scales[r]) and scales[r] > 0, r
+        want, wscale = reference_test_quantize(F(x[r]), bits)
+        assert wscale == scales[r] and np.array_equal(c[r], want), r
+    assert np.max(np.abs(c[2])) == (7 if bits == 4 else 127)
+    assert np.all(c[6] == 0) and np.all(c[0] == 0)
+
+
+def test_prepare_padding_words_untouched():
+    x = BF(np.ones((2, 1024), dtype=np.float32))
+    codes, _, storage = oracle.prepare(x, 1024 + 128, 4)
+    assert np.all(codes[:, 128:] == 0)  # storage was zero-filled; padding unwritten
+
+
+# ---------------------------------------------------------------- Q2
+
+def test_retile_block_formula():
+    """retiled_codes_match_block_formula (src/quantized.rs:1371-1407)."""
+    rows, cols = 256, 512
+    words = cols // 8
+    in_words = words + 16
+    codes = (np.arange(rows)[:, None] * 100000 + np.arange(in_words)[None, :]).astype(np.uint32)
+    tiled = oracle.retile(codes, cols)
+    assert tiled.shape == (rows * words,)
+    for n in range(rows):
+        for q in range(words):
+            idx = ((n // 128) * (words // 32) + q // 32) * 4096 + (n % 128) * 32 + q % 32
+            assert tiled[idx] == codes[n, q]
+    # a permutation of the logical words; padding dropped
+    assert np.array_equal(np.sort(tiled), np.sort(codes[:, :words].ravel()))
+
+
+def test_retile_rejects_bad_shapes():
+    with pytest.raises(oracle.OracleError, match="unsupported packed weight shape for tiling"):
+        oracle.retile(np.zeros((100, 64), np.uint32), 512)
+
+
+# ---------------------------------------------------------------- G1
+
+def random_codes(rng, rows, width, stride):
+    vals = rng.integers(-7, 8, size=(rows, width))
+    words = np.zeros((rows, stride // 8), dtype=np.uint32)
+    nib = (vals & 0xF).astype(np.uint32).reshape(rows, width // 8, 8)
+    words[:, : width // 8] = np.bitwise_or.reduce(nib << (np.arange(8, dtype=np.uint32) * 4), axis=2)
+    return vals, words
+
+
+def test_gemm_acc_brute_force():
+    rng = np.random.default_rng(3)
+    m, n, k = 37, 256, 768
+    a_vals, a_words = random_codes(rng, m, k, k + 0)
+    w_vals, w_words = random_codes(rng, n, k, k)
+    tiled = oracle.retile(w_words, k)
+    acc = oracle.gemm_acc(a_words, tiled, n, k)
+    assert np.array_equal(acc.astype(np.int64), a_vals @ w_vals.T)
+
+
+def test_gemm_epilogue_power_of_two_scales():
+    rng = np.random.default_rng(4)
+    m, n, k = 16, 128, 256
+    a_vals, a_words = random_codes(rng, m, k, k + 128)
+    w_vals, w_words = random_codes(rng, n, k, k)
+    tiled = oracle.retile(w_words, k)
+    a_s = (2.0 ** rng.integers(-10, 3, size=m)).astype(np.float32)
+    w_s = (2.0 ** rng.integers(-10, 3, size=n)).astype(np.float32)
+    out = oracle.gemm(a_words, a_s, tiled, w_s, n, k)
+    exact = (a_vals @ w_vals.T).astype(np.float64) * w_s[None, :].astype(np.float64) * a_s[:, None]
+    assert np.array_equal(out, BF(exact.astype(np.float32)))  # exact before the bf16 step
+    # residual: bf16(f32(res) + f32(out))
+    res = BF(rng.standard_normal((m, n)).astype(np.float32))
+    out_r = oracle.gemm(a_words, a_s, tiled, w_s, n, k, residual=res)
+    assert np.array_equal(out_r, BF(F(res) + F(out)))
+
+
+def test_gemm_saturation_and_nonfinite_rows():
+    k, n = 256, 128
+    a = np.zeros((3, 256), np.float32)
+    a[0, :] = 1.0
+    a[1, :] = 1.0
+    a[2, 0] = np.nan
+    codes, scales, _ = oracle.prepare(BF(a), k, 4)
+    w = np.zeros((n, k), np.float32)
+    w[:, :] = 1.0
+    w_t, w_s = oracle.pack_weight(BF(w))
+    acc = oracle.gemm_acc(codes, w_t, n, k)
+    r0 = np.float32(np.float32(acc[1, 0]) * w_s[0])
+    big = scales.copy()
+    big[1] = np.float32(np.float32(3.4e38) / r0)         # finite y above the bf16 range
+    y = np.float32(r0 * big[1])
+    assert np.isfinite(y) and y > np.float32(3.3895313892515355e38)
+    out = F(oracle.gemm(codes, big, w_t, w_s, n, k))
+    assert np.all(out[0] == F(BF(np.float32(256.0))))  # 256 ones . ones
+    assert np.all(out[1] == F(np.uint16(0x7F7F)))       # finite overflow clamps to bf16::MAX
+    assert np.all(np.isnan(out[2]))                     # 0 * inf scale stays observable
+    big[1] = np.float32(3e38)                            # f32 overflow is not clamped
+    out = F(oracle.gemm(codes, big, w_t, w_s, n, k))
+    assert np.all(np.isposinf(out[1]))
+
+
+def test_identity_weight_round_trip():
+    """activation_scratch_is_bounded (src/quantized.rs:880-915): identity
+    weights reproduce rows 1 + r/16 exactly through 32 layers."""
+    w = np.eye(256, dtype=np.float32)
+    w_t, w_s = oracle.pack_weight(BF(w))
+    x0 = BF(np.array([[1.0 + r / 16.0] * 256 for r in range(17)], dtype=np.float32))
+    x = x0
+    for _ in range(32):
+        codes, scales, _ = oracle.prepare(x, 256, 4)
+        x = oracle.gemm(codes, scales, w_t, w_s, 256, 256)
+    assert np.array_equal(x, x0)
+
+
+def test_packed_weights_cpu_dot_tolerance():
+    """packed_weights_survive_plan_reset oracle (src/quantized.rs:979-1070):
+    bf16(dot*as*ws) within one bf16 step of the product, on its inputs."""
+    vals = F(BF(np.array([((i * 17 % 251) - 125.0) / 128.0 for i in range(256 * 256)], np.float32)))
+    w_t, w_s = oracle.pack_weight(BF(vals.reshape(256, 256)))
+    xin = F(BF(np.array([((i * 31 % 257) - 128.0) / 64.0 for i in range(18 * 256)], np.float32)))
+    codes, scales, _ = oracle.prepare(BF(xin.reshape(18, 256)), 256, 4)
+    out = F(oracle.gemm(codes, scales, w_t, w_s, 256, 256))
+    acc = oracle.gemm_acc(codes, w_t, 256, 256)
+    expected = F(BF((acc.astype(np.float32) * scales[:, None]) * w_s[None, :]))
+    assert np.all(np.isfinite(out))
+    assert np.all(np.abs(out - expected) <= np.maximum(np.abs(out), np.abs(expected)) / 128 + 1e-6)
+
+
+# ---------------------------------------------------------------- R1
+
+def router_phase_values(tokens, experts, phase):
+    """OmniRouterBenchmark phases (src/benchmarking/omni.rs:42-55)."""
+    i = np.arange(tokens * experts)
+    if phase == 0:
+        v = ((i * 37 + i // experts * 11) % 257) / 16.0 - 8.0
+    elif phase == 1:
+        v = ((i * 53 + i // experts * 7) % 5) - 2.0
+    elif phase == 2:
+        v = np.where(i % 2 == 0, 0.0, -0.0)
+    else:
+        v = ((i * 79 + i // experts * 17) % 263) * 16.0 - 2048.0
+    return v.astype(np.float32).reshape(tokens, experts)
+
+
+@pytest.mark.parametrize("phase", [0, 1, 2, 3])
+@pytest.mark.parametrize("bf16_logits", [False, True])
+def test_route_matches_stable_sort(phase, bf16_logits):
+    tokens, experts, topk = 65, 128, 8
+    v = router_phase_values(tokens, experts, phase)
+    logits = BF(v) if bf16_logits else v
+    if bf16_logits:
+        v = F(logits)
+    routes = oracle.route(logits, topk)
+    for t in range(tokens):
+        order = sorted(range(experts), key=lambda e: -float(v[t, e]))  # stable, ties -> lower id
+        assert [int(x) for x in routes[t, :topk]] == order[:topk]
+        sel = np.array([v[t, e] for e in order[:topk]], dtype=np.float64)
+        p = np.exp(sel - sel[0])
+        want = p / p.sum()
+        got = routes[t, topk:].astype(np.float64)
+        # bf16-rounded probabilities: within one bf16 step of the exact value
+        assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-30)
+
+
+def test_route_experts_below_128_and_bad_shape():
+    v = router_phase_values(3, 60, 0)
+    routes = oracle.route(v, 4)
+    for t in range(3):
+        order = sorted(range(60), key=lambda e: -float(v[t, e]))
+        assert [int(x) for x in routes[t, :4]] == order[:4]
+    with pytest.raises(oracle.OracleError, match="invalid expert router shape"):
+        oracle.route(np.zeros((2, 129), np.float32), 8)
+
+
+# ---------------------------------------------------------------- R2 / R3
+
+def grouped_phase_routes(tokens, phase, topk=8):
+    """grouped_routes_match_cpu (src/omni.rs:908-942)."""
+    routes = np.zeros((tokens, 2 * topk), np.float32)
+    for t in range(tokens):
+        for r in range(topk):
+            routes[t, r] = ((0 if phase == 1 else t * 13) + r * 7 + phase * 19) % 128
+    return routes
+
+
+@pytest.mark.parametrize("tokens", [1, 17, 64, 65, 128, 255, 256, 511, 512, 1023, 1024, 2047, 2048])
+def test_group_routes_brute_force(tokens):
+    for phase in range(3):
+        routes = grouped_phase_routes(tokens, phase)
+        groups, order = oracle.group_routes(routes)
+        expected = [[] for _ in range(128)]
+        for t in range(tokens):
+            for r in range(8):
+                expected[int(routes[t, r])].append(t * 8 + r)
+        for e in range(128):
+            assert groups[e, 0] == len(expected[e])
+            assert np.array_equal(groups[e, 1:1 + len(expected[e])], np.array(expected[e], np.float32))
+        # order: ranks sorted by expert id (total order)
+        want = np.argsort(routes[:, :8], axis=1, kind="stable")
+        assert np.array_equal(order, want.astype(np.float32))
+        tasks = oracle.expert_tasks(groups)
+        pairs = [(e, 16 * j) for e in range(128) for j in range((len(expected[e]) + 15) // 16)]
+        assert tasks[0] == len(pairs)
+        assert np.array_equal(tasks[1:1 + 2 * len(pairs)], np.array(pairs, np.float32).ravel())
+
+
+# ---------------------------------------------------------------- E1
+
+def test_expert_matches_dense_oracle_on_routed_rows():
+    rng = np.random.default_rng(11)
+    tokens, topk, k, n = 23, 8, 512, 256
+    logits = rng.standard_normal((tokens, 128)).astype(np.float32)
+    routes = oracle.route(logits, topk)
+    groups, _ = oracle.group_routes(routes)
+    x = BF(rng.standard_normal((tokens, k)).astype(np.float32))
+    codes, scales, _ = oracle.prepare(x, k, 4)
+    w = BF((0.02 * rng.standard_normal((128 * n, k))).astype(np.float32))
+    w_t, w_s = oracle.pack_weight(w)
+    out = oracle.expert_i4(codes, scales, w_t, w_s, groups, tokens, topk, k, n, False)
+    acc = oracle.gemm_acc(codes, w_t, 128 * n, k)  # every token x every expert row
+    for t in range(tokens):
+        for r in range(topk):
+            e = int(routes[t, r])
+            cols = slice(e * n, (e + 1) * n)
+            s = (scales[t] * w_s[cols]).astype(np.float32)
+            want = BF((acc[t, cols].astype(np.float32) * s).astype(np.float32))
+            assert np.array_equal(out[t * topk + r], want)
+
+
+# ---------------------------------------------------------------- S1 / exp
+
+def test_expf_within_two_ulp():
+    xs = np.concatenate([np.linspace(-103.0, 88.7, 200001, dtype=np.float32),
+                         F(np.arange(0, 65536, dtype=np.uint16))])
+    xs = xs[np.isfinite(xs) & (xs > -103.0) & (xs < 88.7)]
+    got = np.array([oracle.expf(float(x)) for x in xs[::7]], dtype=np.float32)
+    want = np.exp(xs[::7].astype(np.float64))
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    ulp = np.maximum(ulp, 2.0 ** -149)
+    assert np.max(np.abs(got - want) / ulp) <= 2.0
+    assert oracle.expf(0.0) == 1.0
+    assert math.isinf(oracle.expf(100.0)) and oracle.expf(-200.0) == 0.0
+
+
+def test_swiglu_every_bf16_gate():
+    """S1 over every bf16 gate value (kernels/swiglu.loom:43-51) against a
+    float64 SiLU: each of the two bf16 roundings adds at most half a step."""
+    g = np.arange(65536, dtype=np.uint16)
+    gf = F(g).astype(np.float64)
+    # exp(-g) overflows f32 below g = -88.72: the f32 formula then gives
+    # g / inf = -0, as the reference kernel does.
+    overflow = gf < -88.72283935546875
+    for u_val in (1.0, -3.5, 0.0078125):
+        u = np.full_like(g, BF(np.float32(u_val)))
+        h = F(oracle.swiglu(g, u)).astype(np.float64)
+        with np.errstate(over="ignore", invalid="ignore"):
+            silu = gf / (1.0 + np.exp(-gf))
+        want = silu * u_val
+        # above the bf16 range the product rounds to +-inf
+        big = np.abs(want) >= 3.3961775292304601e38
+        assert np.all(np.isinf(h[big & np.isfinite(want)]))
+        fin = np.isfinite(want) & np.isfinite(gf) & ~overflow & ~big
+        # bf16(silu) then bf16(. * u): half a step each, the first scaled by |u|
+        half = 2.0 ** -8
+        tol = (abs(u_val) * (np.abs(silu) * half + 2.0 ** -134)
+               + np.abs(want) * (half + 2.0 ** -20) + 2.0 ** -134)
+        assert np.all(np.abs(h[fin] - want[fin]) <= tol[fin])
+        assert np.all(h[overflow & np.isfinite(gf)] == 0.0)
+        assert np.all(np.isnan(h[np.isnan(gf)]))
+
+
+# ---------------------------------------------------------------- C1 / MoE
+
+def test_sparse_moe_oracle_matches_reference_formula():
+    """routed_experts_match_sparse_cpu_oracle (src/omni.rs:946-1051), INT4:
+    identity-scaled experts applied twice, combined in ascending expert order,
+    within the reference's 0.08 absolute tolerance."""
+    experts, topk = 128, 8
+    logits = BF(np.array([((i * 37 + i // experts * 11) % experts) / 16.0 for i in range(3 * experts)],
+                         np.float32).reshape(3, experts))
+    inp = BF(np.array([(i % 17) / 16.0 - 0.5 for i in range(3 * 256)], np.float32).reshape(3, 256))
+    rows = np.arange(experts * 256)
+    w = np.zeros((experts * 256, 256), np.float32)
+    w[rows, rows % 256] = (rows // 256 + 1) / 128.0
+    w_t, w_s = oracle.pack_weight(BF(w))
+    routes = oracle.route(logits, topk)
+    groups, order = oracle.group_routes(routes)
+    codes, scales, _ = oracle.prepare(inp, 256, 4)
+    values = oracle.expert_i4(codes, scales, w_t, w_s, groups, 3, topk, 256, 256, False)
+    codes2, scales2, _ = oracle.prepare(values, 256, 4)
+    values2 = oracle.expert_i4(codes2, scales2, w_t, w_s, groups, 3, topk, 256, 256, True)
+    out = F(oracle.combine(values2, routes))
+    out_ordered = F(oracle.combine(values2, routes, order))
+    assert np.array_equal(out, out_ordered)
+    lf = F(logits)
+    xf = F(inp)
+    for t in range(3):
+        ranked = sorted(range(experts), key=lambda e: -float(lf[t, e]))
+        assert [int(v) for v in routes[t, :topk]] == ranked[:topk]
+        mx = lf[t, ranked[0]]
+        sel = [(e, np.float32(np.exp(np.float32(lf[t, e] - mx)))) for e in ranked[:topk]]
+        s = np.float32(sum(p for _, p in sel))
+        sel = sorted([(e, F(BF(np.float32(p / s)))) for e, p in sel])
+        for col in range(256):
+            acc = np.float32(0.0)
+            for e, p in sel:
+                y = F(BF(np.float32(xf[t, col] * np.float32((e + 1) / 128.0))))
+                y = F(BF(np.float32(y * np.float32((e + 1) / 128.0))))
+                y = F(BF(np.float32(y * p)))
+                acc = F(BF(np.float32(acc + y)))
+            assert abs(out[t, col] - acc) <= 0.08, (t, col, out[t, col], acc)
+
+
+def test_checkpoint_tiles_round_trip():
+    """src/checkpoint.rs:63-106: [rows][cols] <-> [rows/256][cols/64][256][64]."""
+    rows, cols = 512, 192
+    w = np.arange(rows * cols, dtype=np.uint32).astype(np.uint16).reshape(rows, cols)
+    t = oracle.tile_rows(w)
+    flat = t.ravel()
+    for tile in range(rows // 256):
+        for ks in range(cols // 64):
+            for r in (0, 1, 255):
+                base = tile * 256 * cols + (ks * 256 + r) * 64
+                assert np.array_equal(flat[base:base + 64], w[tile * 256 + r, ks * 64:(ks + 1) * 64])
+    assert np.array_equal(oracle.untile_rows(t), w)
