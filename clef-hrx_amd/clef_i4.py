@@ -1,0 +1,340 @@
+"""Python binding of the gfx950 INT4 path (C ABI in include/clef_i4.h).
+
+A thin ctypes layer: torch supplies device memory and the current HIP stream,
+the library does all the work. Function names follow the reference's operator
+API (src/quantized.rs, src/omni.rs, src/ops.rs) so callers read the same:
+outputs are allocated here (as the reference's Engine allocates them) and the
+C entry points only write into them.
+
+Import fails loudly when lib/libclef_i4.so is missing: there is no fallback
+path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libclef_i4.so")
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/clef_i4.h.
+SIGNATURES = {
+    "clef_last_error": (ctypes.c_char_p, []),
+    "clef_abi_version": (ctypes.c_int, []),
+    "clef_i4_activation_stride": (_I32, [_I32, _I32]),
+    "clef_i4_prepared_words": (_I64, [_I64, _I32, _I32]),
+    "clef_i4_prepare": (ctypes.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P]),
+    "clef_i4_prepare_swiglu": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P]),
+    "clef_i4_retile": (ctypes.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P]),
+    "clef_i4_pack_weight_workspace_bytes": (_SZ, [_I64, _I32, _I32]),
+    "clef_i4_pack_weight": (ctypes.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _SZ, _P]),
+    "clef_untile_rows": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
+    "clef_tile_rows": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
+    "clef_i4_gemm": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P]),
+    "clef_i4_gemm_config": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I64, _I32, _I32, _P, _P, _I32, _P]),
+    "clef_i4_gemm_configs": (ctypes.c_int, []),
+    "clef_i4_project_workspace_bytes": (_SZ, [_I64, _I32]),
+    "clef_i4_project": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _I32, _P, _P, _P, _SZ, _P]),
+    "clef_moe_route": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _P, _P]),
+    "clef_moe_group_workspace_bytes": (_SZ, [_I64]),
+    "clef_moe_group_routes": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _SZ, _P]),
+    "clef_moe_expert_tasks": (ctypes.c_int, [_P, _I64, _P, _P]),
+    "clef_moe_expert_workspace_bytes": (_SZ, [_I64, _I32]),
+    "clef_moe_expert_i4": (ctypes.c_int, [_P, _I32, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P,
+                                          _P, _SZ, _P]),
+    "clef_swiglu": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
+    "clef_moe_combine": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _I32, _P, _P]),
+    "clef_moe_layer_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
+    "clef_moe_layer": (ctypes.c_int, [_P, _P, _I32, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P,
+                                      _P, _P, _P, _SZ, _P]),
+}
+
+_lib = None
+
+
+class ClefError(RuntimeError):
+    """A failed entry point: precondition (code -1) or HIP error (code > 0)."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built; run `make -C clef-hrx_amd` "
+                              "(or __graft_entry__.build())")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise ClefError(rc, lib().clef_last_error().decode())
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    assert t.is_cuda and t.is_contiguous(), "device tensors must be contiguous CUDA tensors"
+    return t.data_ptr()
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _empty(shape, dtype, device):
+    return torch.empty(shape, dtype=dtype, device=device)
+
+
+# ---------------------------------------------------------------- Q1 / Q2
+
+def activation_stride(width: int, bits: int = 4) -> int:
+    """src/quantized.rs:161-166."""
+    return int(lib().clef_i4_activation_stride(width, bits))
+
+
+@dataclass
+class Prepared:
+    """quantized::prepare output: one u32 buffer, codes then f32 scales."""
+    storage: torch.Tensor  # int32 [rows * (words + 1)]
+    rows: int
+    width: int
+    stride: int
+    bits: int
+
+    @property
+    def words(self) -> int:
+        return self.stride // (32 // self.bits)
+
+    @property
+    def codes(self) -> torch.Tensor:
+        return self.storage[: self.rows * self.words].view(self.rows, self.words)
+
+    @property
+    def scales(self) -> torch.Tensor:
+        return self.storage[self.rows * self.words:].view(torch.float32)
+
+
+def prepare(x: torch.Tensor, bits: int = 4, stride: int | None = None, out: torch.Tensor | None = None
+            ) -> Prepared:
+    """quantized::prepare (src/quantized.rs:574-686)."""
+    rows, width = x.shape
+    stride = activation_stride(width, bits) if stride is None else stride
+    words = int(lib().clef_i4_prepared_words(rows, stride, bits))
+    if out is None:
+        out = torch.zeros(max(words, 1), dtype=torch.int32, device=x.device)
+    _check(lib().clef_i4_prepare(_ptr(x), rows, width, stride, bits, _ptr(out), _stream()))
+    return Prepared(out, rows, width, stride, bits)
+
+
+def prepare_swiglu(gate: torch.Tensor, up: torch.Tensor, bits: int = 4, stride: int | None = None
+                   ) -> Prepared:
+    """prepare_with_inputs([gate, up]) (src/quantized.rs:605-613)."""
+    rows, width = gate.shape
+    stride = activation_stride(width, bits) if stride is None else stride
+    words = int(lib().clef_i4_prepared_words(rows, stride, bits))
+    out = torch.zeros(max(words, 1), dtype=torch.int32, device=gate.device)
+    _check(lib().clef_i4_prepare_swiglu(_ptr(gate), _ptr(up), rows, width, stride, bits, _ptr(out),
+                                        _stream()))
+    return Prepared(out, rows, width, stride, bits)
+
+
+def retile_codes(codes: torch.Tensor, rows: int, cols: int, bits: int = 4) -> torch.Tensor:
+    """quantized::retile_codes (src/quantized.rs:542-572); codes [rows][in_words]."""
+    in_words = codes.shape[1]
+    tiled = torch.empty(rows * cols // (32 // bits), dtype=torch.int32, device=codes.device)
+    _check(lib().clef_i4_retile(_ptr(codes.contiguous()), rows, in_words, cols, bits, _ptr(tiled),
+                                _stream()))
+    return tiled
+
+
+@dataclass
+class QuantizedWeight:
+    """src/quantized.rs:12-20."""
+    codes: torch.Tensor   # int32 tiled words
+    scales: torch.Tensor  # f32 [rows]
+    rows: int
+    cols: int
+    stride: int
+    bits: int
+
+
+def load_quantized_weight(w: torch.Tensor, bits: int = 4, tiled_checkpoint: bool = False
+                          ) -> QuantizedWeight:
+    """Packing half of Engine::load_quantized_weight (src/quantized.rs:147-234)."""
+    rows, cols = w.shape
+    if tiled_checkpoint:
+        dense = torch.empty_like(w)
+        _check(lib().clef_untile_rows(_ptr(w), rows, cols, _ptr(dense), _stream()))
+        w = dense
+    codes = torch.empty(rows * cols // (32 // bits), dtype=torch.int32, device=w.device)
+    scales = torch.empty(rows, dtype=torch.float32, device=w.device)
+    ws_bytes = int(lib().clef_i4_pack_weight_workspace_bytes(rows, cols, bits))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=w.device)
+    _check(lib().clef_i4_pack_weight(_ptr(w), rows, cols, bits, _ptr(codes), _ptr(scales), _ptr(ws),
+                                     ws_bytes, _stream()))
+    return QuantizedWeight(codes, scales, rows, cols, activation_stride(cols, bits), bits)
+
+
+def untile_rows(tiled: torch.Tensor) -> torch.Tensor:
+    rows, cols = tiled.shape
+    out = torch.empty_like(tiled)
+    _check(lib().clef_untile_rows(_ptr(tiled), rows, cols, _ptr(out), _stream()))
+    return out
+
+
+def tile_rows(dense: torch.Tensor) -> torch.Tensor:
+    rows, cols = dense.shape
+    out = torch.empty_like(dense)
+    _check(lib().clef_tile_rows(_ptr(dense), rows, cols, _ptr(out), _stream()))
+    return out
+
+
+# ---------------------------------------------------------------- G1
+
+def gemm_configs() -> int:
+    return int(lib().clef_i4_gemm_configs())
+
+
+def project_prepared(a: Prepared, w: QuantizedWeight, residual: torch.Tensor | None = None,
+                     config: int = -1, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Engine::project_prepared (src/quantized.rs:470-537)."""
+    if out is None:
+        out = _empty((a.rows, w.rows), torch.bfloat16, a.storage.device)
+    _check(lib().clef_i4_gemm_config(_ptr(a.storage), a.stride, _ptr(a.scales), _ptr(w.codes),
+                                     _ptr(w.scales), a.rows, w.rows, w.cols, _ptr(residual), _ptr(out),
+                                     config, _stream()))
+    return out
+
+
+def project_quantized(x: torch.Tensor, w: QuantizedWeight, residual: torch.Tensor | None = None
+                      ) -> torch.Tensor:
+    """Engine::project_quantized[_with_residual] (src/quantized.rs:235-303)."""
+    m, k = x.shape
+    out = _empty((m, w.rows), torch.bfloat16, x.device)
+    ws_bytes = int(lib().clef_i4_project_workspace_bytes(m, k))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=x.device)
+    _check(lib().clef_i4_project(_ptr(x), m, k, _ptr(w.codes), _ptr(w.scales), w.rows, _ptr(residual),
+                                 _ptr(out), _ptr(ws), ws_bytes, _stream()))
+    return out
+
+
+# ---------------------------------------------------------------- MoE
+
+def omni_route(logits: torch.Tensor, topk: int = 8) -> torch.Tensor:
+    """Engine::omni_route (src/omni.rs:170-190)."""
+    tokens, experts = logits.shape
+    dtype = 0 if logits.dtype == torch.bfloat16 else 1
+    routes = _empty((tokens, 2 * topk), torch.float32, logits.device)
+    _check(lib().clef_moe_route(_ptr(logits), dtype, tokens, experts, topk, _ptr(routes), _stream()))
+    return routes
+
+
+def omni_group_routes(routes: torch.Tensor, ordered: bool = True):
+    """Engine::omni_group_routes[_ordered] (src/omni.rs:192-245) -> (groups, order|None)."""
+    tokens = routes.shape[0]
+    topk = routes.shape[1] // 2
+    groups = torch.zeros((128, tokens + 1), dtype=torch.float32, device=routes.device)
+    order = torch.zeros((tokens, topk), dtype=torch.float32, device=routes.device) if ordered else None
+    ws_bytes = int(lib().clef_moe_group_workspace_bytes(tokens))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=routes.device)
+    _check(lib().clef_moe_group_routes(_ptr(routes), tokens, topk, _ptr(groups), _ptr(order), _ptr(ws),
+                                       ws_bytes, _stream()))
+    return groups, order
+
+
+def omni_expert_tasks(groups: torch.Tensor, topk: int = 8) -> torch.Tensor:
+    """omni_expert_tasks dispatch of Engine::omni_compact_routes (src/omni.rs:155-165)."""
+    tokens = groups.shape[1] - 1
+    tasks = torch.zeros(1 + 2 * ((tokens * topk + 15) // 16 + 127), dtype=torch.float32,
+                        device=groups.device)
+    _check(lib().clef_moe_expert_tasks(_ptr(groups), tokens, _ptr(tasks), _stream()))
+    return tasks
+
+
+def omni_expert(a: Prepared, w: QuantizedWeight, groups: torch.Tensor, tokens: int, topk: int,
+                input_routed: bool) -> torch.Tensor:
+    """Engine::omni_expert_impl (src/omni.rs:289-534); w holds 128 experts' rows."""
+    n = w.rows // 128
+    out = torch.zeros((tokens * topk, n), dtype=torch.bfloat16, device=groups.device)
+    ws_bytes = int(lib().clef_moe_expert_workspace_bytes(tokens, topk))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=groups.device)
+    _check(lib().clef_moe_expert_i4(_ptr(a.storage), a.stride, _ptr(a.scales), _ptr(w.codes),
+                                    _ptr(w.scales), _ptr(groups), tokens, topk, w.cols, n,
+                                    int(input_routed), _ptr(out), _ptr(ws), ws_bytes, _stream()))
+    return out
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """Engine::swiglu (src/ops.rs:9-29)."""
+    if gate.shape != up.shape:
+        raise ClefError(-1, "SwiGLU shape/dtype mismatch")
+    h = torch.empty_like(gate)
+    _check(lib().clef_swiglu(_ptr(gate), _ptr(up), gate.numel(), _ptr(h), _stream()))
+    return h
+
+
+def omni_combine(values: torch.Tensor, routes: torch.Tensor, order: torch.Tensor | None = None
+                 ) -> torch.Tensor:
+    """Engine::omni_combine[_ordered] (src/omni.rs:246-278, 535-556)."""
+    tokens = routes.shape[0]
+    topk = routes.shape[1] // 2
+    width = values.shape[1]
+    out = _empty((tokens, width), torch.bfloat16, values.device)
+    _check(lib().clef_moe_combine(_ptr(values), _ptr(routes), _ptr(order), tokens, width, topk, _ptr(out),
+                                  _stream()))
+    return out
+
+
+class MoeLayer:
+    """Omni INT4 MoE block (src/omni.rs:760-857) over resident packed experts.
+
+    The workspace is allocated once per (tokens) and reused by every call.
+    """
+
+    def __init__(self, gate: QuantizedWeight, up: QuantizedWeight, down: QuantizedWeight, topk: int = 8):
+        self.gate, self.up, self.down, self.topk = gate, up, down, topk
+        self.hidden = gate.cols
+        self.inter = gate.rows // 128
+        self._ws = None
+        self._ws_tokens = -1
+
+    def workspace(self, tokens: int, device) -> torch.Tensor:
+        if self._ws_tokens != tokens:
+            nbytes = int(lib().clef_moe_layer_workspace_bytes(tokens, self.hidden, self.inter, self.topk))
+            self._ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            self._ws_tokens = tokens
+        return self._ws
+
+    def __call__(self, x: torch.Tensor, logits: torch.Tensor, routes_out: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+        tokens = x.shape[0]
+        if out is None:
+            out = _empty((tokens, self.hidden), torch.bfloat16, x.device)
+        ws = self.workspace(tokens, x.device)
+        dtype = 0 if logits.dtype == torch.bfloat16 else 1
+        _check(lib().clef_moe_layer(_ptr(x), _ptr(logits), dtype, tokens, self.hidden, self.inter, 128,
+                                    self.topk, _ptr(self.gate.codes), _ptr(self.gate.scales),
+                                    _ptr(self.up.codes), _ptr(self.up.scales), _ptr(self.down.codes),
+                                    _ptr(self.down.scales), _ptr(routes_out), _ptr(out), _ptr(ws),
+                                    ws.numel(), _stream()))
+        return out

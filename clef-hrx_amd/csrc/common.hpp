@@ -1,0 +1,109 @@
+// Device helpers shared by the gfx950 kernels of the INT4 quantized-matmul and
+// Omni INT4 MoE path. Every helper states the IEEE steps it performs so the
+// arithmetic can be checked against the reference kernels line by line.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace clef {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float as_float(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t as_uint(float f) { return __float_as_uint(f); }
+
+// f32 -> bf16 round-to-nearest-even; a NaN stays a quiet NaN.
+// kernels/common.loom:29-35 (scalar.fptrunc f32 to bf16).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return as_float(h << 16); }
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return as_float(pair & 0xffff0000u); }
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// exp(x) by Cody-Waite reduction with ln 2 split as 0.693359375 - 2.12194440e-4
+// and the degree-5 minimax polynomial of the Cephes expf (S. L. Moshier, Cephes
+// Math Library). Every step is an explicit IEEE op (fma where written), so the
+// host restatement in the oracle produces the same bits. Stands in for the
+// reference's approximate expf<afn> (kernels/swiglu.loom:46,
+// kernels/omni_route.loom:131).
+__device__ __forceinline__ float cephes_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_huge_valf();
+  if (x < -103.972076416015625f) return 0.0f;
+  float n = __builtin_rintf(x * 1.44269504088896341f);
+  float r = __builtin_fmaf(n, -0.693359375f, x);
+  r = __builtin_fmaf(n, 2.12194440e-4f, r);
+  float r2 = r * r;
+  float p = 1.9875691500e-4f;
+  p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+  p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+  p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+  p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+  p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+  p = __builtin_fmaf(p, r2, r);
+  p = p + 1.0f;
+  return __builtin_ldexpf(p, (int)n);
+}
+
+// S1: h = bf16(f32(bf16(g / (1 + exp(-g)))) * u). kernels/swiglu.loom:43-51.
+__device__ __forceinline__ float swiglu1(float g, float u) {
+  float e = cephes_expf(-g);
+  float d = 1.0f + e;
+  float act = g / d;
+  return bf16_round(bf16_round(act) * u);
+}
+
+// One radix-4 stage of the reference rotation on a quad (a, b, c, d) taken at
+// stride s: s01=a+b, s23=c+d, d01=a-b, d23=c-d; a'=s01+d23, b'=s01-d23,
+// c'=d01+s23, d'=s23-d01. Separate f32 adds, no contraction.
+// kernels/prepare_integer_single.loom:109-116, src/quantized.rs:801-824.
+__device__ __forceinline__ void radix4(float& a, float& b, float& c, float& d) {
+  float s01 = a + b, s23 = c + d, d01 = a - b, d23 = c - d;
+  a = s01 + d23;
+  b = s01 - d23;
+  c = d01 + s23;
+  d = s23 - d01;
+}
+
+// Two consecutive stages on 16 values held by one lane: stride 1 over the low
+// base-4 digit of the index, then stride 4 over the next digit.
+__device__ __forceinline__ void radix4x2(float* v) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) radix4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) radix4(v[q], v[q + 4], v[q + 8], v[q + 12]);
+}
+
+// Eight int4 codes of one word (nibble p = code for k = 8q + p) -> two words of
+// int8 bytes holding 16 * code: `lo` carries the even nibbles, `hi` the odd
+// ones. Both GEMM operands use the same map, so their byte products are
+// 256 * code_a * code_b and the i32 sum is 256 times the code dot product.
+__device__ __forceinline__ void unpack16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  hi = w & 0xf0f0f0f0u;
+  lo = (w << 4) & 0xf0f0f0f0u;
+}
+
+__device__ __forceinline__ v4i unpack_pair(uint32_t w0, uint32_t w1) {
+  uint32_t a, b, c, d;
+  unpack16(w0, a, b);
+  unpack16(w1, c, d);
+  v4i r;
+  r.x = (int)a;
+  r.y = (int)b;
+  r.z = (int)c;
+  r.w = (int)d;
+  return r;
+}
+
+__device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+}  // namespace clef

@@ -1,0 +1,270 @@
+// G1 dense INT4 GEMM and E1 grouped expert INT4 GEMM for gfx950.
+//
+// G1 (kernels/gemm_integer.loom:394-433, identical in gemm_integer_m128.loom
+// and gemm_integer_wide_k.loom): acc = sum_k a[m][k] * w[n][k] exact in i32;
+// y = RN(RN(f32(acc) * ws[n]) * as[m]) + 0; finite y clamped to the bf16
+// finite range; out = bf16(y); residual variant out = bf16(f32(res) + f32(out)).
+//
+// E1 (kernels/omni_expert_i4.loom:113-125, 436-462): for expert e and slot i,
+// route = groups[e][1+i], xr = input_routed ? route : route / topk,
+// out[route][c] = bf16(RN(f32(acc) * RN(as[xr] * ws[e*n + c]))), no clamp.
+#include "gemm_core.hpp"
+#include "kernels.hpp"
+
+namespace clef {
+
+namespace {
+
+constexpr float kBf16Max = 3.3895313892515355e38f;
+
+__device__ __forceinline__ uint32_t g1_value(int32_t acc, float ws, float as) {
+  float y = (float)(acc >> 8) * ws;
+  y = y * as;
+  y = y + 0.0f;
+  float sat = __builtin_fmaxf(__builtin_fminf(y, kBf16Max), -kBf16Max);
+  float checked = __builtin_fabsf(y) < __builtin_huge_valf() ? sat : y;
+  return f32_to_bf16(checked);
+}
+
+__device__ __forceinline__ uint32_t add_residual(uint32_t out, uint32_t res) {
+  return f32_to_bf16(bf16_to_f32(res) + bf16_to_f32(out));
+}
+
+template <class T, bool RESID>
+__global__ __launch_bounds__(256) void gemm_i4_kernel(
+    const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
+    const uint32_t* __restrict__ w, const float* __restrict__ ws, int64_t M, int N, int kb,
+    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_n) {
+  extern __shared__ __align__(16) char lds[];
+  const int tid = threadIdx.x;
+  const int64_t bid = blockIdx.x;
+  const int tn = (int)(bid % tiles_n);
+  const int64_t m0 = (bid / tiles_n) * T::BM;
+  const int n0 = tn * T::BN;
+
+  const uint32_t* a_ptr[T::AL];
+  const uint32_t* b_ptr[T::BL];
+#pragma unroll
+  for (int j = 0; j < T::AL; ++j) {
+    const int idx = tid + 256 * j;
+    int64_t row = m0 + (idx >> 3);
+    row = row < M ? row : M - 1;
+    a_ptr[j] = a + row * a_words + (idx & 7) * 4;
+  }
+#pragma unroll
+  for (int j = 0; j < T::BL; ++j) {
+    const int idx = tid + 256 * j;
+    const int64_t nb = n0 / 128 + (idx >> 10);
+    b_ptr[j] = w + nb * kb * 4096 + (idx & 1023) * 4;
+  }
+  v4i acc[T::TM][T::TN];
+  gemm_mainloop<T>(a_ptr, b_ptr, kb, lds, acc);
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+  const int g = lane >> 4, lr = lane & 15;
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    const int64_t m = m0 + wm * T::WM + 16 * i + lr;
+    if (m >= M) continue;
+    const float asv = as[m];
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j) {
+      const int n = n0 + wn * T::WN + 16 * j + 4 * g;
+      const float4 wsv = *reinterpret_cast<const float4*>(ws + n);
+      uint32_t v0 = g1_value(acc[i][j].x, wsv.x, asv);
+      uint32_t v1 = g1_value(acc[i][j].y, wsv.y, asv);
+      uint32_t v2 = g1_value(acc[i][j].z, wsv.z, asv);
+      uint32_t v3 = g1_value(acc[i][j].w, wsv.w, asv);
+      uint2* dst = reinterpret_cast<uint2*>(out + m * N + n);
+      if (RESID) {
+        const uint2 r = *reinterpret_cast<const uint2*>(residual + m * N + n);
+        v0 = add_residual(v0, r.x & 0xffffu);
+        v1 = add_residual(v1, r.x >> 16);
+        v2 = add_residual(v2, r.y & 0xffffu);
+        v3 = add_residual(v3, r.y >> 16);
+      }
+      *dst = make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
+    }
+  }
+}
+
+template <class T, bool RESID>
+hipError_t launch_dense(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
+                        const float* ws, int64_t m, int n, int k, const uint16_t* residual,
+                        uint16_t* out, hipStream_t stream) {
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i4_kernel<T, RESID>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const int tiles_n = n / T::BN;
+  const int64_t tiles_m = (m + T::BM - 1) / T::BM;
+  const int64_t blocks = tiles_m * tiles_n;
+  gemm_i4_kernel<T, RESID><<<(unsigned)blocks, 256, T::LDS_BYTES, stream>>>(
+      a, a_words, as, w, ws, m, n, k / 256, residual, out, tiles_n);
+  return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_dense_any(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
+                            const float* ws, int64_t m, int n, int k, const uint16_t* residual,
+                            uint16_t* out, hipStream_t stream) {
+  if (residual) return launch_dense<T, true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return launch_dense<T, false>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+}
+
+using Tile128x128 = GemmTile<128, 128, 64, 64>;
+using Tile256x128 = GemmTile<256, 128, 128, 64>;
+using Tile128x256 = GemmTile<128, 256, 64, 128>;
+using Tile64x128 = GemmTile<64, 128, 32, 64>;
+
+// ---------------------------------------------------------------- experts
+
+constexpr int kExpertBM = 128;
+using ExpertTile = GemmTile<kExpertBM, 128, 64, 64>;
+
+// Per-expert tile list: schedule[0] = tiles, then (expert, first slot) pairs
+// for experts ascending and tiles of kExpertBM slots each. With bm = 16 and
+// float output the same walk is the reference task list R3
+// (kernels/omni_expert_tasks.loom:30-62).
+template <class OutT>
+__global__ __launch_bounds__(128) void tile_list_kernel(const float* __restrict__ groups,
+                                                        int64_t tokens, int bm, OutT* __restrict__ list) {
+  __shared__ int scan[128];
+  const int e = threadIdx.x;
+  const int count = (int)groups[(int64_t)e * (tokens + 1)];
+  const int tiles = (count + bm - 1) / bm;
+  scan[e] = tiles;
+  __syncthreads();
+  for (int off = 1; off < 128; off <<= 1) {
+    const int v = e >= off ? scan[e - off] : 0;
+    __syncthreads();
+    scan[e] += v;
+    __syncthreads();
+  }
+  const int start = scan[e] - tiles;
+  for (int t = 0; t < tiles; ++t) {
+    list[1 + 2 * (start + t)] = (OutT)e;
+    list[2 + 2 * (start + t)] = (OutT)(t * bm);
+  }
+  if (e == 127) list[0] = (OutT)scan[127];
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void expert_i4_kernel(
+    const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
+    const uint32_t* __restrict__ w, const float* __restrict__ ws, const float* __restrict__ groups,
+    const int32_t* __restrict__ schedule, int64_t tokens, int topk, int kb, int n, int input_routed,
+    uint16_t* __restrict__ out, int tiles_n) {
+  extern __shared__ __align__(16) char lds[];
+  const int tile = blockIdx.x / tiles_n;
+  if (tile >= schedule[0]) return;
+  const int tn = blockIdx.x - tile * tiles_n;
+  const int e = schedule[1 + 2 * tile];
+  const int row0 = schedule[2 + 2 * tile];
+  const float* list = groups + (int64_t)e * (tokens + 1);
+  const int count = (int)list[0];
+  const int n0 = tn * T::BN;
+  const int tid = threadIdx.x;
+
+  const uint32_t* a_ptr[T::AL];
+  const uint32_t* b_ptr[T::BL];
+#pragma unroll
+  for (int j = 0; j < T::AL; ++j) {
+    const int idx = tid + 256 * j;
+    int slot = row0 + (idx >> 3);
+    slot = slot < count ? slot : row0;
+    const int64_t route = (int64_t)list[1 + slot];
+    const int64_t xr = input_routed ? route : route / topk;
+    a_ptr[j] = a + xr * a_words + (idx & 7) * 4;
+  }
+#pragma unroll
+  for (int j = 0; j < T::BL; ++j) {
+    const int idx = tid + 256 * j;
+    const int64_t nb = ((int64_t)e * n + n0) / 128 + (idx >> 10);
+    b_ptr[j] = w + nb * kb * 4096 + (idx & 1023) * 4;
+  }
+  v4i acc[T::TM][T::TN];
+  gemm_mainloop<T>(a_ptr, b_ptr, kb, lds, acc);
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+  const int g = lane >> 4, lr = lane & 15;
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    const int slot = row0 + wm * T::WM + 16 * i + lr;
+    if (slot >= count) continue;
+    const int64_t route = (int64_t)list[1 + slot];
+    const int64_t xr = input_routed ? route : route / topk;
+    const float asv = as[xr];
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j) {
+      const int c = n0 + wn * T::WN + 16 * j + 4 * g;
+      const float4 wsv = *reinterpret_cast<const float4*>(ws + (int64_t)e * n + c);
+      const uint32_t v0 = f32_to_bf16((float)(acc[i][j].x >> 8) * (asv * wsv.x));
+      const uint32_t v1 = f32_to_bf16((float)(acc[i][j].y >> 8) * (asv * wsv.y));
+      const uint32_t v2 = f32_to_bf16((float)(acc[i][j].z >> 8) * (asv * wsv.z));
+      const uint32_t v3 = f32_to_bf16((float)(acc[i][j].w >> 8) * (asv * wsv.w));
+      *reinterpret_cast<uint2*>(out + route * n + c) = make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
+    }
+  }
+}
+
+}  // namespace
+
+int gemm_config_count() { return 4; }
+
+hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
+                          const float* ws, int64_t m, int n, int k, const uint16_t* residual,
+                          uint16_t* out, int config, hipStream_t stream) {
+  if (config < 0) config = (n % 256 == 0 && m >= 2048) ? 2 : (m >= 256 ? 1 : 0);
+  if (config == 2 && n % 256 != 0) config = 1;
+  switch (config) {
+    case 0: return launch_dense_any<Tile128x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 1: return launch_dense_any<Tile256x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 2: return launch_dense_any<Tile128x256>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 3: return launch_dense_any<Tile64x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+int64_t expert_max_tiles(int64_t routes) { return (routes + kExpertBM - 1) / kExpertBM + 128; }
+
+size_t expert_schedule_bytes(int64_t routes) {
+  return (size_t)(1 + 2 * expert_max_tiles(routes)) * sizeof(int32_t);
+}
+
+hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int32_t* schedule,
+                                  hipStream_t stream) {
+  tile_list_kernel<int32_t><<<1, 128, 0, stream>>>(groups, tokens, kExpertBM, schedule);
+  return hipGetLastError();
+}
+
+hipError_t launch_expert_tasks(const float* groups, int64_t tokens, float* tasks, hipStream_t stream) {
+  tile_list_kernel<float><<<1, 128, 0, stream>>>(groups, tokens, 16, tasks);
+  return hipGetLastError();
+}
+
+hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
+                            const float* ws, const float* groups, const int32_t* schedule,
+                            int64_t tokens, int topk, int k, int n, int input_routed, uint16_t* out,
+                            hipStream_t stream) {
+  using T = ExpertTile;
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&expert_i4_kernel<T>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const int tiles_n = n / T::BN;
+  const int64_t blocks = expert_max_tiles(tokens * topk) * tiles_n;
+  expert_i4_kernel<T><<<(unsigned)blocks, 256, T::LDS_BYTES, stream>>>(
+      a, a_words, as, w, ws, groups, schedule, tokens, topk, k / 256, n, input_routed, out, tiles_n);
+  return hipGetLastError();
+}
+
+}  // namespace clef

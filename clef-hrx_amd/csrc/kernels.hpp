@@ -1,0 +1,49 @@
+// Launchers of the gfx950 kernels (internal to the library; the public
+// boundary is include/clef_i4.h). Each returns the launch's hipError_t and
+// assumes the caller already checked every shape and alignment precondition.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace clef {
+
+hipError_t launch_prepare(const uint16_t* x, int64_t rows, int width, int stride, int bits,
+                          uint32_t* out, hipStream_t stream);
+hipError_t launch_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t rows, int width,
+                                 int stride, int bits, uint32_t* out, hipStream_t stream);
+hipError_t launch_retile(const uint32_t* codes, int64_t rows, int in_words, int words,
+                         uint32_t* tiled, hipStream_t stream);
+hipError_t launch_tile_permute(const uint16_t* src, int64_t rows, int cols, uint16_t* dst,
+                               bool to_tiled, hipStream_t stream);
+
+hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* a_scales,
+                          const uint32_t* w_tiled, const float* w_scales, int64_t m, int n, int k,
+                          const uint16_t* residual, uint16_t* out, int config, hipStream_t stream);
+int gemm_config_count();
+
+hipError_t launch_route(const void* logits, int dtype, int64_t tokens, int experts, int topk,
+                        float* routes, hipStream_t stream);
+size_t group_workspace_bytes(int64_t tokens);
+hipError_t launch_group_routes(const float* routes, int64_t tokens, int topk, float* groups,
+                               float* order, void* workspace, hipStream_t stream);
+hipError_t launch_expert_tasks(const float* groups, int64_t tokens, float* tasks,
+                               hipStream_t stream);
+
+// Tile schedule of the grouped expert GEMM: int32 [1 + 2 * max_tiles].
+int64_t expert_max_tiles(int64_t routes);
+size_t expert_schedule_bytes(int64_t routes);
+hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int32_t* schedule,
+                                  hipStream_t stream);
+hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* a_scales,
+                            const uint32_t* w_tiled, const float* w_scales, const float* groups,
+                            const int32_t* schedule, int64_t tokens, int topk, int k, int n,
+                            int input_routed, uint16_t* out, hipStream_t stream);
+
+hipError_t launch_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h,
+                         hipStream_t stream);
+hipError_t launch_combine(const uint16_t* values, const float* routes, const float* order,
+                          int64_t tokens, int width, int topk, uint16_t* out, hipStream_t stream);
+
+}  // namespace clef

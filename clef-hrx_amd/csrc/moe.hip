@@ -1,0 +1,303 @@
+// Omni MoE routing, grouping, SwiGLU and combine for gfx950.
+//
+// R1 router (kernels/omni_route.loom:84-146): per token, topk rounds of
+// "largest remaining logit, ties -> lowest expert id", the selected slot reset
+// to -FLT_MAX; routes[t][r] = f32(id), then p_j = exp(v_j - v_0) summed in
+// rank order and routes[t][topk+j] = f32(bf16(p_j / sum)).
+// R2 grouping (kernels/omni_group_routes.loom:43-82 and the ordered variant
+// kernels/omni_group_routes_ordered.loom:50-87): groups[e][0] = count,
+// groups[e][1+i] = f32(t*topk + r) for the i-th token (ascending) routed to e
+// at rank r; order[t][#(ids < e)] = r.
+// S1 (kernels/swiglu.loom:43-51) and C1 (kernels/omni_combine_ordered.loom:51-79,
+// kernels/omni_combine.loom:50-77).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace clef {
+
+namespace {
+
+constexpr float kNegMax = -3.402823466e38f;
+constexpr int kInvalidId = 2147483647;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ int wave_min(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const int o = __shfl_xor(v, off, 64);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
+// One wave per token; lane l holds expert slots 2l and 2l+1 (E <= 128).
+__global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ logits, int dtype,
+                                                    int64_t tokens, int experts, int topk,
+                                                    float* __restrict__ routes) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= tokens) return;
+  float v[2];
+  bool valid[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int e = 2 * lane + s;
+    valid[s] = e < experts;
+    if (!valid[s]) {
+      v[s] = kNegMax;
+    } else if (dtype == 0) {
+      v[s] = bf16_to_f32(static_cast<const uint16_t*>(logits)[t * experts + e]);
+    } else {
+      v[s] = static_cast<const float*>(logits)[t * experts + e];
+    }
+  }
+  float* out = routes + t * 2 * topk;
+  for (int r = 0; r < topk; ++r) {
+    const float best = wave_max(__builtin_fmaxf(v[0], v[1]));
+    int cand = kInvalidId;
+    if (valid[1] && v[1] == best) cand = 2 * lane + 1;
+    if (valid[0] && v[0] == best) cand = 2 * lane;
+    const int id = wave_min(cand);
+    if (lane == 0) {
+      out[r] = (float)id;
+      out[topk + r] = best;
+    }
+    if (id == 2 * lane) v[0] = kNegMax;
+    if (id == 2 * lane + 1) v[1] = kNegMax;
+  }
+  if (lane == 0) {
+    const float vmax = out[topk];
+    float sum = 0.0f;
+    for (int j = 0; j < topk; ++j) {
+      const float p = cephes_expf(out[topk + j] - vmax);
+      out[topk + j] = p;
+      sum = sum + p;
+    }
+    for (int j = 0; j < topk; ++j) out[topk + j] = bf16_round(out[topk + j] / sum);
+  }
+}
+
+// ---------------------------------------------------------------- grouping
+//
+// Three passes over blocks of 256 tokens (one token per thread):
+//   count:   per-wave 64-bit lane masks per expert (LDS atomic OR), block
+//            counts per expert -> workspace [blocks][128]
+//   scan:    per expert, exclusive prefix over blocks; counts -> groups[e][0]
+//   scatter: rank of (t, r) within expert e = block prefix + earlier waves'
+//            counts + popcount of the wave mask below this lane
+// Every position is computed, not claimed, so the lists are in ascending
+// token order exactly.
+
+constexpr int kGroupBlock = 256;
+
+// Expert id of route slot r, or -1 when the slot names no expert in 0..127
+// (the oracle compares (int32_t)id against each expert).
+__device__ __forceinline__ int route_expert(float id) {
+  return (id > -1.0f && id < 128.0f) ? (int)id : -1;
+}
+
+// True when slot r is the last slot of this token naming its expert.
+__device__ __forceinline__ bool last_slot(const float* rt, int topk, int r, int e) {
+  for (int q = r + 1; q < topk; ++q)
+    if (route_expert(rt[q]) == e) return false;
+  return true;
+}
+
+__device__ void build_masks(const float* __restrict__ routes, int64_t tokens, int topk,
+                            unsigned long long (*masks)[128], int* wave_counts /* [4][128] */) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < 4 * 128; i += 256) (&masks[0][0])[i] = 0ull;
+  __syncthreads();
+  const int64_t t = (int64_t)blockIdx.x * kGroupBlock + tid;
+  if (t < tokens) {
+    const float* rt = routes + t * 2 * topk;
+    for (int r = 0; r < topk; ++r) {
+      const int e = route_expert(rt[r]);
+      if (e >= 0) atomicOr(&masks[wave][e], 1ull << lane);
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < 4 * 128; i += 256) wave_counts[i] = __popcll((&masks[0][0])[i]);
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void group_count_kernel(const float* __restrict__ routes,
+                                                          int64_t tokens, int topk,
+                                                          int* __restrict__ block_counts) {
+  __shared__ unsigned long long masks[4][128];
+  __shared__ int wave_counts[4 * 128];
+  build_masks(routes, tokens, topk, masks, wave_counts);
+  const int e = threadIdx.x;
+  if (e < 128) {
+    block_counts[(int64_t)blockIdx.x * 128 + e] =
+        wave_counts[e] + wave_counts[128 + e] + wave_counts[256 + e] + wave_counts[384 + e];
+  }
+}
+
+// One workgroup of 1024 threads: 8 threads per expert, each summing a
+// contiguous run of blocks, then an 8-way scan.
+__global__ __launch_bounds__(1024) void group_scan_kernel(int* __restrict__ block_counts, int64_t blocks,
+                                                          int64_t tokens, float* __restrict__ groups) {
+  __shared__ int part[8][128];
+  const int e = threadIdx.x & 127, j = threadIdx.x >> 7;
+  const int64_t per = (blocks + 7) / 8;
+  const int64_t b0 = j * per, b1 = b0 + per < blocks ? b0 + per : blocks;
+  int sum = 0;
+  for (int64_t b = b0; b < b1; ++b) sum += block_counts[b * 128 + e];
+  part[j][e] = sum;
+  __syncthreads();
+  int run = 0;
+  for (int q = 0; q < j; ++q) run += part[q][e];
+  for (int64_t b = b0; b < b1; ++b) {
+    const int c = block_counts[b * 128 + e];
+    block_counts[b * 128 + e] = run;
+    run += c;
+  }
+  if (j == 7) groups[(int64_t)e * (tokens + 1)] = (float)run;
+}
+
+__global__ __launch_bounds__(256) void group_scatter_kernel(const float* __restrict__ routes,
+                                                            int64_t tokens, int topk,
+                                                            const int* __restrict__ block_offsets,
+                                                            float* __restrict__ groups,
+                                                            float* __restrict__ order) {
+  __shared__ unsigned long long masks[4][128];
+  __shared__ int wave_counts[4 * 128];
+  build_masks(routes, tokens, topk, masks, wave_counts);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t = (int64_t)blockIdx.x * kGroupBlock + tid;
+  if (t >= tokens) return;
+  const float* rt = routes + t * 2 * topk;
+  const unsigned long long below = (1ull << lane) - 1ull;
+  for (int r = 0; r < topk; ++r) {
+    const int e = route_expert(rt[r]);
+    if (e < 0 || !last_slot(rt, topk, r, e)) continue;
+    int rank = block_offsets[(int64_t)blockIdx.x * 128 + e];
+    for (int w = 0; w < wave; ++w) rank += wave_counts[w * 128 + e];
+    rank += __popcll(masks[wave][e] & below);
+    groups[(int64_t)e * (tokens + 1) + 1 + rank] = (float)(t * topk + r);
+    if (order) {
+      int less = 0;
+      for (int q = 0; q < topk; ++q) less += rt[q] < (float)e ? 1 : 0;
+      order[t * topk + less] = (float)r;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- S1, C1
+
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict__ gate,
+                                                     const uint16_t* __restrict__ up, int64_t n,
+                                                     uint16_t* __restrict__ h) {
+  const int64_t i8 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i8 + 8 <= n) {
+    const uint4 g = *reinterpret_cast<const uint4*>(gate + i8);
+    const uint4 u = *reinterpret_cast<const uint4*>(up + i8);
+    const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+    uint32_t hw[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = f32_to_bf16(swiglu1(bf16_lo(gw[q]), bf16_lo(uw[q])));
+      const uint32_t hi = f32_to_bf16(swiglu1(bf16_hi(gw[q]), bf16_hi(uw[q])));
+      hw[q] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4*>(h + i8) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+  } else {
+    for (int64_t i = i8; i < n; ++i)
+      h[i] = (uint16_t)f32_to_bf16(swiglu1(bf16_to_f32(gate[i]), bf16_to_f32(up[i])));
+  }
+}
+
+// One thread per (token, 8 columns).
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ values,
+                                                      const float* __restrict__ routes,
+                                                      const float* __restrict__ order, int64_t tokens,
+                                                      int width, int topk, uint16_t* __restrict__ out) {
+  const int chunks = width / 8;
+  const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (id >= tokens * chunks) return;
+  const int64_t t = id / chunks;
+  const int c = (int)(id - t * chunks) * 8;
+  const float* rt = routes + t * 2 * topk;
+  float acc[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+  float prev = -1.0f;
+  for (int j = 0; j < topk; ++j) {
+    int rank;
+    if (order) {
+      rank = (int)order[t * topk + j];
+    } else {
+      // j-th smallest expert id (kernels/omni_combine.loom:50-77).
+      float best = 1000000.0f;
+      rank = 0;
+      for (int r = 0; r < topk; ++r)
+        if (rt[r] > prev && rt[r] < best) {
+          best = rt[r];
+          rank = r;
+        }
+      prev = best;
+    }
+    const float p = rt[topk + rank];
+    const uint4 v = *reinterpret_cast<const uint4*>(values + ((t * topk + rank) * width + c));
+    const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      acc[2 * q] = bf16_round(acc[2 * q] + bf16_round(bf16_lo(vw[q]) * p));
+      acc[2 * q + 1] = bf16_round(acc[2 * q + 1] + bf16_round(bf16_hi(vw[q]) * p));
+    }
+  }
+  uint32_t ow[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) ow[q] = f32_to_bf16(acc[2 * q]) | (f32_to_bf16(acc[2 * q + 1]) << 16);
+  *reinterpret_cast<uint4*>(out + t * width + c) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+}
+
+}  // namespace
+
+hipError_t launch_route(const void* logits, int dtype, int64_t tokens, int experts, int topk,
+                        float* routes, hipStream_t stream) {
+  const int64_t blocks = (tokens + 3) / 4;
+  route_kernel<<<(unsigned)blocks, 256, 0, stream>>>(logits, dtype, tokens, experts, topk, routes);
+  return hipGetLastError();
+}
+
+size_t group_workspace_bytes(int64_t tokens) {
+  const int64_t blocks = (tokens + kGroupBlock - 1) / kGroupBlock;
+  return (size_t)blocks * 128 * sizeof(int);
+}
+
+hipError_t launch_group_routes(const float* routes, int64_t tokens, int topk, float* groups,
+                               float* order, void* workspace, hipStream_t stream) {
+  const int64_t blocks = (tokens + kGroupBlock - 1) / kGroupBlock;
+  int* counts = static_cast<int*>(workspace);
+  group_count_kernel<<<(unsigned)blocks, 256, 0, stream>>>(routes, tokens, topk, counts);
+  group_scan_kernel<<<1, 1024, 0, stream>>>(counts, blocks, tokens, groups);
+  group_scatter_kernel<<<(unsigned)blocks, 256, 0, stream>>>(routes, tokens, topk, counts, groups, order);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h,
+                         hipStream_t stream) {
+  const int64_t threads = (n + 7) / 8;
+  const int64_t blocks = (threads + 255) / 256;
+  if (blocks == 0) return hipSuccess;
+  swiglu_kernel<<<(unsigned)blocks, 256, 0, stream>>>(gate, up, n, h);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(const uint16_t* values, const float* routes, const float* order,
+                          int64_t tokens, int width, int topk, uint16_t* out, hipStream_t stream) {
+  const int64_t threads = tokens * (width / 8);
+  const int64_t blocks = (threads + 255) / 256;
+  if (blocks == 0) return hipSuccess;
+  combine_kernel<<<(unsigned)blocks, 256, 0, stream>>>(values, routes, order, tokens, width, topk, out);
+  return hipGetLastError();
+}
+
+}  // namespace clef

@@ -1,0 +1,317 @@
+// Q1: Hadamard-rotated per-row quantizer, and Q2's retile permutation.
+//
+// Q1 follows kernels/prepare_integer_single.loom:65-286 (and the CPU test
+// oracle at src/quantized.rs:801-824, 990-1004): per 256-column group a
+// four-stage radix-4 rotation (strides 1, 4, 16, 64, exact op order), the row
+// maximum of |v| with NaN counted as +inf, scale = (max(m/16, 1e-30)) / qmax,
+// inv = (1/16) / scale, codes = clamp(roundeven(v * inv), -qmax, qmax), all
+// codes 0 when the scale is not finite. Storage is the reference's single
+// buffer: codes [rows][stride/(32/bits)] followed by rows f32 scales
+// (src/quantized.rs:656-664).
+//
+// gfx950 mapping: 16 lanes own one 256-column group, 16 consecutive values per
+// lane (one 32-byte load). Stages 1-2 run in-lane; a transpose through LDS
+// gives each lane the 16 values that differ in the two high base-4 digits, and
+// stages 3-4 run in-lane again. After the row maximum, a second LDS transpose
+// returns natural order so each lane packs two (int4) or four (int8) whole
+// words. A 256-thread workgroup holds 16 groups: 16/G rows of G groups when
+// the row has G <= 16 groups, else one row over P passes kept in registers.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace clef {
+
+namespace {
+
+constexpr int kPitch = 20;            // floats per 16-value LDS row (80 bytes)
+constexpr int kGroupLds = 16 * kPitch; // LDS floats per 256-column group
+
+struct PlainSource {
+  const uint16_t* x;
+  __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
+    const u4* p = reinterpret_cast<const u4*>(x + row * width + col);
+    u4 a = p[0], b = p[1];
+    uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[2 * i] = bf16_lo(w[i]);
+      v[2 * i + 1] = bf16_hi(w[i]);
+    }
+  }
+};
+
+// S1 applied on load (kernels/prepare_integer_register.loom:155-172): the
+// rotation sees f32(bf16(swiglu)) exactly as if h had been materialized.
+struct SwigluSource {
+  const uint16_t* gate;
+  const uint16_t* up;
+  __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
+    const u4* pg = reinterpret_cast<const u4*>(gate + row * width + col);
+    const u4* pu = reinterpret_cast<const u4*>(up + row * width + col);
+    u4 ga = pg[0], gb = pg[1], ua = pu[0], ub = pu[1];
+    uint32_t g[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+    uint32_t u[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[2 * i] = swiglu1(bf16_lo(g[i]), bf16_lo(u[i]));
+      v[2 * i + 1] = swiglu1(bf16_hi(g[i]), bf16_hi(u[i]));
+    }
+  }
+};
+
+__device__ __forceinline__ uint32_t group_max16(uint32_t m) {
+  // Reduce over the 16 lanes of a group (lanes differ in the low 4 bits).
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) {
+    uint32_t o = (uint32_t)__shfl_xor((int)m, off, 64);
+    m = m > o ? m : o;
+  }
+  return m;
+}
+
+template <int BITS>
+__device__ __forceinline__ uint32_t pack_codes(const float* v, float inv, bool valid) {
+  constexpr int per = 32 / BITS;
+  constexpr float qmax = BITS == 8 ? 127.0f : 7.0f;
+  constexpr uint32_t mask = BITS == 8 ? 0xffu : 0xfu;
+  uint32_t word = 0;
+#pragma unroll
+  for (int p = 0; p < per; ++p) {
+    float scaled = v[p] * inv;
+    float s = valid ? scaled : 0.0f;
+    float r = __builtin_rintf(s);
+    float lo = __builtin_fmaxf(r, -qmax);
+    float hi = __builtin_fminf(lo, qmax);
+    int code = (int)hi;
+    word |= ((uint32_t)code & mask) << (p * BITS);
+  }
+  return word;
+}
+
+template <int P, int BITS, class Src>
+__global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int width,
+                                                      int out_words, uint32_t* __restrict__ out) {
+  __shared__ __align__(16) float lds[16 * kGroupLds];
+  __shared__ uint32_t gmax[16];
+  const int tid = threadIdx.x;
+  const int lg = tid >> 4;
+  const int L = tid & 15;
+  const int G = width >> 8;
+  int rows_per_block, row_local, grp0;
+  if (P == 1) {
+    rows_per_block = 16 / G;
+    row_local = lg / G;
+    grp0 = lg - row_local * G;
+  } else {
+    rows_per_block = 1;
+    row_local = 0;
+    grp0 = lg;
+  }
+  const int64_t row = (int64_t)blockIdx.x * rows_per_block + row_local;
+  const bool active = row_local < rows_per_block && row < rows;
+  float* buf = lds + lg * kGroupLds;
+
+  float v[P][16];
+  uint32_t mbits = 0;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int grp = grp0 + 16 * p;
+    const bool on = active && grp < G;
+    if (on) {
+      src.load16(row, width, grp * 256 + 16 * L, v[p]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[p][i] = 0.0f;
+    }
+    radix4x2(v[p]);  // strides 1 and 4
+    float4* wrow = reinterpret_cast<float4*>(buf + L * kPitch);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      wrow[c] = make_float4(v[p][4 * c], v[p][4 * c + 1], v[p][4 * c + 2], v[p][4 * c + 3]);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[p][k] = buf[k * kPitch + L];
+    __syncthreads();
+    radix4x2(v[p]);  // strides 16 and 64 (value k holds index L + 16k)
+    if (on) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        uint32_t a = as_uint(v[p][k]) & 0x7fffffffu;
+        mbits = mbits > a ? mbits : a;
+      }
+    }
+  }
+  mbits = group_max16(mbits);
+  if (L == 0) gmax[lg] = mbits;
+  __syncthreads();
+  uint32_t m = 0;
+  if (P == 1) {
+    for (int g = 0; g < G; ++g) {
+      uint32_t o = gmax[(row_local < rows_per_block ? row_local : 0) * G + g];
+      m = m > o ? m : o;
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < 16; ++g) m = m > gmax[g] ? m : gmax[g];
+  }
+  // |v| < inf ? |v| : inf with NaN -> inf: any pattern >= +inf's is +inf.
+  const float mf = m >= 0x7f800000u ? __builtin_huge_valf() : as_float(m);
+  constexpr float qmax = BITS == 8 ? 127.0f : 7.0f;
+  const float normal = mf * 0.0625f;
+  const float safe = __builtin_fmaxf(normal, 1e-30f);
+  const float scale = safe / qmax;
+  const bool valid = scale < __builtin_huge_valf();
+  const float inv = 0.0625f / scale;
+
+  constexpr int per = 32 / BITS;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int grp = grp0 + 16 * p;
+    const bool on = active && grp < G;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) buf[k * kPitch + L] = v[p][k];
+    __syncthreads();
+    float nat[16];
+    const float4* rrow = reinterpret_cast<const float4*>(buf + L * kPitch);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float4 t = rrow[c];
+      nat[4 * c] = t.x;
+      nat[4 * c + 1] = t.y;
+      nat[4 * c + 2] = t.z;
+      nat[4 * c + 3] = t.w;
+    }
+    __syncthreads();
+    if (on) {
+      uint32_t* dst = out + row * out_words + (grp * 256 + 16 * L) / per;
+      if (BITS == 4) {
+        uint2 w = make_uint2(pack_codes<4>(nat, inv, valid), pack_codes<4>(nat + 8, inv, valid));
+        *reinterpret_cast<uint2*>(dst) = w;
+      } else {
+        uint4 w = make_uint4(pack_codes<8>(nat, inv, valid), pack_codes<8>(nat + 4, inv, valid),
+                             pack_codes<8>(nat + 8, inv, valid), pack_codes<8>(nat + 12, inv, valid));
+        *reinterpret_cast<uint4*>(dst) = w;
+      }
+    }
+  }
+  if (active && grp0 == 0 && L == 0) {
+    float* scales = reinterpret_cast<float*>(out + rows * out_words);
+    scales[row] = scale;
+  }
+}
+
+template <int BITS, class Src>
+hipError_t launch_prepare_bits(const Src& src, int64_t rows, int width, int out_words,
+                               uint32_t* out, hipStream_t stream) {
+  const int G = width / 256;
+  if (G <= 16) {
+    const int per_block = 16 / G;
+    const unsigned grid = (unsigned)((rows + per_block - 1) / per_block);
+    prepare_kernel<1, BITS, Src><<<grid, 256, 0, stream>>>(src, rows, width, out_words, out);
+  } else {
+    const int passes = (G + 15) / 16;
+    const unsigned grid = (unsigned)rows;
+    switch (passes) {
+#define CLEF_PREP_CASE(N) \
+  case N: prepare_kernel<N, BITS, Src><<<grid, 256, 0, stream>>>(src, rows, width, out_words, out); break;
+      CLEF_PREP_CASE(2)
+      CLEF_PREP_CASE(3)
+      CLEF_PREP_CASE(4)
+      CLEF_PREP_CASE(5)
+      CLEF_PREP_CASE(6)
+      CLEF_PREP_CASE(7)
+      CLEF_PREP_CASE(8)
+#undef CLEF_PREP_CASE
+      default: return hipErrorInvalidValue;
+    }
+  }
+  return hipGetLastError();
+}
+
+template <class Src>
+hipError_t launch_prepare_src(const Src& src, int64_t rows, int width, int stride, int bits,
+                              uint32_t* out, hipStream_t stream) {
+  const int out_words = stride / (32 / bits);
+  if (bits == 4) return launch_prepare_bits<4>(src, rows, width, out_words, out, stream);
+  return launch_prepare_bits<8>(src, rows, width, out_words, out, stream);
+}
+
+// Q2 retile: word (n, q) of the row-major codes lands at
+// ((n / 128) * blocks_k + q / 32) * 4096 + (n % 128) * 32 + q % 32.
+// kernels/retile_codes.loom:2-5, 38-55. One thread moves 16 bytes; a
+// workgroup writes one contiguous 16 KiB output block.
+__global__ __launch_bounds__(256) void retile_kernel(const uint32_t* __restrict__ codes, int64_t rows,
+                                                     int in_words, int blocks_k,
+                                                     uint32_t* __restrict__ tiled) {
+  const int64_t block = blockIdx.x;  // (n / 128) * blocks_k + q / 32
+  const int64_t nb = block / blocks_k;
+  const int kb = (int)(block - nb * blocks_k);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = threadIdx.x + 256 * j;  // 16-byte chunk within the block
+    const int r = idx >> 3, c = idx & 7;
+    const int64_t n = nb * 128 + r;
+    const uint32_t* src = codes + n * in_words + kb * 32 + c * 4;
+    uint4 w;
+    if ((in_words & 3) == 0) {
+      w = *reinterpret_cast<const uint4*>(src);
+    } else {
+      w = make_uint4(src[0], src[1], src[2], src[3]);
+    }
+    *reinterpret_cast<uint4*>(tiled + block * 4096 + idx * 4) = w;
+  }
+}
+
+// Checkpoint tiling [rows/256][cols/64][256][64] <-> row-major [rows][cols]
+// (src/checkpoint.rs:24-32, 63-106). Threads walk the tiled order in 16-byte
+// chunks (8 bf16): element (tile, ks, r, c) is dense (tile*256 + r)*cols +
+// ks*64 + c and tiled tile*256*cols + (ks*256 + r)*64 + c.
+__global__ __launch_bounds__(256) void tile_permute_kernel(const uint16_t* __restrict__ src,
+                                                           int64_t chunks, int cols, bool to_tiled,
+                                                           uint16_t* __restrict__ dst) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= chunks) return;
+  const int c = (int)(q & 7) * 8;
+  const int64_t rest = q >> 3;
+  const int r = (int)(rest & 255);
+  const int64_t rest2 = rest >> 8;
+  const int ksteps = cols / 64;
+  const int64_t tile = rest2 / ksteps;
+  const int ks = (int)(rest2 - tile * ksteps);
+  const int64_t dense = (tile * 256 + r) * cols + ks * 64 + c;
+  const int64_t tiled = q * 8;
+  if (to_tiled)
+    *reinterpret_cast<uint4*>(dst + tiled) = *reinterpret_cast<const uint4*>(src + dense);
+  else
+    *reinterpret_cast<uint4*>(dst + dense) = *reinterpret_cast<const uint4*>(src + tiled);
+}
+
+}  // namespace
+
+hipError_t launch_prepare(const uint16_t* x, int64_t rows, int width, int stride, int bits,
+                          uint32_t* out, hipStream_t stream) {
+  return launch_prepare_src(PlainSource{x}, rows, width, stride, bits, out, stream);
+}
+
+hipError_t launch_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t rows, int width,
+                                 int stride, int bits, uint32_t* out, hipStream_t stream) {
+  return launch_prepare_src(SwigluSource{gate, up}, rows, width, stride, bits, out, stream);
+}
+
+hipError_t launch_retile(const uint32_t* codes, int64_t rows, int in_words, int words,
+                         uint32_t* tiled, hipStream_t stream) {
+  const int blocks_k = words / 32;
+  const int64_t blocks = (rows / 128) * blocks_k;
+  retile_kernel<<<(unsigned)blocks, 256, 0, stream>>>(codes, rows, in_words, blocks_k, tiled);
+  return hipGetLastError();
+}
+
+hipError_t launch_tile_permute(const uint16_t* src, int64_t rows, int cols, uint16_t* dst,
+                               bool to_tiled, hipStream_t stream) {
+  const int64_t chunks = rows * cols / 8;
+  const int64_t blocks = (chunks + 255) / 256;
+  tile_permute_kernel<<<(unsigned)blocks, 256, 0, stream>>>(src, chunks, cols, to_tiled, dst);
+  return hipGetLastError();
+}
+
+}  // namespace clef

@@ -1,0 +1,239 @@
+/*
+ * clef_i4.h - C ABI of the MI355X (gfx950) INT4 quantized-matmul and Omni INT4
+ * MoE hot path.
+ *
+ * Drop-in boundary for the reference's crate-internal operator API. Each
+ * entry point names the reference function it replaces (paths relative to the
+ * reference repository). Memory layouts are the reference's, byte for byte:
+ *
+ *   bf16 tensors          uint16_t bit patterns, row-major
+ *   packed activation     uint32_t [rows][stride/(32/bits)] codes (8 int4 or
+ *                         4 int8 per word, low bits first), then rows f32
+ *                         scales (src/quantized.rs:656-664)
+ *   tiled weight codes    128-row x 32-word blocks:
+ *                         word (n, q) -> ((n/128)*(K/256) + q/32)*4096
+ *                                        + (n%128)*32 + q%32
+ *                         (kernels/retile_codes.loom:2-5)
+ *   routes                float [T][2*topk]: expert ids, then probabilities
+ *   groups                float [128][T+1]: count, then route ordinals t*topk+r
+ *   order                 float [T][topk]: rank of the j-th smallest expert id
+ *   tasks                 float [1 + 2*(ceil(T*topk/16) + 127)]
+ *
+ * Conventions:
+ *   - Every pointer argument is a device pointer owned by the caller, 16-byte
+ *     aligned. Outputs are written, never allocated. No entry point allocates
+ *     device memory; scratch comes from the caller's workspace (size query
+ *     functions below).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default
+ *     stream) and is asynchronous. Calls on distinct streams are independent.
+ *   - Return 0 on success; CLEF_EINVAL (-1) when a precondition fails, with
+ *     the reference's message (or a message of this library where the
+ *     reference has no check) from clef_last_error(); a positive value is the
+ *     hipError_t of a failed launch.
+ *   - clef_last_error() is per calling thread.
+ */
+#ifndef CLEF_I4_H
+#define CLEF_I4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* clef_stream_t;
+
+#define CLEF_OK 0
+#define CLEF_EINVAL (-1)
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* clef_last_error(void);
+
+/* ABI version of this header (major * 100 + minor). */
+int clef_abi_version(void);
+
+/* ------------------------------------------------------------------ Q1/Q2 */
+
+/* Activation/weight stride rule: width + (width % 1024 == 0 ? 512/bits : 0).
+ * Replaces the stride computation at src/quantized.rs:161-166. */
+int32_t clef_i4_activation_stride(int32_t width, int32_t bits);
+
+/* Words of one packed buffer: rows * (stride/(32/bits) + 1). */
+int64_t clef_i4_prepared_words(int64_t rows, int32_t stride, int32_t bits);
+
+/* Hadamard-rotated per-row quantizer (bits 4 or 8) into the packed layout.
+ * Padding words [width/(32/bits), stride/(32/bits)) of each row are not
+ * written. Replaces quantized::prepare / prepare_inputs
+ * (src/quantized.rs:574-686) and the h3_prepare_plain_tiled_i4/_i8 kernels
+ * (kernels/prepare_integer_single.loom, prepare_integer.loom,
+ * prepare_integer_register.loom:317-352).
+ * Preconditions (src/quantized.rs:640-649): bits in {4,8}, 256 <= width <=
+ * 32768, width % 256 == 0, 1 <= rows <= 1048576, width <= stride <= 65536,
+ * stride % (512/bits) == 0 -> else "unsupported rotated integer operand". */
+int clef_i4_prepare(const uint16_t* x, int64_t rows, int32_t width, int32_t stride, int32_t bits,
+                    uint32_t* out, clef_stream_t stream);
+
+/* SwiGLU fused into the quantizer: quantizes bf16(swiglu(gate, up)) with the
+ * rounding of a materialized SwiGLU. Replaces prepare_with_inputs([gate, up])
+ * / h3_prepare_swiglu_i4 (src/quantized.rs:406-439, 605-613;
+ * kernels/prepare_integer_register.loom:155-172, 353-368). Same
+ * preconditions as clef_i4_prepare. */
+int clef_i4_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t rows, int32_t width,
+                           int32_t stride, int32_t bits, uint32_t* out, clef_stream_t stream);
+
+/* Row-major packed codes [rows][in_words] -> tiled blocks, dropping padding.
+ * Replaces quantized::retile_codes (src/quantized.rs:542-572) and
+ * kernels/retile_codes.loom. Preconditions: rows % 128 == 0, words =
+ * cols/(32/bits) with words % 32 == 0, in_words >= words -> else
+ * "unsupported packed weight shape for tiling". */
+int clef_i4_retile(const uint32_t* codes, int64_t rows, int32_t in_words, int32_t cols, int32_t bits,
+                   uint32_t* tiled, clef_stream_t stream);
+
+/* Bytes of scratch clef_i4_pack_weight needs (the row-major packed staging). */
+size_t clef_i4_pack_weight_workspace_bytes(int64_t rows, int32_t cols, int32_t bits);
+
+/* bf16 weight [rows][cols] (logical row order) -> tiled codes
+ * [rows*cols/(32/bits)] words and f32 scales [rows]: quantize with the
+ * activation stride, retile, keep one scale per row. Replaces the packing
+ * half of Engine::load_quantized_weight (src/quantized.rs:147-234) after its
+ * CPU untile. Preconditions: rows % 256 == 0 && cols % 256 == 0 ->
+ * "unsupported quantized weight shape"; then those of prepare and retile. */
+int clef_i4_pack_weight(const uint16_t* w, int64_t rows, int32_t cols, int32_t bits, uint32_t* tiled,
+                        float* scales, void* workspace, size_t workspace_bytes,
+                        clef_stream_t stream);
+
+/* 256x64-tiled checkpoint layout [rows/256][cols/64][256][64] <-> logical
+ * rows. Replace checkpoint::untile_rows / tile_rows (src/checkpoint.rs:63-106,
+ * 24-32). Preconditions: rows % 256 == 0, cols % 64 == 0 -> "tiled layout
+ * requires 256-row and 64-column multiples". */
+int clef_untile_rows(const uint16_t* tiled, int64_t rows, int32_t cols, uint16_t* out,
+                     clef_stream_t stream);
+int clef_tile_rows(const uint16_t* dense, int64_t rows, int32_t cols, uint16_t* out,
+                   clef_stream_t stream);
+
+/* ------------------------------------------------------------------ G1 */
+
+/* INT4 x INT4 -> i32 dense GEMM with the reference epilogue
+ * out[m][n] = bf16(sat(RN(RN(f32(acc) * w_scales[n]) * a_scales[m]) + 0)),
+ * plus residual (bf16 [m][n], nullable): out = bf16(res + out).
+ * `a` points at the packed activation codes (row pitch k_stride/8 words) and
+ * `a_scales` at its scales. Replaces Engine::project_prepared
+ * (src/quantized.rs:470-537) and h3_gemm_i4_256[_residual]
+ * (kernels/gemm_integer.loom, gemm_integer_m128.loom, gemm_integer_wide_k.loom).
+ * Preconditions: m >= 1, n % 128 == 0, k % 256 == 0, k >= 256, k_stride >= k,
+ * k_stride % 32 == 0 -> "unsupported integer projection shape". */
+int clef_i4_gemm(const uint32_t* a, int32_t k_stride, const float* a_scales, const uint32_t* w_tiled,
+                 const float* w_scales, int64_t m, int32_t n, int32_t k, const uint16_t* residual,
+                 uint16_t* out, clef_stream_t stream);
+
+/* Same, with an explicit tile configuration (0..clef_i4_gemm_configs()-1;
+ * -1 = automatic). For tuning and tests. */
+int clef_i4_gemm_config(const uint32_t* a, int32_t k_stride, const float* a_scales,
+                        const uint32_t* w_tiled, const float* w_scales, int64_t m, int32_t n,
+                        int32_t k, const uint16_t* residual, uint16_t* out, int32_t config,
+                        clef_stream_t stream);
+int clef_i4_gemm_configs(void);
+
+/* Bytes of scratch clef_i4_project needs (the packed activation). */
+size_t clef_i4_project_workspace_bytes(int64_t m, int32_t k);
+
+/* Quantize x [m][k] with the weight's stride (clef_i4_activation_stride(k,
+ * 4)) and run G1. Replaces Engine::project_quantized /
+ * project_quantized_with_residual (src/quantized.rs:235-303). */
+int clef_i4_project(const uint16_t* x, int64_t m, int32_t k, const uint32_t* w_tiled,
+                    const float* w_scales, int32_t n, const uint16_t* residual, uint16_t* out,
+                    void* workspace, size_t workspace_bytes, clef_stream_t stream);
+
+/* ------------------------------------------------------------------ MoE */
+
+/* Top-k router: ties -> lowest expert id, softmax over the selected logits,
+ * probabilities rounded to bf16. logits_dtype 0 = bf16, 1 = f32.
+ * Replaces Engine::omni_route (src/omni.rs:170-190), kernels/omni_route.loom.
+ * Preconditions: 0 < topk <= experts <= 128 -> "invalid expert router shape";
+ * tokens >= 1. */
+int clef_moe_route(const void* logits, int32_t logits_dtype, int64_t tokens, int32_t experts,
+                   int32_t topk, float* routes, clef_stream_t stream);
+
+/* Bytes of scratch clef_moe_group_routes needs. */
+size_t clef_moe_group_workspace_bytes(int64_t tokens);
+
+/* Stable per-expert route lists (128 experts) and, when `order` is non-NULL,
+ * the ascending-expert rank order. Replaces Engine::omni_group_routes /
+ * omni_group_routes_ordered (src/omni.rs:192-245) and
+ * kernels/omni_group_routes.loom, omni_group_routes_ordered.loom. The
+ * reference caps tokens at 2048 per chunk (src/omni.rs:11); this library
+ * accepts up to 1048576 tokens in one call (every stage is row-local).
+ * Preconditions: 1 <= tokens <= 1048576, 1 <= topk <= 128 ->
+ * "unsupported Omni route grouping shape". */
+int clef_moe_group_routes(const float* routes, int64_t tokens, int32_t topk, float* groups,
+                          float* order, void* workspace, size_t workspace_bytes,
+                          clef_stream_t stream);
+
+/* Compact task list: tasks[0] = count, then (expert, 16*tile) pairs for
+ * experts ascending. Replaces the omni_expert_tasks dispatch of
+ * Engine::omni_compact_routes (src/omni.rs:126-169) and
+ * kernels/omni_expert_tasks.loom. tasks holds 1 + 2*(ceil(T*8/16)+127)
+ * floats. */
+int clef_moe_expert_tasks(const float* groups, int64_t tokens, float* tasks, clef_stream_t stream);
+
+/* Bytes of scratch clef_moe_expert_i4 needs (its tile schedule). */
+size_t clef_moe_expert_workspace_bytes(int64_t tokens, int32_t topk);
+
+/* Grouped INT4 expert GEMM over all 128 experts:
+ * out[route][c] = bf16(RN(f32(acc) * RN(a_scales[xr] * w_scales[e*n + c]))),
+ * xr = input_routed ? route : route/topk. `a` is the packed activation (row
+ * pitch stride/8 words, rows = tokens or tokens*topk), w_tiled the 128
+ * experts' codes concatenated as [128*n][k]. Output bf16 [tokens*topk][n].
+ * Replaces Engine::omni_expert_impl / omni_expert_inputs
+ * (src/omni.rs:289-534) and kernels/omni_expert_i4.loom,
+ * omni_expert_i4_k128_down.loom, omni_expert_i4_compact.loom.
+ * Preconditions: k % 256 == 0 && n % 256 == 0 && k, n >= 256 && stride >= k
+ * && stride % 8 == 0 -> "unsupported Omni expert tile shape"; tokens >= 1,
+ * 1 <= topk <= 128 -> "invalid grouped expert routes". */
+int clef_moe_expert_i4(const uint32_t* a, int32_t stride, const float* a_scales,
+                       const uint32_t* w_tiled, const float* w_scales, const float* groups,
+                       int64_t tokens, int32_t topk, int32_t k, int32_t n, int32_t input_routed,
+                       uint16_t* out, void* workspace, size_t workspace_bytes,
+                       clef_stream_t stream);
+
+/* h = bf16(bf16(g/(1+exp(-g))) * u) elementwise over n values. Replaces
+ * Engine::swiglu (src/ops.rs:9-29) and kernels/swiglu.loom. Precondition:
+ * n >= 0 -> "SwiGLU shape/dtype mismatch". */
+int clef_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h,
+                clef_stream_t stream);
+
+/* Weighted combine in ascending expert order with a bf16 rounding per step.
+ * `order` NULL selects the unordered variant (ascending ids found from the
+ * routes). Replaces Engine::omni_combine / omni_combine_ordered
+ * (src/omni.rs:246-278, 535-556) and kernels/omni_combine.loom,
+ * omni_combine_ordered.loom. Preconditions: width % 8 == 0, 1 <= topk <=
+ * 128, tokens >= 1 -> "unsupported ordered Omni accumulation". */
+int clef_moe_combine(const uint16_t* values, const float* routes, const float* order,
+                     int64_t tokens, int32_t width, int32_t topk, uint16_t* out,
+                     clef_stream_t stream);
+
+/* Bytes of scratch clef_moe_layer needs. */
+size_t clef_moe_layer_workspace_bytes(int64_t tokens, int32_t hidden, int32_t inter,
+                                      int32_t topk);
+
+/* Omni INT4 MoE block: route -> ordered grouping -> quantize x (shared by
+ * gate and up) -> gate and up expert GEMMs -> SwiGLU -> quantize h per routed
+ * row -> down expert GEMM (routed input) -> ordered combine. Output bf16
+ * [tokens][hidden]; routes_out (nullable) receives the routes. Replaces the
+ * MoE half of omni::forward_layers_cached (src/omni.rs:760-857) without the
+ * bf16 router-gate projection (logits are an input) and without the residual
+ * add. Preconditions: experts == 128 -> "Omni MoE requires 128 experts";
+ * hidden, inter % 256 == 0; then those of the stages. */
+int clef_moe_layer(const uint16_t* x, const void* logits, int32_t logits_dtype, int64_t tokens,
+                   int32_t hidden, int32_t inter, int32_t experts, int32_t topk,
+                   const uint32_t* gate_w, const float* gate_s, const uint32_t* up_w,
+                   const float* up_s, const uint32_t* down_w, const float* down_s,
+                   float* routes_out, uint16_t* out, void* workspace, size_t workspace_bytes,
+                   clef_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CLEF_I4_H */

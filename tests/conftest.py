@@ -1,15 +1,23 @@
 import os
+import subprocess
 import sys
 
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-if ROOT not in sys.path:
-    sys.path.insert(0, ROOT)
+PKG = os.path.join(ROOT, "clef-hrx_amd")
+for p in (ROOT, PKG):
+    if p not in sys.path:
+        sys.path.insert(0, p)
 
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+    # Build only what is missing; a built tree is used as is.
+    if not os.path.exists(os.path.join(PKG, "lib", "libclef_i4.so")):
+        subprocess.run(["make", "-s", "-C", PKG], check=True)
+    if not os.path.exists(os.path.join(ROOT, "oracle", "_build", "libclef_oracle.so")):
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
 
 
 def pytest_collection_modifyitems(config, items):

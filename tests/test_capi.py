@@ -1,0 +1,135 @@
+"""C ABI checks that need no GPU: the library loads, exports every entry point
+include/clef_i4.h declares, and rejects bad shapes with the reference's
+messages before touching the device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import clef_i4
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "clef_i4.h")
+FAKE = 1 << 20  # never dereferenced: every call below fails its checks first
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(clef_\w+)\s*\(", text)))
+
+
+def call(name, *args):
+    rc = getattr(clef_i4.lib(), name)(*args)
+    return rc, clef_i4.lib().clef_last_error().decode()
+
+
+def test_header_symbols_exported_and_bound():
+    syms = declared_symbols()
+    assert len(syms) >= 20
+    handle = ctypes.CDLL(clef_i4.LIB_PATH)
+    for s in syms:
+        assert hasattr(handle, s), s
+        assert s in clef_i4.SIGNATURES, f"{s} missing from the Python binding"
+    assert set(clef_i4.SIGNATURES) == set(syms)
+
+
+def test_abi_version_and_stride_rule():
+    assert clef_i4.lib().clef_abi_version() == 100
+    # src/quantized.rs:161-166
+    assert clef_i4.activation_stride(2048, 4) == 2176
+    assert clef_i4.activation_stride(768, 4) == 768
+    assert clef_i4.activation_stride(4096, 8) == 4160
+    assert clef_i4.activation_stride(12288, 4) == 12416
+    assert clef_i4.lib().clef_i4_prepared_words(3, 2176, 4) == 3 * 273
+
+
+@pytest.mark.parametrize("rows,width,stride,bits", [
+    (4, 255, 256, 4), (4, 300, 384, 4), (0, 256, 256, 4), (1048577, 256, 256, 4),
+    (4, 256, 200, 4), (4, 256, 65664, 4), (4, 256, 320, 4), (4, 256, 256, 5), (4, 32768 + 256, 33024, 4),
+])
+def test_prepare_rejects(rows, width, stride, bits):
+    rc, msg = call("clef_i4_prepare", FAKE, rows, width, stride, bits, FAKE, None)
+    assert rc == -1 and msg == "unsupported rotated integer operand"
+
+
+def test_prepare_rejects_misaligned_pointer():
+    rc, msg = call("clef_i4_prepare", FAKE + 2, 4, 256, 256, 4, FAKE, None)
+    assert rc == -1 and "aligned" in msg
+
+
+@pytest.mark.parametrize("rows,in_words,cols", [(100, 32, 256), (128, 16, 256), (128, 32, 200)])
+def test_retile_rejects(rows, in_words, cols):
+    rc, msg = call("clef_i4_retile", FAKE, rows, in_words, cols, 4, FAKE, None)
+    assert rc == -1 and msg == "unsupported packed weight shape for tiling"
+
+
+def test_pack_weight_rejects():
+    rc, msg = call("clef_i4_pack_weight", FAKE, 128, 256, 4, FAKE, FAKE, FAKE, 1 << 20, None)
+    assert rc == -1 and msg == "unsupported quantized weight shape"
+    need = clef_i4.lib().clef_i4_pack_weight_workspace_bytes(256, 256, 4)
+    assert need >= 256 * (256 // 8 + 1) * 4
+    rc, msg = call("clef_i4_pack_weight", FAKE, 256, 256, 4, FAKE, FAKE, FAKE, need - 1, None)
+    assert rc == -1 and msg == "workspace too small"
+
+
+@pytest.mark.parametrize("m,n,k,ks", [(0, 128, 256, 256), (4, 100, 256, 256), (4, 128, 300, 320),
+                                      (4, 128, 256, 200), (4, 128, 256, 272)])
+def test_gemm_rejects(m, n, k, ks):
+    rc, msg = call("clef_i4_gemm", FAKE, ks, FAKE, FAKE, FAKE, m, n, k, None, FAKE, None)
+    assert rc == -1 and msg == "unsupported integer projection shape"
+
+
+def test_gemm_rejects_unknown_config():
+    rc, msg = call("clef_i4_gemm_config", FAKE, 256, FAKE, FAKE, FAKE, 4, 128, 256, None, FAKE, 99, None)
+    assert rc == -1 and "configuration" in msg
+
+
+@pytest.mark.parametrize("experts,topk", [(129, 8), (8, 9), (8, 0)])
+def test_route_rejects(experts, topk):
+    rc, msg = call("clef_moe_route", FAKE, 0, 4, experts, topk, FAKE, None)
+    assert rc == -1 and msg == "invalid expert router shape"
+
+
+def test_group_rejects():
+    rc, msg = call("clef_moe_group_routes", FAKE, 0, 8, FAKE, None, FAKE, 1 << 20, None)
+    assert rc == -1 and msg == "unsupported Omni route grouping shape"
+    need = clef_i4.lib().clef_moe_group_workspace_bytes(4096)
+    rc, msg = call("clef_moe_group_routes", FAKE, 4096, 8, FAKE, None, FAKE, need - 1, None)
+    assert rc == -1 and msg == "workspace too small"
+
+
+@pytest.mark.parametrize("k,n,stride", [(300, 256, 320), (256, 128, 256), (256, 256, 200)])
+def test_expert_rejects(k, n, stride):
+    rc, msg = call("clef_moe_expert_i4", FAKE, stride, FAKE, FAKE, FAKE, FAKE, 4, 8, k, n, 0, FAKE, FAKE,
+                   1 << 20, None)
+    assert rc == -1 and msg == "unsupported Omni expert tile shape"
+
+
+def test_combine_rejects():
+    rc, msg = call("clef_moe_combine", FAKE, FAKE, FAKE, 4, 12, 8, FAKE, None)
+    assert rc == -1 and msg == "unsupported ordered Omni accumulation"
+
+
+def test_swiglu_rejects_and_empty_is_noop():
+    rc, msg = call("clef_swiglu", FAKE, FAKE, -1, FAKE, None)
+    assert rc == -1 and msg == "SwiGLU shape/dtype mismatch"
+    rc, _ = call("clef_swiglu", FAKE, FAKE, 0, FAKE, None)
+    assert rc == 0
+
+
+def test_tile_rows_rejects():
+    rc, msg = call("clef_untile_rows", FAKE, 128, 64, FAKE, None)
+    assert rc == -1 and msg == "tiled layout requires 256-row and 64-column multiples"
+
+
+def test_moe_layer_rejects():
+    rc, msg = call("clef_moe_layer", FAKE, FAKE, 0, 16, 2048, 768, 64, 8, FAKE, FAKE, FAKE, FAKE, FAKE,
+                   FAKE, None, FAKE, FAKE, 1 << 30, None)
+    assert rc == -1 and msg == "Omni MoE requires 128 experts"
+    need = clef_i4.lib().clef_moe_layer_workspace_bytes(16, 2048, 768, 8)
+    assert need > 16 * 8 * 2048 * 2
+    rc, msg = call("clef_moe_layer", FAKE, FAKE, 0, 16, 2048, 768, 128, 8, FAKE, FAKE, FAKE, FAKE, FAKE,
+                   FAKE, None, FAKE, FAKE, need - 1, None)
+    assert rc == -1 and msg == "workspace too small"

@@ -1,0 +1,423 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle on the same
+seeded inputs. Integer stages and bf16 outputs are compared bit for bit: the
+kernels and the oracle compute the same IEEE sequence (routing probabilities
+and SwiGLU use the same explicit exp steps on both sides).
+
+Each test names the reference test whose inputs or edge cases it follows.
+"""
+import numpy as np
+import pytest
+import torch
+
+import clef_i4
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+BF = oracle.f32_to_bf16
+F = oracle.bf16_to_f32
+DEV = "cuda"
+
+
+def to_dev_bf16(a_u16: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a_u16).view(np.int16)).view(torch.bfloat16).to(DEV)
+
+
+def bf16_host(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def u32_host(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().cpu().numpy().view(np.uint32)
+
+
+def to_dev_u32(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(DEV)
+
+
+def to_dev_f32(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(DEV)
+
+
+def randn_bf16(rng, shape, std=1.0) -> np.ndarray:
+    return BF((rng.standard_normal(shape) * std).astype(np.float32))
+
+
+def assert_same_u16(got: np.ndarray, want: np.ndarray, what: str):
+    if not np.array_equal(got, want):
+        bad = np.argwhere(got != want)
+        i = tuple(bad[0])
+        raise AssertionError(f"{what}: {len(bad)} mismatches, first at {i}: got {got[i]:#06x} "
+                             f"want {want[i]:#06x}")
+
+
+def assert_same_u32(got: np.ndarray, want: np.ndarray, what: str):
+    if not np.array_equal(got, want):
+        bad = np.argwhere(got != want)
+        i = tuple(bad[0])
+        raise AssertionError(f"{what}: {len(bad)} mismatches, first at {i}: got {got[i]:#010x} "
+                             f"want {want[i]:#010x}")
+
+
+def exceptional_rows(width: int) -> np.ndarray:
+    """Rows of src/quantized.rs:1138-1150 plus zero and e_0 rows."""
+    rows = []
+    base = F(BF(np.array([((i * 37 % 257) - 128) / 91.0 for i in range(width)], dtype=np.float32)))
+    r = base.copy()
+    r[259 % width] = np.nan
+    rows.append(r)
+    r = base.copy()
+    r[515 % width] = np.inf
+    rows.append(r)
+    r = base.copy()
+    r[3] = F(np.array([0x7F7F], dtype=np.uint16))[0]  # bf16::MAX
+    rows.append(r)
+    r = base.copy()
+    r[7] = F(np.array([0x0001], dtype=np.uint16))[0]  # bf16 denormal
+    rows.append(r)
+    rows.append(np.full(width, -0.5, dtype=np.float32))
+    rows.append(np.full(width, 19.0, dtype=np.float32))
+    rows.append(np.zeros(width, dtype=np.float32))
+    e0 = np.zeros(width, dtype=np.float32)
+    e0[0] = 1.0
+    rows.append(e0)
+    rows.append(base)
+    return BF(np.stack(rows))
+
+
+# ---------------------------------------------------------------- Q1 / Q2
+
+@pytest.mark.parametrize("width", [256, 768, 1024, 2048, 4096, 4352, 5120, 12288, 17408, 32768])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_prepare_matches_oracle(width, bits):
+    """rotated_packing_cpu_oracle / register_packing_matches_reference
+    (src/quantized.rs:1074-1185): codes and scales exact."""
+    rng = np.random.default_rng(width * 10 + bits)
+    rows = 37 if width <= 4096 else 11
+    x = np.concatenate([randn_bf16(rng, (rows, width)), exceptional_rows(width)])
+    stride = oracle.activation_stride(width, bits)
+    _, _, want = oracle.prepare(x, stride, bits)
+    got = clef_i4.prepare(to_dev_bf16(x), bits=bits, stride=stride)
+    assert_same_u32(u32_host(got.storage), want, f"prepare width={width} bits={bits}")
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 5, 16, 17, 1000])
+def test_prepare_row_counts(rows):
+    rng = np.random.default_rng(rows)
+    for width in (768, 2048):
+        x = randn_bf16(rng, (rows, width), std=3.0)
+        stride = oracle.activation_stride(width)
+        _, _, want = oracle.prepare(x, stride)
+        got = clef_i4.prepare(to_dev_bf16(x), stride=stride)
+        assert_same_u32(u32_host(got.storage), want, f"prepare rows={rows} width={width}")
+
+
+@pytest.mark.parametrize("width", [768, 2048, 17408])
+def test_prepare_swiglu_matches_oracle(width):
+    """fused_swiglu_packing_matches_reference (src/quantized.rs:1189-1266)."""
+    rng = np.random.default_rng(width)
+    rows = 19
+    g = randn_bf16(rng, (rows, width), std=2.0)
+    u = randn_bf16(rng, (rows, width), std=2.0)
+    stride = oracle.activation_stride(width)
+    _, _, want = oracle.prepare_swiglu(g, u, stride)
+    got = clef_i4.prepare_swiglu(to_dev_bf16(g), to_dev_bf16(u), stride=stride)
+    assert_same_u32(u32_host(got.storage), want, f"prepare_swiglu width={width}")
+
+
+@pytest.mark.parametrize("rows,cols", [(128, 256), (256, 2048), (384, 768)])
+def test_retile_matches_block_formula(rows, cols):
+    """retiled_codes_match_block_formula (src/quantized.rs:1371-1407)."""
+    in_words = cols // 8 + 16
+    codes = (np.arange(rows * in_words, dtype=np.uint64) * 2654435761 % (1 << 32)).astype(np.uint32)
+    codes = codes.reshape(rows, in_words)
+    want = oracle.retile(codes, cols)
+    got = clef_i4.retile_codes(to_dev_u32(codes), rows, cols)
+    assert_same_u32(u32_host(got), want, "retile")
+
+
+def test_pack_weight_matches_oracle():
+    rng = np.random.default_rng(3)
+    for rows, cols in [(256, 2048), (512, 768), (256, 4096)]:
+        w = randn_bf16(rng, (rows, cols), std=0.02)
+        want_codes, want_scales = oracle.pack_weight(w)
+        qw = clef_i4.load_quantized_weight(to_dev_bf16(w))
+        assert_same_u32(u32_host(qw.codes), want_codes, "pack codes")
+        assert np.array_equal(qw.scales.cpu().numpy().view(np.uint32), want_scales.view(np.uint32))
+
+
+def test_untile_rows_roundtrip():
+    rng = np.random.default_rng(4)
+    w = rng.integers(0, 1 << 16, size=(512, 192), dtype=np.uint16)
+    tiled = oracle.tile_rows(w)
+    got = clef_i4.untile_rows(to_dev_bf16(tiled))
+    assert_same_u16(bf16_host(got), w, "untile")
+    back = clef_i4.tile_rows(to_dev_bf16(w))
+    assert_same_u16(bf16_host(back), tiled, "tile")
+
+
+# ---------------------------------------------------------------- G1
+
+def make_operands(rng, m, n, k, x_std=1.0, w_std=0.02):
+    x = randn_bf16(rng, (m, k), std=x_std)
+    w = randn_bf16(rng, (n, k), std=w_std)
+    stride = oracle.activation_stride(k)
+    a_codes, a_scales, _ = oracle.prepare(x, stride)
+    w_tiled, w_scales = oracle.pack_weight(w)
+    return x, w, stride, a_codes, a_scales, w_tiled, w_scales
+
+
+def dev_prepared(x_u16, stride):
+    return clef_i4.prepare(to_dev_bf16(x_u16), stride=stride)
+
+
+def dev_weight(w_tiled, w_scales, n, k):
+    return clef_i4.QuantizedWeight(to_dev_u32(w_tiled), to_dev_f32(w_scales), n, k,
+                                   oracle.activation_stride(k), 4)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 128, 256), (17, 256, 768), (128, 128, 2048), (300, 384, 1024),
+                                   (257, 512, 4096), (64, 1024, 12288)])
+def test_gemm_matches_oracle_all_configs(m, n, k):
+    """G1 epilogue bit-exact for every tile configuration; M not a tile
+    multiple exercises the row guard (residual_projection_matches_separate_addition
+    covers 36 row counts, src/quantized.rs:1411-1552)."""
+    rng = np.random.default_rng(m * 7 + n + k)
+    x, w, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
+    want = oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k)
+    a = dev_prepared(x, stride)
+    qw = dev_weight(w_tiled, w_scales, n, k)
+    for cfg in range(clef_i4.gemm_configs()):
+        got = clef_i4.project_prepared(a, qw, config=cfg)
+        assert_same_u16(bf16_host(got), want, f"gemm m={m} n={n} k={k} config={cfg}")
+    got = clef_i4.project_quantized(to_dev_bf16(x), qw)
+    assert_same_u16(bf16_host(got), want, "project_quantized")
+
+
+@pytest.mark.parametrize("m", [1, 31, 128, 129, 255, 256, 257, 4032])
+def test_gemm_residual_matches_oracle(m):
+    """residual_projection_matches_separate_addition (src/quantized.rs:1411-1552)."""
+    n, k = 256, 1024
+    rng = np.random.default_rng(m)
+    x, w, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
+    res = randn_bf16(rng, (m, n), std=4.0)
+    want = oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k, residual=res)
+    sep = oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k)
+    assert np.array_equal(want, BF(F(res) + F(sep)))
+    a = dev_prepared(x, stride)
+    qw = dev_weight(w_tiled, w_scales, n, k)
+    for cfg in range(clef_i4.gemm_configs()):
+        got = clef_i4.project_prepared(a, qw, residual=to_dev_bf16(res), config=cfg)
+        assert_same_u16(bf16_host(got), want, f"residual m={m} config={cfg}")
+
+
+def test_gemm_extreme_codes_and_saturation():
+    """All codes at +-7 (|acc| = 49 K), huge scales (saturation to bf16 max),
+    infinite and NaN activation scales (kernels/gemm_integer.loom:411-418)."""
+    m, n, k = 64, 128, 4096
+    stride = oracle.activation_stride(k)
+    a_words = np.full((m, stride // 8), 0x77777777, dtype=np.uint32)
+    a_words[1::2, : k // 8] = 0x99999999  # -7
+    w_codes = np.full((n, stride // 8), 0x99999999, dtype=np.uint32)
+    w_codes[::3, : k // 8] = 0x77777777
+    w_tiled = oracle.retile(w_codes, k)
+    a_scales = np.full(m, 1e30, dtype=np.float32)
+    a_scales[5] = np.inf
+    a_scales[6] = np.nan
+    a_scales[7] = 1e-3
+    w_scales = np.full(n, 1e10, dtype=np.float32)
+    w_scales[::5] = 1e-30
+    want = oracle.gemm(a_words, a_scales, w_tiled, w_scales, n, k)
+    storage = np.concatenate([a_words.reshape(-1), a_scales.view(np.uint32)])
+    a = clef_i4.Prepared(to_dev_u32(storage), m, k, stride, 4)
+    qw = dev_weight(w_tiled, w_scales, n, k)
+    for cfg in range(clef_i4.gemm_configs()):
+        got = clef_i4.project_prepared(a, qw, config=cfg)
+        assert_same_u16(bf16_host(got), want, f"extreme config={cfg}")
+
+
+def test_identity_weight_reproduces_input():
+    """activation_scratch_is_bounded (src/quantized.rs:880-915): a 256x256
+    identity weight maps a constant row to itself exactly."""
+    k = n = 256
+    w = np.zeros((n, k), dtype=np.float32)
+    np.fill_diagonal(w, 1.0)
+    qw = clef_i4.load_quantized_weight(to_dev_bf16(BF(w)))
+    x = BF(np.stack([np.full(k, v, dtype=np.float32) for v in (0.25, 1.0, -3.0, 8.0)]))
+    y = clef_i4.project_quantized(to_dev_bf16(x), qw)
+    assert_same_u16(bf16_host(y), x, "identity projection")
+
+
+def test_gemm_is_deterministic():
+    m, n, k = 512, 512, 2048
+    rng = np.random.default_rng(11)
+    x, w, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
+    a = dev_prepared(x, stride)
+    qw = dev_weight(w_tiled, w_scales, n, k)
+    first = bf16_host(clef_i4.project_prepared(a, qw))
+    for _ in range(3):
+        assert np.array_equal(bf16_host(clef_i4.project_prepared(a, qw)), first)
+
+
+# ---------------------------------------------------------------- MoE routing
+
+def tie_logits(rng, tokens, experts, dtype):
+    """Router phases of src/benchmarking/omni.rs:43-55: duplicates, +-0, large values."""
+    logits = rng.standard_normal((tokens, experts)).astype(np.float32)
+    logits[::4] = np.round(logits[::4] * 2) / 2          # many exact ties
+    logits[1::7] = 0.0
+    logits[1::7, ::3] = -0.0
+    logits[2::9] *= 1e4
+    logits[3::11, :16] = 7.0                             # one tied block
+    if dtype == "bf16":
+        return BF(logits)
+    return logits
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("experts,topk", [(128, 8), (64, 8), (128, 1), (100, 16)])
+def test_route_matches_oracle(dtype, experts, topk):
+    """OmniRouter paired check (src/benchmarking/omni.rs:42-90): ids exact,
+    probabilities bit-exact (same exp steps)."""
+    rng = np.random.default_rng(experts + topk)
+    logits = tie_logits(rng, 333, experts, dtype)
+    want = oracle.route(logits, topk)
+    dev = to_dev_bf16(logits) if dtype == "bf16" else to_dev_f32(logits)
+    got = clef_i4.omni_route(dev, topk).cpu().numpy()
+    assert np.array_equal(got[:, :topk], want[:, :topk]), "route ids"
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "route probabilities"
+
+
+def test_route_ids_are_stable_sort():
+    """The selected ids equal a stable descending sort (src/omni.rs:997-1009)."""
+    rng = np.random.default_rng(5)
+    logits = tie_logits(rng, 200, 128, "f32")
+    got = clef_i4.omni_route(to_dev_f32(logits), 8).cpu().numpy()
+    want = np.argsort(-logits, axis=1, kind="stable")[:, :8]
+    assert np.array_equal(got[:, :8].astype(np.int64), want)
+
+
+def random_routes(rng, tokens, topk=8, skew=0.0):
+    logits = rng.standard_normal((tokens, 128)).astype(np.float32)
+    if skew:
+        logits -= skew * np.log1p(rng.permutation(128)).astype(np.float32)
+    return oracle.route(logits, topk)
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 17, 255, 256, 257, 1000, 4096])
+def test_group_routes_matches_oracle(tokens):
+    """grouped_routes_match_cpu (src/omni.rs:908-942): stable lists, counts, order."""
+    rng = np.random.default_rng(tokens)
+    routes = random_routes(rng, tokens, skew=1.0 if tokens > 100 else 0.0)
+    want_g, want_o = oracle.group_routes(routes)
+    g, o = clef_i4.omni_group_routes(to_dev_f32(routes))
+    g = g.cpu().numpy()
+    o = o.cpu().numpy()
+    for e in range(128):
+        c = int(want_g[e, 0])
+        assert g[e, 0] == want_g[e, 0], f"count e={e}"
+        assert np.array_equal(g[e, 1:1 + c], want_g[e, 1:1 + c]), f"list e={e}"
+    assert np.array_equal(o, want_o), "order"
+    tasks = clef_i4.omni_expert_tasks(to_dev_f32(want_g)).cpu().numpy()
+    want_t = oracle.expert_tasks(want_g)
+    total = int(want_t[0])
+    assert np.array_equal(tasks[: 1 + 2 * total], want_t[: 1 + 2 * total]), "tasks"
+
+
+def test_group_routes_empty_and_full_experts():
+    """Empty experts and one expert taking every token (src/omni.rs:920-938)."""
+    tokens = 600
+    routes = np.zeros((tokens, 16), dtype=np.float32)
+    for t in range(tokens):
+        ids = [5] + [int(x) for x in np.random.default_rng(t).choice(np.arange(6, 128), 7, replace=False)]
+        routes[t, :8] = ids
+        routes[t, 8:] = 0.125
+    want_g, want_o = oracle.group_routes(routes)
+    g, o = clef_i4.omni_group_routes(to_dev_f32(routes))
+    g = g.cpu().numpy()
+    assert g[5, 0] == tokens and all(g[e, 0] == 0 for e in range(5))
+    for e in range(128):
+        c = int(want_g[e, 0])
+        assert np.array_equal(g[e, :1 + c], want_g[e, :1 + c]), f"e={e}"
+    assert np.array_equal(o.cpu().numpy(), want_o)
+
+
+# ---------------------------------------------------------------- E1, S1, C1
+
+def packed_experts(rng, n, k):
+    w = randn_bf16(rng, (128 * n, k), std=0.02)
+    return oracle.pack_weight(w)
+
+
+@pytest.mark.parametrize("tokens", [3, 64, 300])
+def test_expert_gemm_matches_oracle(tokens):
+    """routed_experts_match_sparse_cpu_oracle (src/omni.rs:946-1051) and the
+    OmniExpert paired check (src/benchmarking/omni.rs:328-356), bit-exact."""
+    rng = np.random.default_rng(tokens)
+    hidden, inter, topk = 512, 256, 8
+    routes = random_routes(rng, tokens, skew=2.0)
+    groups, _ = oracle.group_routes(routes)
+    x = randn_bf16(rng, (tokens, hidden))
+    sx = oracle.activation_stride(hidden)
+    ax_codes, ax_scales, _ = oracle.prepare(x, sx)
+    gw, gs = packed_experts(rng, inter, hidden)
+    want = oracle.expert_i4(ax_codes, ax_scales, gw, gs, groups, tokens, topk, hidden, inter, False)
+    got = clef_i4.omni_expert(dev_prepared(x, sx), dev_weight(gw, gs, 128 * inter, hidden),
+                              to_dev_f32(groups), tokens, topk, False)
+    assert_same_u16(bf16_host(got), want, "expert gate")
+    # routed input (down projection): rows are routes
+    h = randn_bf16(rng, (tokens * topk, inter))
+    sh = oracle.activation_stride(inter)
+    ah_codes, ah_scales, _ = oracle.prepare(h, sh)
+    dw, ds = packed_experts(rng, hidden, inter)
+    want = oracle.expert_i4(ah_codes, ah_scales, dw, ds, groups, tokens, topk, inter, hidden, True)
+    got = clef_i4.omni_expert(dev_prepared(h, sh), dev_weight(dw, ds, 128 * hidden, inter),
+                              to_dev_f32(groups), tokens, topk, True)
+    assert_same_u16(bf16_host(got), want, "expert down")
+
+
+def test_swiglu_every_bf16_gate():
+    """swiglu_preserves_materialized_rounding (src/ops.rs:482-520) over all
+    65536 gate bit patterns."""
+    gate = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    rng = np.random.default_rng(9)
+    up = randn_bf16(rng, 65536, std=3.0)
+    want = oracle.swiglu(gate, up)
+    got = clef_i4.swiglu(to_dev_bf16(gate), to_dev_bf16(up))
+    assert_same_u16(bf16_host(got), want, "swiglu")
+    odd = clef_i4.swiglu(to_dev_bf16(gate[:1003]), to_dev_bf16(up[:1003]))
+    assert_same_u16(bf16_host(odd), want[:1003], "swiglu tail")
+
+
+@pytest.mark.parametrize("ordered", [True, False])
+def test_combine_matches_oracle(ordered):
+    """OmniCombine paired check (src/benchmarking/omni.rs:387-431)."""
+    rng = np.random.default_rng(int(ordered))
+    tokens, width, topk = 77, 2048, 8
+    routes = random_routes(rng, tokens)
+    _, order = oracle.group_routes(routes)
+    values = randn_bf16(rng, (tokens * topk, width), std=2.0)
+    want = oracle.combine(values, routes, order if ordered else None)
+    got = clef_i4.omni_combine(to_dev_bf16(values), to_dev_f32(routes),
+                               to_dev_f32(order) if ordered else None)
+    assert_same_u16(bf16_host(got), want, "combine")
+
+
+@pytest.mark.parametrize("tokens,hidden,inter", [(5, 512, 256), (96, 2048, 768), (300, 1024, 512)])
+def test_moe_layer_matches_oracle(tokens, hidden, inter):
+    """Whole Omni INT4 MoE block (src/omni.rs:762-857) bit-exact vs the oracle."""
+    rng = np.random.default_rng(tokens + hidden)
+    x = randn_bf16(rng, (tokens, hidden))
+    logits = BF(rng.standard_normal((tokens, 128)).astype(np.float32))
+    gate = packed_experts(rng, inter, hidden)
+    up = packed_experts(rng, inter, hidden)
+    down = packed_experts(rng, hidden, inter)
+    want, want_routes = oracle.moe_layer(x, logits, gate, up, down)
+    layer = clef_i4.MoeLayer(dev_weight(*gate, 128 * inter, hidden), dev_weight(*up, 128 * inter, hidden),
+                             dev_weight(*down, 128 * hidden, inter))
+    routes = torch.empty((tokens, 16), dtype=torch.float32, device=DEV)
+    got = layer(to_dev_bf16(x), to_dev_bf16(logits), routes_out=routes)
+    assert np.array_equal(routes.cpu().numpy().view(np.uint32), want_routes.view(np.uint32))
+    assert_same_u16(bf16_host(got), want, f"moe layer tokens={tokens}")
+    again = layer(to_dev_bf16(x), to_dev_bf16(logits))
+    assert_same_u16(bf16_host(again), want, "moe layer replay")
