@@ -1,0 +1,241 @@
+"""Benchmark of the gfx950 INT4 quantized-matmul + Omni INT4 MoE hot path.
+
+Metric: INT4 GEMM TOPS (% of the int8 MFMA peak) + MoE-layer tokens/s at
+M=4096 on one MI355X.
+
+  value        TOPS of the INT4 GEMM M=4096 K=4096 N=12288 (the gate projection
+               of the 4096-token INT4-MLP block), prepacked operands resident in
+               HBM, timed over --steps launches. TOPS = 2*M*N*K / time.
+  moe_*        Omni INT4 MoE layer, 4096 tokens, hidden 2048, 128 experts,
+               top-8, expert intermediate 768: route -> group -> expert GEMMs
+               -> SwiGLU -> combine, timed over --steps layer calls.
+  mlp_*        INT4-MLP dense block, 4096 x 4096 input, gate|up 24576 x 4096,
+               down 4096 x 12288: quantize -> GEMM -> SwiGLU+quantize -> GEMM.
+  roofline     the GEMM kernel against the int8 MFMA peak (5.0 POP/s).
+  cpu_baseline the CPU oracle (quantize + i32 matmul + epilogue; MoE layer) on
+               a bounded sample, timed on this host's cores.
+
+Inputs are synthetic: X ~ N(0,1) bf16, weights ~ N(0,0.02) bf16 packed by the
+library's own quantizer, router logits ~ N(0,1) bf16, all seeded.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "clef-hrx_amd"))
+sys.path.insert(0, ROOT)
+
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--only", choices=["gemm", "moe", "mlp"], default=None)
+    return p.parse_args()
+
+
+def timed(fn, steps, warmup):
+    """Average ms per call of fn over `steps` calls on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def bf16_randn(shape, std, seed):
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return (torch.randn(shape, generator=g, device="cuda", dtype=torch.float32) * std).to(torch.bfloat16)
+
+
+def gemm_leg(args):
+    import clef_i4
+
+    m, k, n = 4096, 4096, 12288
+    x = bf16_randn((m, k), 1.0, 1002 * 16 + 0)
+    w = bf16_randn((n, k), 0.02, 1002 * 16 + 1)
+    qw = clef_i4.load_quantized_weight(w)
+    a = clef_i4.prepare(x)
+    import torch
+
+    out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    ms = timed(lambda: clef_i4.project_prepared(a, qw, out=out), args.steps, args.warmup)
+    prep_ms = timed(lambda: clef_i4.prepare(x, out=a.storage), args.steps, args.warmup)
+    ops = 2.0 * m * n * k
+    return {"m": m, "n": n, "k": k, "ms": ms, "tops": ops / ms / 1e9, "prepare_ms": prep_ms,
+            "ops": ops}
+
+
+def mlp_leg(args):
+    import torch
+
+    import clef_i4
+
+    m, d, f = 4096, 4096, 12288
+    x = bf16_randn((m, d), 1.0, 1002 * 16 + 0)
+    wg = clef_i4.load_quantized_weight(bf16_randn((f, d), 0.02, 1002 * 16 + 2))
+    wu = clef_i4.load_quantized_weight(bf16_randn((f, d), 0.02, 1002 * 16 + 3))
+    wd = clef_i4.load_quantized_weight(bf16_randn((d, f), 0.02, 1002 * 16 + 4))
+    gate = torch.empty((m, f), dtype=torch.bfloat16, device="cuda")
+    up = torch.empty((m, f), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((m, d), dtype=torch.bfloat16, device="cuda")
+    a = clef_i4.prepare(x)
+    sh = clef_i4.activation_stride(f)
+    h = clef_i4.Prepared(torch.zeros(m * (sh // 8 + 1), dtype=torch.int32, device="cuda"), m, f, sh, 4)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def block():
+        clef_i4.prepare(x, out=a.storage)
+        clef_i4.project_prepared(a, wg, out=gate)
+        clef_i4.project_prepared(a, wu, out=up)
+        clef_i4._check(clef_i4.lib().clef_i4_prepare_swiglu(gate.data_ptr(), up.data_ptr(), m, f, sh, 4,
+                                                            h.storage.data_ptr(), stream))
+        clef_i4.project_prepared(h, wd, out=y)
+
+    ms = timed(block, max(1, args.steps // 2), args.warmup)
+    ops = 2.0 * m * (2 * f) * d + 2.0 * m * d * f
+    return {"ms": ms, "tops": ops / ms / 1e9}
+
+
+def moe_leg(args):
+    import torch
+
+    import clef_i4
+
+    t, d, inter = 4096, 2048, 768
+    x = bf16_randn((t, d), 1.0, 1004 * 16 + 0)
+    logits = bf16_randn((t, 128), 1.0, 1004 * 16 + 1)
+    gate = clef_i4.load_quantized_weight(bf16_randn((128 * inter, d), 0.02, 1004 * 16 + 2))
+    up = clef_i4.load_quantized_weight(bf16_randn((128 * inter, d), 0.02, 1004 * 16 + 3))
+    down = clef_i4.load_quantized_weight(bf16_randn((128 * d, inter), 0.02, 1004 * 16 + 4))
+    layer = clef_i4.MoeLayer(gate, up, down)
+    out = torch.empty((t, d), dtype=torch.bfloat16, device="cuda")
+    ms = timed(lambda: layer(x, logits, out=out), args.steps, args.warmup)
+    ops = 8.0 * t * 2 * (2 * inter * d + d * inter)
+    return {"tokens": t, "ms": ms, "tokens_per_s": t / ms * 1e3, "tops": ops / ms / 1e9}
+
+
+def cpu_leg():
+    """The oracle on the GEMM and MoE workloads, timed on this host's cores.
+
+    Timing does not depend on the weight values, so weights are random packed
+    codes with unit scales; activations are N(0,1) bf16 quantized inside the
+    timed region (the reference's CPU path is quantize -> i32 dot -> scale).
+    """
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(1002)
+    threads = oracle.threads()
+
+    def codes(words):
+        return rng.integers(0, 1 << 32, size=words, dtype=np.uint64).astype(np.uint32)
+
+    m, n, k = 4096, 12288, 4096
+    x = oracle.f32_to_bf16(rng.standard_normal((m, k)).astype(np.float32))
+    w_tiled, w_scales = codes(n * k // 8), np.full(n, 1e-3, dtype=np.float32)
+    t0 = time.perf_counter()
+    a_codes, a_scales, _ = oracle.prepare(x, oracle.activation_stride(k))
+    oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k)
+    gemm_s = time.perf_counter() - t0
+
+    t, d, inter = 4096, 2048, 768
+    xs = oracle.f32_to_bf16(rng.standard_normal((t, d)).astype(np.float32))
+    lg = oracle.f32_to_bf16(rng.standard_normal((t, 128)).astype(np.float32))
+    g = (codes(128 * inter * d // 8), np.full(128 * inter, 1e-3, dtype=np.float32))
+    u = (codes(128 * inter * d // 8), np.full(128 * inter, 1e-3, dtype=np.float32))
+    dn = (codes(128 * d * inter // 8), np.full(128 * d, 1e-3, dtype=np.float32))
+    t0 = time.perf_counter()
+    oracle.moe_layer(xs, lg, g, u, dn)
+    moe_s = time.perf_counter() - t0
+    return {
+        "value": round(2.0 * m * n * k / gemm_s / 1e12, 4),
+        "unit": "TOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"full INT4 GEMM M{m} N{n} K{k} incl. activation quantize ({gemm_s:.2f} s); "
+                  f"full MoE layer T{t} D{d} I{inter} ({moe_s:.2f} s)",
+        "moe_tokens_per_s": round(t / moe_s, 1),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
+              "sharding of this path is a design note, not a measured configuration.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import clef_i4
+
+    clef_i4.lib()
+    torch.cuda.init()
+    res = {}
+    if args.only in (None, "gemm"):
+        res["gemm"] = gemm_leg(args)
+    if args.only in (None, "moe"):
+        res["moe"] = moe_leg(args)
+    if args.only in (None, "mlp"):
+        res["mlp"] = mlp_leg(args)
+    cpu = None if args.no_cpu or args.only else cpu_leg()
+
+    g = res.get("gemm")
+    line = {
+        "metric": "INT4 GEMM TOPS (% int8 MFMA peak) + MoE-layer tokens/s at M=4096, 1 MI355X",
+        "value": round(g["tops"], 1) if g else None,
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["ms"], 4) if g else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xint4->i32 (int8 MFMA), bf16 out",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, packed by the library)",
+        "config": {"workload": "int4_gemm M4096 K4096 N12288 prepacked + omni_int4_moe T4096 "
+                               "D2048 E128 top8 I768 + int4_mlp M4096 D4096 F12288",
+                   "parallelism": "single GPU"},
+    }
+    if g:
+        line["pct_int8_peak"] = round(100.0 * g["tops"] / INT8_PEAK_TOPS, 2)
+        line["prepare_ms"] = round(g["prepare_ms"], 4)
+        line["roofline"] = {"bound": "mfma", "achieved": round(g["tops"], 1), "peak": INT8_PEAK_TOPS,
+                            "unit": "TFLOP/s", "frac": round(g["tops"] / INT8_PEAK_TOPS, 4),
+                            "traffic": None}
+    if "moe" in res:
+        line["moe_tokens_per_s"] = round(res["moe"]["tokens_per_s"], 1)
+        line["moe_layer_ms"] = round(res["moe"]["ms"], 4)
+        line["moe_tops"] = round(res["moe"]["tops"], 1)
+    if "mlp" in res:
+        line["mlp_block_ms"] = round(res["mlp"]["ms"], 4)
+        line["mlp_tops"] = round(res["mlp"]["tops"], 1)
+    if cpu:
+        line["cpu_baseline"] = cpu
+        if "moe" in res:
+            line["moe_vs_cpu"] = round(res["moe"]["tokens_per_s"] / cpu["moe_tokens_per_s"], 1)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

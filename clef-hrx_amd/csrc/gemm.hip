@@ -9,6 +9,7 @@
 // route = groups[e][1+i], xr = input_routed ? route : route / topk,
 // out[route][c] = bf16(RN(f32(acc) * RN(as[xr] * ws[e*n + c]))), no clamp.
 #include "gemm_core.hpp"
+#include "gemm_dma.hpp"
 #include "kernels.hpp"
 
 namespace clef {
@@ -88,6 +89,110 @@ __global__ __launch_bounds__(256) void gemm_i4_kernel(
     }
   }
 }
+
+// Block -> output tile. Workgroups are dispatched round-robin over the 8
+// XCDs (block b runs on XCD b % 8), so block b is renumbered to make each
+// XCD's blocks consecutive, then the renumbered order walks 8-tile-tall
+// column bands: 32 co-resident blocks of one XCD cover an 8 x 4 patch and
+// share its A and B panels in that XCD's L2.
+__device__ __forceinline__ void tile_of_block(int64_t b, int64_t blocks, int tiles_m, int tiles_n,
+                                              int64_t& tm, int& tn) {
+  const int64_t per = blocks / 8;
+  const int64_t r = b < 8 * per ? (b % 8) * per + b / 8 : b;
+  const int64_t band = 8 * (int64_t)tiles_n;
+  const int64_t group = r / band, within = r - group * band;
+  const int64_t first = group * 8;
+  const int64_t height = tiles_m - first < 8 ? tiles_m - first : 8;
+  tm = first + within % height;
+  tn = (int)(within / height);
+}
+
+template <class T, bool RESID>
+__global__ __launch_bounds__(T::THREADS) void gemm_dma_kernel(
+    const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
+    const uint32_t* __restrict__ w, const float* __restrict__ ws, int64_t M, int N, int kb,
+    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
+  extern __shared__ __align__(16) char lds[];
+  const int tid = threadIdx.x;
+  int64_t tm;
+  int tn;
+  tile_of_block(blockIdx.x, (int64_t)gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = tm * T::BM;
+  const int n0 = tn * T::BN;
+  const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a + m0 * a_words, (uint32_t)(rows_here * a_words * 4));
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      make_rsrc(w + (int64_t)(n0 / 128) * kb * 4096, (uint32_t)((T::BN / 128) * kb * 16384));
+  v16i acc[T::TM][T::TN];
+  dma_mainloop<T>(a_rsrc, a_words * 4, b_rsrc, kb, lds, acc);
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+  const int h = lane >> 5, lr = lane & 31;
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    const int64_t m = m0 + wm * T::WM + 32 * i + lr;
+    if (m >= M) continue;
+    const float asv = as[m];
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
+        const float4 wsv = *reinterpret_cast<const float4*>(ws + n);
+        uint32_t v0 = g1_value(acc[i][j][4 * q + 0], wsv.x, asv);
+        uint32_t v1 = g1_value(acc[i][j][4 * q + 1], wsv.y, asv);
+        uint32_t v2 = g1_value(acc[i][j][4 * q + 2], wsv.z, asv);
+        uint32_t v3 = g1_value(acc[i][j][4 * q + 3], wsv.w, asv);
+        uint2* dst = reinterpret_cast<uint2*>(out + m * N + n);
+        if (RESID) {
+          const uint2 r = *reinterpret_cast<const uint2*>(residual + m * N + n);
+          v0 = add_residual(v0, r.x & 0xffffu);
+          v1 = add_residual(v1, r.x >> 16);
+          v2 = add_residual(v2, r.y & 0xffffu);
+          v3 = add_residual(v3, r.y >> 16);
+        }
+        *dst = make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
+      }
+    }
+  }
+}
+
+template <class T, bool RESID>
+hipError_t launch_dma(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
+                      const float* ws, int64_t m, int n, int k, const uint16_t* residual,
+                      uint16_t* out, hipStream_t stream) {
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_kernel<T, RESID>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const int tiles_n = n / T::BN;
+  const int64_t tiles_m = (m + T::BM - 1) / T::BM;
+  const int64_t blocks = tiles_m * tiles_n;
+  gemm_dma_kernel<T, RESID><<<(unsigned)blocks, T::THREADS, T::LDS_BYTES, stream>>>(
+      a, a_words, as, w, ws, m, n, k / 256, residual, out, (int)tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_dma_any(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
+                          const float* ws, int64_t m, int n, int k, const uint16_t* residual,
+                          uint16_t* out, hipStream_t stream) {
+  if (residual) return launch_dma<T, true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return launch_dma<T, false>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+}
+
+using Dma256x256 = DmaTile<128, 128, 2, 2>;
+using Dma256x128 = DmaTile<128, 64, 2, 2>;
+using Dma128x128 = DmaTile<64, 64, 2, 2>;
+using Dma256x256NoHint = DmaTile<128, 128, 2, 2, false>;
+using Dma128x128NoHint = DmaTile<64, 64, 2, 2, false>;
+using Dma256x256W8 = DmaTile<128, 64, 2, 4, false>;
+using Dma256x256W8b = DmaTile<64, 128, 4, 2, false>;
+using Dma256x256W8Hint = DmaTile<128, 64, 2, 4, true>;
 
 template <class T, bool RESID>
 hipError_t launch_dense(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
@@ -215,18 +320,29 @@ __global__ __launch_bounds__(256) void expert_i4_kernel(
 
 }  // namespace
 
-int gemm_config_count() { return 4; }
+int gemm_config_count() { return 12; }
 
 hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
                           const float* ws, int64_t m, int n, int k, const uint16_t* residual,
                           uint16_t* out, int config, hipStream_t stream) {
-  if (config < 0) config = (n % 256 == 0 && m >= 2048) ? 2 : (m >= 256 ? 1 : 0);
-  if (config == 2 && n % 256 != 0) config = 1;
+  if (config < 0) config = (n % 256 == 0 && m >= 1024) ? 9 : 6;
+  // Configurations with a 256-wide N tile need n % 256 == 0; the others
+  // (N tile 128) take any n % 128 == 0.
+  const bool wide_n = config == 2 || config == 4 || config == 7 || config >= 9;
+  if (wide_n && n % 256 != 0) config = 5;
   switch (config) {
     case 0: return launch_dense_any<Tile128x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case 1: return launch_dense_any<Tile256x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case 2: return launch_dense_any<Tile128x256>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case 3: return launch_dense_any<Tile64x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 4: return launch_dma_any<Dma256x256>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 5: return launch_dma_any<Dma256x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 6: return launch_dma_any<Dma128x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 7: return launch_dma_any<Dma256x256NoHint>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 8: return launch_dma_any<Dma128x128NoHint>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 9: return launch_dma_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 10: return launch_dma_any<Dma256x256W8b>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 11: return launch_dma_any<Dma256x256W8Hint>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     default: return hipErrorInvalidValue;
   }
 }
