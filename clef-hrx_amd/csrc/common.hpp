@@ -14,18 +14,23 @@ typedef unsigned u4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float as_float(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t as_uint(float f) { return __float_as_uint(f); }
 
-// f32 -> bf16 round-to-nearest-even; a NaN stays a quiet NaN.
-// kernels/common.loom:29-35 (scalar.fptrunc f32 to bf16).
-__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  uint32_t u = as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// f32 -> bf16 round-to-nearest-even; a NaN stays a quiet NaN with its sign and
+// top payload bits ((u >> 16) | 0x40). kernels/common.loom:29-35
+// (scalar.fptrunc f32 to bf16). gfx950's v_cvt_pk_bf16_f32 computes exactly
+// this for every f32 bit pattern (checked exhaustively on the device), so the
+// conversion is one instruction per pair.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) { return pack_bf16x2(f, 0.0f) & 0xffffu; }
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return as_float(h << 16); }
 __device__ __forceinline__ float bf16_lo(uint32_t pair) { return as_float(pair << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t pair) { return as_float(pair & 0xffff0000u); }
-__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+__device__ __forceinline__ float bf16_round(float f) { return as_float(pack_bf16x2(0.0f, f) & 0xffff0000u); }
 
 // exp(x) by Cody-Waite reduction with ln 2 split as 0.693359375 - 2.12194440e-4
 // and the degree-5 minimax polynomial of the Cephes expf (S. L. Moshier, Cephes

@@ -90,6 +90,111 @@ __global__ __launch_bounds__(256) void gemm_i4_kernel(
   }
 }
 
+// G1 epilogue for the 32x32 MFMA layout (lane: row m = l % 32; register r:
+// column 8(r/4) + 4(l/32) + r%4).
+//
+// Fast path, taken when the whole wave qualifies: acc = 256 * dot exactly, so
+// f32(acc) * (ws * 2^-8) rounds exactly like f32(dot) * ws whenever ws * 2^-8
+// is exact (every scale the quantizer produces; checked per column), and the
+// bf16-range clamp cannot fire when 98 * K * max|ws| * max|as| < bf16 max
+// (infinite or NaN scales pass through the clamp unchanged in the reference
+// too). Otherwise the general path runs the reference sequence step by step.
+template <class T, bool RESID>
+__device__ __forceinline__ void dense_epilogue(const v16i (&acc)[T::TM][T::TN], const float* __restrict__ as,
+                                               const float* __restrict__ ws, int64_t M, int N, int K,
+                                               int64_t m0, int n0, const uint16_t* __restrict__ residual,
+                                               uint16_t* __restrict__ out) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+  const int h = lane >> 5, lr = lane & 31;
+  const float inf = __builtin_huge_valf();
+
+  float asr[T::TM];
+  float mas = 0.0f;
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    const int64_t m = m0 + wm * T::WM + 32 * i + lr;
+    asr[i] = m < M ? as[m] : 0.0f;
+    const float a = __builtin_fabsf(asr[i]);
+    mas = __builtin_fmaxf(mas, a < inf ? a : 0.0f);
+  }
+  float4 wsr[T::TN][4];
+  float mws = 0.0f;
+  bool exact = true;
+#pragma unroll
+  for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
+      wsr[j][q] = *reinterpret_cast<const float4*>(ws + n);
+      const float w4[4] = {wsr[j][q].x, wsr[j][q].y, wsr[j][q].z, wsr[j][q].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        exact = exact && (w4[e] * 0.00390625f) * 256.0f == w4[e];
+        const float a = __builtin_fabsf(w4[e]);
+        mws = __builtin_fmaxf(mws, a < inf ? a : 0.0f);
+      }
+    }
+  const bool fast = __all(exact && mws * mas * (98.0f * (float)K) < kBf16Max);
+
+  if (fast) {
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i) {
+      const int64_t m = m0 + wm * T::WM + 32 * i + lr;
+      if (m >= M) continue;
+      const float asv = asr[i];
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
+          const float w4[4] = {wsr[j][q].x, wsr[j][q].y, wsr[j][q].z, wsr[j][q].w};
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            y[e] = (float)acc[i][j][4 * q + e] * (w4[e] * 0.00390625f);
+            y[e] = y[e] * asv;
+            y[e] = y[e] + 0.0f;
+          }
+          uint32_t p0 = pack_bf16x2(y[0], y[1]), p1 = pack_bf16x2(y[2], y[3]);
+          if (RESID) {
+            const uint2 r = *reinterpret_cast<const uint2*>(residual + m * N + n);
+            p0 = pack_bf16x2(bf16_lo(r.x) + bf16_lo(p0), bf16_hi(r.x) + bf16_hi(p0));
+            p1 = pack_bf16x2(bf16_lo(r.y) + bf16_lo(p1), bf16_hi(r.y) + bf16_hi(p1));
+          }
+          *reinterpret_cast<uint2*>(out + m * N + n) = make_uint2(p0, p1);
+        }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    const int64_t m = m0 + wm * T::WM + 32 * i + lr;
+    if (m >= M) continue;
+    const float asv = asr[i];
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
+        const float4 wsv = wsr[j][q];
+        uint32_t v0 = g1_value(acc[i][j][4 * q + 0], wsv.x, asv);
+        uint32_t v1 = g1_value(acc[i][j][4 * q + 1], wsv.y, asv);
+        uint32_t v2 = g1_value(acc[i][j][4 * q + 2], wsv.z, asv);
+        uint32_t v3 = g1_value(acc[i][j][4 * q + 3], wsv.w, asv);
+        if (RESID) {
+          const uint2 r = *reinterpret_cast<const uint2*>(residual + m * N + n);
+          v0 = add_residual(v0, r.x & 0xffffu);
+          v1 = add_residual(v1, r.x >> 16);
+          v2 = add_residual(v2, r.y & 0xffffu);
+          v3 = add_residual(v3, r.y >> 16);
+        }
+        *reinterpret_cast<uint2*>(out + m * N + n) = make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
+      }
+  }
+}
+
 // Block -> output tile. Workgroups are dispatched round-robin over the 8
 // XCDs (block b runs on XCD b % 8), so block b is renumbered to make each
 // XCD's blocks consecutive, then the renumbered order walks 8-tile-tall
@@ -113,7 +218,6 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dma_kernel(
     const uint32_t* __restrict__ w, const float* __restrict__ ws, int64_t M, int N, int kb,
     const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
   extern __shared__ __align__(16) char lds[];
-  const int tid = threadIdx.x;
   int64_t tm;
   int tn;
   tile_of_block(blockIdx.x, (int64_t)gridDim.x, tiles_m, tiles_n, tm, tn);
@@ -125,37 +229,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dma_kernel(
       make_rsrc(w + (int64_t)(n0 / 128) * kb * 4096, (uint32_t)((T::BN / 128) * kb * 16384));
   v16i acc[T::TM][T::TN];
   dma_mainloop<T>(a_rsrc, a_words * 4, b_rsrc, kb, lds, acc);
-
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
-  const int h = lane >> 5, lr = lane & 31;
-#pragma unroll
-  for (int i = 0; i < T::TM; ++i) {
-    const int64_t m = m0 + wm * T::WM + 32 * i + lr;
-    if (m >= M) continue;
-    const float asv = as[m];
-#pragma unroll
-    for (int j = 0; j < T::TN; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
-        const float4 wsv = *reinterpret_cast<const float4*>(ws + n);
-        uint32_t v0 = g1_value(acc[i][j][4 * q + 0], wsv.x, asv);
-        uint32_t v1 = g1_value(acc[i][j][4 * q + 1], wsv.y, asv);
-        uint32_t v2 = g1_value(acc[i][j][4 * q + 2], wsv.z, asv);
-        uint32_t v3 = g1_value(acc[i][j][4 * q + 3], wsv.w, asv);
-        uint2* dst = reinterpret_cast<uint2*>(out + m * N + n);
-        if (RESID) {
-          const uint2 r = *reinterpret_cast<const uint2*>(residual + m * N + n);
-          v0 = add_residual(v0, r.x & 0xffffu);
-          v1 = add_residual(v1, r.x >> 16);
-          v2 = add_residual(v2, r.y & 0xffffu);
-          v3 = add_residual(v3, r.y >> 16);
-        }
-        *dst = make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
-      }
-    }
-  }
+  dense_epilogue<T, RESID>(acc, as, ws, M, N, kb * 256, m0, n0, residual, out);
 }
 
 template <class T, bool RESID>

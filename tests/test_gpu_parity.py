@@ -236,6 +236,36 @@ def test_gemm_extreme_codes_and_saturation():
         assert_same_u16(bf16_host(got), want, f"extreme config={cfg}")
 
 
+def assert_same_bf16_nan_aware(got: np.ndarray, want: np.ndarray, what: str):
+    """Bit-exact, except that any NaN equals any NaN: a NaN made by 0 * inf
+    carries the sign bit of the machine's default NaN (0x7fc00000 on the GPU,
+    0xffc00000 on x86), which the reference does not specify."""
+    gn = (got & 0x7FFF) > 0x7F80
+    wn = (want & 0x7FFF) > 0x7F80
+    assert np.array_equal(gn, wn), f"{what}: NaN positions differ"
+    assert_same_u16(np.where(gn, 0, got), np.where(wn, 0, want), what)
+
+
+def test_gemm_nan_and_inf_activation_rows():
+    """NaN/Inf rows quantize to zero codes with scale +inf
+    (kernels/prepare_integer_single.loom:251-271) and stay observable through
+    the GEMM (kernels/gemm_integer.loom:411-418)."""
+    n, k = 256, 1024
+    rng = np.random.default_rng(21)
+    x = np.concatenate([randn_bf16(rng, (40, k)), exceptional_rows(k)])
+    w = randn_bf16(rng, (n, k), std=0.02)
+    stride = oracle.activation_stride(k)
+    a_codes, a_scales, _ = oracle.prepare(x, stride)
+    w_tiled, w_scales = oracle.pack_weight(w)
+    want = oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k)
+    assert ((want[40] & 0x7FFF) > 0x7F80).all(), "NaN row must give NaN outputs"
+    a = dev_prepared(x, stride)
+    qw = dev_weight(w_tiled, w_scales, n, k)
+    for cfg in range(clef_i4.gemm_configs()):
+        got = clef_i4.project_prepared(a, qw, config=cfg)
+        assert_same_bf16_nan_aware(bf16_host(got), want, f"nan rows config={cfg}")
+
+
 def test_identity_weight_reproduces_input():
     """activation_scratch_is_bounded (src/quantized.rs:880-915): a 256x256
     identity weight maps a constant row to itself exactly."""
