@@ -10,6 +10,7 @@
 // out[route][c] = bf16(RN(f32(acc) * RN(as[xr] * ws[e*n + c]))), no clamp.
 #include "gemm_core.hpp"
 #include "gemm_dma.hpp"
+#include "gemm_persist.hpp"
 #include "kernels.hpp"
 
 namespace clef {
@@ -93,19 +94,27 @@ __global__ __launch_bounds__(256) void gemm_i4_kernel(
 // G1 epilogue for the 32x32 MFMA layout (lane: row m = l % 32; register r:
 // column 8(r/4) + 4(l/32) + r%4).
 //
-// Fast path, taken when the whole wave qualifies: acc = 256 * dot exactly, so
-// f32(acc) * (ws * 2^-8) rounds exactly like f32(dot) * ws whenever ws * 2^-8
-// is exact (every scale the quantizer produces; checked per column), and the
-// bf16-range clamp cannot fire when 98 * K * max|ws| * max|as| < bf16 max
-// (infinite or NaN scales pass through the clamp unchanged in the reference
-// too). Otherwise the general path runs the reference sequence step by step.
+// Values: fast path, taken when the whole wave qualifies: acc = 256 * dot
+// exactly, so f32(acc) * (ws * 2^-8) rounds exactly like f32(dot) * ws
+// whenever ws * 2^-8 is exact (every scale the quantizer produces; checked
+// per column), and the bf16-range clamp cannot fire when
+// 98 * K * max|ws| * max|as| < bf16 max (infinite or NaN scales pass the clamp
+// unchanged in the reference too). Otherwise the general path runs the
+// reference sequence step by step.
+//
+// Stores: each wave stages its WM x WN bf16 tile in LDS (free after the main
+// loop; 8-byte blocks XOR-swizzled by row) and writes it back as 16-byte row
+// chunks, 8 lanes per 128-byte line; the residual is added on that pass.
 template <class T, bool RESID>
 __device__ __forceinline__ void dense_epilogue(const v16i (&acc)[T::TM][T::TN], const float* __restrict__ as,
                                                const float* __restrict__ ws, int64_t M, int N, int K,
                                                int64_t m0, int n0, const uint16_t* __restrict__ residual,
-                                               uint16_t* __restrict__ out) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+                                               uint16_t* __restrict__ out, char* lds) {
+  static_assert(T::WN >= 64 && T::NW * T::WM * T::WN * 2 <= T::LDS_BYTES, "LDS staging of the output tile");
+  constexpr int RP = T::WN * 2;        // staged row pitch, bytes
+  constexpr int LPR = T::WN / 8;       // lanes per row on the store pass
+  constexpr int RPP = 64 / LPR;        // rows per store pass
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
   const int h = lane >> 5, lr = lane & 31;
   const float inf = __builtin_huge_valf();
@@ -138,18 +147,25 @@ __device__ __forceinline__ void dense_epilogue(const v16i (&acc)[T::TM][T::TN], 
     }
   const bool fast = __all(exact && mws * mas * (98.0f * (float)K) < kBf16Max);
 
-  if (fast) {
+  // All waves are done reading the pipeline stages before LDS is reused.
+  __syncthreads();
+  char* tile = lds + wave * (T::WM * T::WN * 2);
+  auto stage = [&](int row, int col, uint32_t p0, uint32_t p1) {
+    const int blk = (col >> 2) ^ (row & 15);
+    *reinterpret_cast<uint2*>(tile + row * RP + blk * 8) = make_uint2(p0, p1);
+  };
 #pragma unroll
-    for (int i = 0; i < T::TM; ++i) {
-      const int64_t m = m0 + wm * T::WM + 32 * i + lr;
-      if (m >= M) continue;
-      const float asv = asr[i];
+  for (int i = 0; i < T::TM; ++i) {
+    const float asv = asr[i];
 #pragma unroll
-      for (int j = 0; j < T::TN; ++j)
+    for (int j = 0; j < T::TN; ++j)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int n = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
-          const float w4[4] = {wsr[j][q].x, wsr[j][q].y, wsr[j][q].z, wsr[j][q].w};
+      for (int q = 0; q < 4; ++q) {
+        const int row = 32 * i + lr, col = 32 * j + 8 * q + 4 * h;
+        const float4 wsv = wsr[j][q];
+        uint32_t p0, p1;
+        if (fast) {
+          const float w4[4] = {wsv.x, wsv.y, wsv.z, wsv.w};
           float y[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -157,41 +173,37 @@ __device__ __forceinline__ void dense_epilogue(const v16i (&acc)[T::TM][T::TN], 
             y[e] = y[e] * asv;
             y[e] = y[e] + 0.0f;
           }
-          uint32_t p0 = pack_bf16x2(y[0], y[1]), p1 = pack_bf16x2(y[2], y[3]);
-          if (RESID) {
-            const uint2 r = *reinterpret_cast<const uint2*>(residual + m * N + n);
-            p0 = pack_bf16x2(bf16_lo(r.x) + bf16_lo(p0), bf16_hi(r.x) + bf16_hi(p0));
-            p1 = pack_bf16x2(bf16_lo(r.y) + bf16_lo(p1), bf16_hi(r.y) + bf16_hi(p1));
-          }
-          *reinterpret_cast<uint2*>(out + m * N + n) = make_uint2(p0, p1);
+          p0 = pack_bf16x2(y[0], y[1]);
+          p1 = pack_bf16x2(y[2], y[3]);
+        } else {
+          p0 = g1_value(acc[i][j][4 * q + 0], wsv.x, asv) | (g1_value(acc[i][j][4 * q + 1], wsv.y, asv) << 16);
+          p1 = g1_value(acc[i][j][4 * q + 2], wsv.z, asv) | (g1_value(acc[i][j][4 * q + 3], wsv.w, asv) << 16);
         }
-    }
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < T::TM; ++i) {
-    const int64_t m = m0 + wm * T::WM + 32 * i + lr;
-    if (m >= M) continue;
-    const float asv = asr[i];
-#pragma unroll
-    for (int j = 0; j < T::TN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
-        const float4 wsv = wsr[j][q];
-        uint32_t v0 = g1_value(acc[i][j][4 * q + 0], wsv.x, asv);
-        uint32_t v1 = g1_value(acc[i][j][4 * q + 1], wsv.y, asv);
-        uint32_t v2 = g1_value(acc[i][j][4 * q + 2], wsv.z, asv);
-        uint32_t v3 = g1_value(acc[i][j][4 * q + 3], wsv.w, asv);
-        if (RESID) {
-          const uint2 r = *reinterpret_cast<const uint2*>(residual + m * N + n);
-          v0 = add_residual(v0, r.x & 0xffffu);
-          v1 = add_residual(v1, r.x >> 16);
-          v2 = add_residual(v2, r.y & 0xffffu);
-          v3 = add_residual(v3, r.y >> 16);
-        }
-        *reinterpret_cast<uint2*>(out + m * N + n) = make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
+        stage(row, col, p0, p1);
       }
+  }
+  // Each wave reads back only its own region; the LDS ops of a wave complete
+  // in order, so no barrier is needed between the two phases.
+  const int c = lane % LPR;
+#pragma unroll
+  for (int pass = 0; pass < T::WM / RPP; ++pass) {
+    const int row = RPP * pass + lane / LPR;
+    const int x = row & 15;
+    uint4 v = *reinterpret_cast<const uint4*>(tile + row * RP + ((c ^ (x >> 1)) << 4));
+    if (x & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+    const int64_t m = m0 + wm * T::WM + row;
+    if (m >= M) continue;
+    const int64_t at = m * N + n0 + wn * T::WN + 8 * c;
+    if (RESID) {
+      const uint4 r = *reinterpret_cast<const uint4*>(residual + at);
+      const uint32_t rv[4] = {r.x, r.y, r.z, r.w};
+      uint32_t ov[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        ov[t] = pack_bf16x2(bf16_lo(rv[t]) + bf16_lo(ov[t]), bf16_hi(rv[t]) + bf16_hi(ov[t]));
+      v = make_uint4(ov[0], ov[1], ov[2], ov[3]);
+    }
+    *reinterpret_cast<uint4*>(out + at) = v;
   }
 }
 
@@ -217,6 +229,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dma_kernel(
     const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
     const uint32_t* __restrict__ w, const float* __restrict__ ws, int64_t M, int N, int kb,
     const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
+#if defined(__HIP_DEVICE_COMPILE__)  // buffer-resource builtins exist only in the device pass
   extern __shared__ __align__(16) char lds[];
   int64_t tm;
   int tn;
@@ -228,8 +241,168 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dma_kernel(
   const __amdgpu_buffer_rsrc_t b_rsrc =
       make_rsrc(w + (int64_t)(n0 / 128) * kb * 4096, (uint32_t)((T::BN / 128) * kb * 16384));
   v16i acc[T::TM][T::TN];
-  dma_mainloop<T>(a_rsrc, a_words * 4, b_rsrc, kb, lds, acc);
-  dense_epilogue<T, RESID>(acc, as, ws, M, N, kb * 256, m0, n0, residual, out);
+  int voff_a[T::A_INST];
+  {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int ql = 0; ql < T::A_INST; ++ql) voff_a[ql] = (lane >> 3) * a_words * 4 + dma_chunk16(wave, lane);
+  }
+  dma_mainloop<T>(a_rsrc, voff_a, a_words * 4, b_rsrc, kb, lds, acc);
+  dense_epilogue<T, RESID>(acc, as, ws, M, N, kb * 256, m0, n0, residual, out, lds);
+#endif
+}
+
+// G1 epilogue of the persistent kernel: same values as dense_epilogue, stored
+// straight from the accumulators with exactly TM * TN * 4 buffer stores per
+// wave (rows past M fall outside the output range and are dropped), so the
+// next tile's k-step 0 can wait on its own DMA only.
+template <class T, bool RESID>
+__device__ __forceinline__ void direct_epilogue(const v16i (&acc)[T::TM][T::TN], const float* __restrict__ as,
+                                                const float* __restrict__ ws, int64_t M, int N, int K,
+                                                int64_t m0, int n0, const uint16_t* __restrict__ residual,
+                                                uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+  const int h = lane >> 5, lr = lane & 31;
+  const float inf = __builtin_huge_valf();
+  const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
+  const __amdgpu_buffer_rsrc_t out_rsrc = make_rsrc(out + m0 * N, (uint32_t)(rows_here * N * 2));
+  const __amdgpu_buffer_rsrc_t res_rsrc =
+      make_rsrc(RESID ? residual + m0 * N : out, RESID ? (uint32_t)(rows_here * N * 2) : 0u);
+
+  float asr[T::TM];
+  float mas = 0.0f;
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    const int64_t m = m0 + wm * T::WM + 32 * i + lr;
+    asr[i] = m < M ? as[m] : 0.0f;
+    const float a = __builtin_fabsf(asr[i]);
+    mas = __builtin_fmaxf(mas, a < inf ? a : 0.0f);
+  }
+  float mws = 0.0f;
+  bool exact = true;
+#pragma unroll
+  for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
+      const float4 w = *reinterpret_cast<const float4*>(ws + n);
+      const float w4[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        exact = exact && (w4[e] * 0.00390625f) * 256.0f == w4[e];
+        const float a = __builtin_fabsf(w4[e]);
+        mws = __builtin_fmaxf(mws, a < inf ? a : 0.0f);
+      }
+    }
+  const bool fast = __all(exact && mws * mas * (98.0f * (float)K) < kBf16Max);
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    const float asv = asr[i];
+    const int row = wm * T::WM + 32 * i + lr;
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
+        const int off = (row * N + col) * 2;
+        const float4 wsv = *reinterpret_cast<const float4*>(ws + col);
+        uint32_t p0, p1;
+        if (fast) {
+          const float w4[4] = {wsv.x, wsv.y, wsv.z, wsv.w};
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            y[e] = (float)acc[i][j][4 * q + e] * (w4[e] * 0.00390625f);
+            y[e] = y[e] * asv;
+            y[e] = y[e] + 0.0f;
+          }
+          p0 = pack_bf16x2(y[0], y[1]);
+          p1 = pack_bf16x2(y[2], y[3]);
+        } else {
+          p0 = g1_value(acc[i][j][4 * q + 0], wsv.x, asv) | (g1_value(acc[i][j][4 * q + 1], wsv.y, asv) << 16);
+          p1 = g1_value(acc[i][j][4 * q + 2], wsv.z, asv) | (g1_value(acc[i][j][4 * q + 3], wsv.w, asv) << 16);
+        }
+        if (RESID) {
+          const v2i r = __builtin_amdgcn_raw_buffer_load_b64(res_rsrc, off, 0, 0);
+          p0 = pack_bf16x2(bf16_lo((uint32_t)r.x) + bf16_lo(p0), bf16_hi((uint32_t)r.x) + bf16_hi(p0));
+          p1 = pack_bf16x2(bf16_lo((uint32_t)r.y) + bf16_lo(p1), bf16_hi((uint32_t)r.y) + bf16_hi(p1));
+        }
+        __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)p0, (int)p1}, out_rsrc, off, 0, 0);
+      }
+  }
+}
+
+template <class T, bool RESID>
+__global__ __launch_bounds__(T::THREADS) void gemm_persistent_kernel(
+    const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
+    const uint32_t* __restrict__ w, const float* __restrict__ ws, int64_t M, int N, int kb,
+    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
+#if defined(__HIP_DEVICE_COMPILE__)  // buffer-resource builtins exist only in the device pass
+  extern __shared__ __align__(16) char lds[];
+  const int total = tiles_m * tiles_n;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  auto get = [&](int t) {
+    TileRsrc ta;
+    int64_t tm;
+    int tn;
+    tile_of_block(t, total, tiles_m, tiles_n, tm, tn);
+    const int64_t m0 = tm * T::BM;
+    const int n0 = tn * T::BN;
+    const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
+    ta.a_rsrc = make_rsrc(a + m0 * a_words, (uint32_t)(rows_here * a_words * 4));
+    ta.b_rsrc = make_rsrc(w + (int64_t)(n0 / 128) * kb * 4096, (uint32_t)((T::BN / 128) * kb * 16384));
+    return ta;
+  };
+  auto epi = [&](int t, const v16i (&acc)[T::TM][T::TN]) {
+    int64_t tm;
+    int tn;
+    tile_of_block(t, total, tiles_m, tiles_n, tm, tn);
+    direct_epilogue<T, RESID>(acc, as, ws, M, N, kb * 256, tm * T::BM, tn * T::BN, residual, out);
+  };
+  const int voff = (lane >> 3) * a_words * 4 + dma_chunk16(wave, lane);
+  persistent_loop<T, T::TM * T::TN * 4, TileRsrc>(blockIdx.x, gridDim.x, total, kb, voff, a_words * 4, lds, get,
+                                                  epi);
+#endif
+}
+
+template <class T, bool RESID>
+hipError_t launch_persistent(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
+                             const float* ws, int64_t m, int n, int k, const uint16_t* residual,
+                             uint16_t* out, int per_cu, hipStream_t stream) {
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_persistent_kernel<T, RESID>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+  }
+  const int tiles_n = n / T::BN;
+  const int64_t tiles_m = (m + T::BM - 1) / T::BM;
+  const int64_t total = tiles_m * tiles_n;
+  int64_t grid = (int64_t)cus * per_cu;
+  grid = grid / 8 * 8;
+  if (grid > total) grid = total;
+  gemm_persistent_kernel<T, RESID><<<(unsigned)grid, T::THREADS, T::LDS_BYTES, stream>>>(
+      a, a_words, as, w, ws, m, n, k / 256, residual, out, (int)tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_persistent_any(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
+                                 const float* ws, int64_t m, int n, int k, const uint16_t* residual,
+                                 uint16_t* out, int per_cu, hipStream_t stream) {
+  if (residual)
+    return launch_persistent<T, true>(a, a_words, as, w, ws, m, n, k, residual, out, per_cu, stream);
+  return launch_persistent<T, false>(a, a_words, as, w, ws, m, n, k, residual, out, per_cu, stream);
 }
 
 template <class T, bool RESID>
@@ -392,9 +565,87 @@ __global__ __launch_bounds__(256) void expert_i4_kernel(
   }
 }
 
+// E1 on the DMA core: rows gathered through the expert's route list.
+// Slots past the expert's count get an out-of-range offset (2^31 >= the
+// buffer size, checked by the launcher) and read zeros; they are not stored.
+template <class T>
+__global__ __launch_bounds__(T::THREADS) void expert_dma_kernel(
+    const uint32_t* __restrict__ a, int a_words, uint32_t a_bytes, const float* __restrict__ as,
+    const uint32_t* __restrict__ w, const float* __restrict__ ws, const float* __restrict__ groups,
+    const int32_t* __restrict__ schedule, int64_t tokens, int topk, int kb, int n, int input_routed,
+    uint16_t* __restrict__ out, int tiles_n) {
+#if defined(__HIP_DEVICE_COMPILE__)  // buffer-resource builtins exist only in the device pass
+  extern __shared__ __align__(16) char lds[];
+  // Work items are (tile, column block) pairs in expert-major order. Block b
+  // runs on XCD b % 8 (round-robin dispatch); XCD x takes the contiguous item
+  // range [x * C, (x + 1) * C), so the row tiles of one expert and weight
+  // panel run together on one XCD and share the panel in its L2. The grid is
+  // a multiple of 8 and covers 8 * C items.
+  const int64_t items = (int64_t)schedule[0] * tiles_n;
+  const int64_t chunk = (items + 7) / 8;
+  const int64_t local = blockIdx.x / 8;
+  if (local >= chunk) return;
+  const int64_t item = (blockIdx.x % 8) * chunk + local;
+  if (item >= items) return;
+  const int tile = (int)(item / tiles_n);
+  const int tn = (int)(item - (int64_t)tile * tiles_n);
+  const int e = schedule[1 + 2 * tile];
+  const int row0 = schedule[2 + 2 * tile];
+  const float* list = groups + (int64_t)e * (tokens + 1);
+  const int count = (int)list[0];
+  const int n0 = tn * T::BN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  int voff_a[T::A_INST];
+#pragma unroll
+  for (int ql = 0; ql < T::A_INST; ++ql) {
+    const int slot = row0 + 8 * (wave + T::NW * ql) + (lane >> 3);
+    if (slot < count) {
+      const int64_t route = (int64_t)list[1 + slot];
+      const int64_t xr = input_routed ? route : route / topk;
+      voff_a[ql] = (int)(xr * a_words * 4) + dma_chunk16(wave, lane);
+    } else {
+      voff_a[ql] = (int)0x80000000u;
+    }
+  }
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a, a_bytes);
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      make_rsrc(w + (((int64_t)e * n + n0) / 128) * kb * 4096, (uint32_t)((T::BN / 128) * kb * 16384));
+  v16i acc[T::TM][T::TN];
+  dma_mainloop<T>(a_rsrc, voff_a, 0, b_rsrc, kb, lds, acc);
+
+  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+  const int h = lane >> 5, lr = lane & 31;
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    const int slot = row0 + wm * T::WM + 32 * i + lr;
+    if (slot >= count) continue;
+    const int64_t route = (int64_t)list[1 + slot];
+    const int64_t xr = input_routed ? route : route / topk;
+    const float asv = as[xr];
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
+        const float4 wsv = *reinterpret_cast<const float4*>(ws + (int64_t)e * n + c);
+        const float y0 = (float)(acc[i][j][4 * q + 0] >> 8) * (asv * wsv.x);
+        const float y1 = (float)(acc[i][j][4 * q + 1] >> 8) * (asv * wsv.y);
+        const float y2 = (float)(acc[i][j][4 * q + 2] >> 8) * (asv * wsv.z);
+        const float y3 = (float)(acc[i][j][4 * q + 3] >> 8) * (asv * wsv.w);
+        *reinterpret_cast<uint2*>(out + route * n + c) = make_uint2(pack_bf16x2(y0, y1), pack_bf16x2(y2, y3));
+      }
+  }
+#endif
+}
+
+using ExpertDmaTile = DmaTile<64, 64, 2, 2>;
+static_assert(ExpertDmaTile::BM == kExpertBM, "expert schedule tile height");
+
 }  // namespace
 
-int gemm_config_count() { return 12; }
+int gemm_config_count() { return 14; }
 
 hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
                           const float* ws, int64_t m, int n, int k, const uint16_t* residual,
@@ -402,7 +653,9 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
   if (config < 0) config = (n % 256 == 0 && m >= 1024) ? 9 : 6;
   // Configurations with a 256-wide N tile need n % 256 == 0; the others
   // (N tile 128) take any n % 128 == 0.
-  const bool wide_n = config == 2 || config == 4 || config == 7 || config >= 9;
+  const bool wide_n = config == 2 || config == 4 || config == 7 || (config >= 9 && config <= 12);
+  // The persistent loop needs at least two k-steps.
+  if (k < 512 && config >= 12) config = config == 12 ? 9 : 6;
   if (wide_n && n % 256 != 0) config = 5;
   switch (config) {
     case 0: return launch_dense_any<Tile128x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
@@ -417,6 +670,8 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
     case 9: return launch_dma_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case 10: return launch_dma_any<Dma256x256W8b>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case 11: return launch_dma_any<Dma256x256W8Hint>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 12: return launch_persistent_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, 1, stream);
+    case 13: return launch_persistent_any<Dma128x128>(a, a_words, as, w, ws, m, n, k, residual, out, 2, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -442,6 +697,25 @@ hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* as, con
                             const float* ws, const float* groups, const int32_t* schedule,
                             int64_t tokens, int topk, int k, int n, int input_routed, uint16_t* out,
                             hipStream_t stream) {
+  const int64_t a_rows = input_routed ? tokens * topk : tokens;
+  const int64_t a_bytes = a_rows * a_words * 4;
+  if (a_bytes < ((int64_t)1 << 31)) {
+    using T = ExpertDmaTile;
+    static bool configured = false;
+    if (!configured) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&expert_dma_kernel<T>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
+      if (e != hipSuccess) return e;
+      configured = true;
+    }
+    const int tiles_n = n / T::BN;
+    const int64_t blocks = 8 * ((expert_max_tiles(tokens * topk) * tiles_n + 7) / 8);
+    expert_dma_kernel<T><<<(unsigned)blocks, T::THREADS, T::LDS_BYTES, stream>>>(
+        a, a_words, (uint32_t)a_bytes, as, w, ws, groups, schedule, tokens, topk, k / 256, n, input_routed,
+        out, tiles_n);
+    return hipGetLastError();
+  }
+  // Activation buffers of 2 GiB or more: 64-bit row addressing.
   using T = ExpertTile;
   static bool configured = false;
   if (!configured) {

@@ -37,6 +37,7 @@ namespace clef {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 
 template <int WM_, int WN_, int WAVES_M_, int WAVES_N_, bool HINT_ = true>
 struct DmaTile {
@@ -71,13 +72,29 @@ __device__ __forceinline__ v16i mfma32_i8(v4i a, v4i b, v16i c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
-// a_rsrc covers the workgroup's BM activation rows (row pitch a_row_bytes);
-// b_rsrc covers its BN/128 retile block rows for all k-steps (block (b, kt) at
-// (b * ksteps + kt) * 16 KiB).
+// Logical 16-byte chunk (times 16) that DMA lane `lane` of wave `wave` moves:
+// lane -> tile row r = 8q + lane/8, physical chunk lane%8, which holds logical
+// chunk (lane%8) ^ g(r) with g(r) = (r >> 1) & 7 = ((q & 1) << 2) | (lane >> 4);
+// q & 1 = wave & 1 for every DMA instruction of a wave (q = wave + NW * ql,
+// NW even).
+__device__ __forceinline__ int dma_chunk16(int wave, int lane) {
+  return ((lane & 7) ^ ((((wave & 1) << 2) | (lane >> 4)) & 7)) * 16;
+}
+
+// A-operand DMA addressing: slot ql of wave w covers tile rows 8q .. 8q+7
+// (q = w + NW * ql); voff_a[ql] is the lane's byte offset of its chunk at
+// k-step 0 and the wave-uniform part is 8 * q * a_q_stride + kt * 128.
+// Contiguous rows: a_rsrc starts at the tile's first row, voff_a[ql] =
+// (lane/8) * row_bytes + chunk, a_q_stride = row_bytes. Gathered rows:
+// voff_a[ql] = the lane's row offset in the whole buffer + chunk (or an
+// out-of-range offset, which reads zeros), a_q_stride = 0.
+//
+// b_rsrc covers the tile's BN/128 retile block rows for all k-steps (block
+// (b, kt) at (b * ksteps + kt) * 16 KiB).
 template <class T>
-__device__ __forceinline__ void dma_mainloop(__amdgpu_buffer_rsrc_t a_rsrc, int a_row_bytes,
-                                             __amdgpu_buffer_rsrc_t b_rsrc, int ksteps, char* lds,
-                                             v16i (&acc)[T::TM][T::TN]) {
+__device__ __forceinline__ void dma_mainloop(__amdgpu_buffer_rsrc_t a_rsrc, const int (&voff_a)[T::A_INST],
+                                             int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc, int ksteps,
+                                             char* lds, v16i (&acc)[T::TM][T::TN]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // Wave-uniform by construction; readfirstlane lets the compiler keep the
@@ -91,14 +108,7 @@ __device__ __forceinline__ void dma_mainloop(__amdgpu_buffer_rsrc_t a_rsrc, int 
 #pragma unroll
     for (int j = 0; j < T::TN; ++j) acc[i][j] = v16i{};
 
-  // DMA lane mapping: lane -> row r = 8q + lane/8, physical chunk lane%8,
-  // which holds logical chunk (lane%8) ^ g(r) with g(r) = (r >> 1) & 7
-  // = ((q & 1) << 2) | (lane >> 4); q & 1 = wave & 1 for every DMA
-  // instruction of this wave (q = wave + NW * ql, NW even).
-  const int sub = lane >> 3;
-  const int logical_chunk = (lane & 7) ^ ((((wave & 1) << 2) | (lane >> 4)) & 7);
-  const int voff_a = sub * a_row_bytes + logical_chunk * 16;
-  const int voff_b = sub * 128 + logical_chunk * 16;
+  const int voff_b = (lane >> 3) * 128 + dma_chunk16(wave, lane);
 
   auto issue = [&](int kt, int stage) {
     char* sa = lds + stage * T::STAGE_BYTES;
@@ -106,8 +116,8 @@ __device__ __forceinline__ void dma_mainloop(__amdgpu_buffer_rsrc_t a_rsrc, int 
 #pragma unroll
     for (int ql = 0; ql < T::A_INST; ++ql) {
       const int q = wave + T::NW * ql;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(sa + q * 1024), 16, voff_a,
-                                               8 * q * a_row_bytes + kt * 128, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(sa + q * 1024), 16, voff_a[ql],
+                                               8 * q * a_q_stride + kt * 128, 0, 0);
     }
 #pragma unroll
     for (int ql = 0; ql < T::B_INST; ++ql) {
