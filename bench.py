@@ -30,6 +30,11 @@ sys.path.insert(0, ROOT)
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
 HBM_PEAK_GBS = 8000.0
+# HBM bytes moved per launch of the M4096 K4096 N12288 GEMM kernel: rocprofv3
+# FETCH_SIZE and WRITE_SIZE passes over `bench.py --only gemm`, each scaled by
+# the reading for a plain 512 MiB copy (x2.000 fetch, x1.000 write); the runs
+# and raw readings are in profiles/int4_gemm_m4096_k4096_n12288.txt.
+GEMM_TRAFFIC_BYTES = 269.1e6
 
 
 def parse():
@@ -38,7 +43,9 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--only", choices=["gemm", "moe", "mlp"], default=None)
+    p.add_argument("--only", choices=["gemm", "moe", "mlp", "copy"], default=None,
+                   help="run one leg; 'copy' is a plain 512 MiB device copy, the known-size "
+                        "kernel that scales HBM byte counters")
     return p.parse_args()
 
 
@@ -80,8 +87,10 @@ def gemm_leg(args):
     ms = timed(lambda: clef_i4.project_prepared(a, qw, out=out), args.steps, args.warmup)
     prep_ms = timed(lambda: clef_i4.prepare(x, out=a.storage), args.steps, args.warmup)
     ops = 2.0 * m * n * k
+    # operands read once (codes + f32 scales) and the bf16 output written once
+    nbytes = m * k // 2 + 4 * m + n * k // 2 + 4 * n + 2 * m * n
     return {"m": m, "n": n, "k": k, "ms": ms, "tops": ops / ms / 1e9, "prepare_ms": prep_ms,
-            "ops": ops}
+            "ops": ops, "bytes": nbytes}
 
 
 def mlp_leg(args):
@@ -131,6 +140,19 @@ def moe_leg(args):
     ms = timed(lambda: layer(x, logits, out=out), args.steps, args.warmup)
     ops = 8.0 * t * 2 * (2 * inter * d + d * inter)
     return {"tokens": t, "ms": ms, "tokens_per_s": t / ms * 1e3, "tops": ops / ms / 1e9}
+
+
+def copy_leg(args):
+    """Plain device-to-device copy of 512 MiB: read and written bytes are known
+    exactly, so a counter run over it gives the factor between the FETCH_SIZE /
+    WRITE_SIZE readings and bytes."""
+    import torch
+
+    nbytes = 512 << 20
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    ms = timed(lambda: dst.copy_(src), args.steps, args.warmup)
+    return {"bytes": nbytes, "ms": ms, "gbs": 2 * nbytes / ms / 1e6}
 
 
 def cpu_leg():
@@ -197,6 +219,11 @@ def main():
         res["moe"] = moe_leg(args)
     if args.only in (None, "mlp"):
         res["mlp"] = mlp_leg(args)
+    if args.only == "copy":
+        c = copy_leg(args)
+        print(json.dumps({"copy_bytes": c["bytes"], "copy_ms": round(c["ms"], 4),
+                          "copy_gbs": round(c["gbs"], 1)}))
+        return
     cpu = None if args.no_cpu or args.only else cpu_leg()
 
     g = res.get("gemm")
@@ -222,7 +249,8 @@ def main():
         line["prepare_ms"] = round(g["prepare_ms"], 4)
         line["roofline"] = {"bound": "mfma", "achieved": round(g["tops"], 1), "peak": INT8_PEAK_TOPS,
                             "unit": "TFLOP/s", "frac": round(g["tops"] / INT8_PEAK_TOPS, 4),
-                            "traffic": None}
+                            "traffic": GEMM_TRAFFIC_BYTES,
+                            "algorithmic_bytes": g["bytes"]}
     if "moe" in res:
         line["moe_tokens_per_s"] = round(res["moe"]["tokens_per_s"], 1)
         line["moe_layer_ms"] = round(res["moe"]["ms"], 4)

@@ -178,6 +178,57 @@ class QuantizedWeight:
     bits: int
 
 
+class QuantizedProjections:
+    """Which checkpoint weights the INT4 path packs, and their resident size.
+
+    Mirrors QuantizedProjections::{for_precision, precision, resident_bytes,
+    is_bf16, is_full_int4} (src/quantized.rs:41-62, 104-127) with Precision
+    from src/model.rs:22-29 given as "bf16", "int4_mlp" or "int4".
+    """
+
+    PRECISIONS = ("bf16", "int4_mlp", "int4")
+
+    def __init__(self, bits: int | None = None, backbone_bits: int | None = None,
+                 projections=("up", "gate", "down"), share_packing: bool = False):
+        self.bits = bits
+        self.backbone_bits = backbone_bits
+        self.projections = list(projections)
+        self.share_packing = share_packing
+
+    @classmethod
+    def for_precision(cls, precision: str) -> "QuantizedProjections":
+        if precision not in cls.PRECISIONS:
+            raise ValueError(f"unknown precision {precision!r}")
+        return cls(bits=4 if precision == "int4_mlp" else None,
+                   backbone_bits=4 if precision == "int4" else None,
+                   share_packing=precision != "bf16")
+
+    def is_bf16(self) -> bool:
+        return self.bits is None and self.backbone_bits is None
+
+    def is_full_int4(self) -> bool:
+        return self.bits is None and self.backbone_bits == 4 and self.projections == ["up", "gate", "down"]
+
+    def precision(self, name: str, rows: int, cols: int) -> int | None:
+        """Bits a weight is packed with, or None if it stays bf16."""
+        if not name.startswith("model.language_model.layers.") or not name.endswith(".weight"):
+            return None
+        if ".mlp." in name:
+            if any(name.endswith(f".{p}_proj.weight") for p in self.projections):
+                return self.bits if self.bits is not None else self.backbone_bits
+            return None
+        if rows >= 4096 and cols >= 1024 and rows % 256 == 0 and cols % 256 == 0:
+            return self.backbone_bits
+        return None
+
+    def resident_bytes(self, name: str, rows: int, cols: int) -> int:
+        bits = self.precision(name, rows, cols)
+        if bits is None:
+            return rows * cols * 2
+        # retiled codes carry no stride padding; one f32 scale per row
+        return rows * cols * bits // 8 + rows * 4
+
+
 def load_quantized_weight(w: torch.Tensor, bits: int = 4, tiled_checkpoint: bool = False
                           ) -> QuantizedWeight:
     """Packing half of Engine::load_quantized_weight (src/quantized.rs:147-234)."""

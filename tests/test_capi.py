@@ -133,3 +133,47 @@ def test_moe_layer_rejects():
     rc, msg = call("clef_moe_layer", FAKE, FAKE, 0, 16, 2048, 768, 128, 8, FAKE, FAKE, FAKE, FAKE, FAKE,
                    FAKE, None, FAKE, FAKE, need - 1, None)
     assert rc == -1 and msg == "workspace too small"
+
+
+def test_resident_storage_keeps_scales_and_original_precision_outside_backbone():
+    """resident_storage_keeps_scales_and_original_precision_outside_backbone
+    (src/quantized.rs:782-799)."""
+    packing = clef_i4.QuantizedProjections.for_precision("int4")
+    assert packing.resident_bytes("model.language_model.layers.0.mlp.up_proj.weight", 17408, 5120) == \
+        17408 * 5120 // 2 + 17408 * 4
+    for name in ("model.visual.blocks.0.mlp.up_proj.weight", "head.scorer.weight"):
+        assert packing.resident_bytes(name, 4096, 4096) == 4096 * 4096 * 2
+
+
+@pytest.mark.parametrize("mode,mlp_bits,qkv_bits", [("bf16", None, None), ("int4_mlp", 4, None),
+                                                    ("int4", 4, 4)])
+def test_explicit_precision_selects_only_requested_projections(mode, mlp_bits, qkv_bits):
+    """explicit_precision_selects_only_requested_projections
+    (src/quantized.rs:826-857)."""
+    mlp = "model.language_model.layers.0.mlp.up_proj.weight"
+    qkv = "model.language_model.layers.0.linear_attn.in_proj_qkv.weight"
+    config = clef_i4.QuantizedProjections.for_precision(mode)
+    assert config.is_bf16() == (mode == "bf16")
+    assert config.is_full_int4() == (mode == "int4")
+    assert config.precision(mlp, 17408, 5120) == mlp_bits
+    assert config.precision(qkv, 10240, 5120) == qkv_bits
+    assert config.precision("model.visual.blocks.0.mlp.up_proj.weight", 17408, 5120) is None
+    assert config.precision("joint_head.weight", 5120, 5120) is None
+    assert config.precision("model.language_model.layers.3.self_attn.k_proj.weight", 1024, 5120) is None
+
+
+def test_precision_policy_mlp_projection_subset():
+    """Only the listed MLP projections are packed; other .mlp. weights stay bf16
+    (src/quantized.rs:108-115)."""
+    config = clef_i4.QuantizedProjections(bits=4, projections=("up",))
+    assert config.precision("model.language_model.layers.1.mlp.up_proj.weight", 4096, 4096) == 4
+    assert config.precision("model.language_model.layers.1.mlp.down_proj.weight", 4096, 4096) is None
+    # backbone eligibility needs rows >= 4096, cols >= 1024, both multiples of 256
+    backbone = clef_i4.QuantizedProjections.for_precision("int4")
+    name = "model.language_model.layers.1.self_attn.q_proj.weight"
+    assert backbone.precision(name, 4096, 1024) == 4
+    assert backbone.precision(name, 4096, 768) is None
+    assert backbone.precision(name, 4352, 1280) == 4
+    assert backbone.precision(name, 4100, 1024) is None
+    with pytest.raises(ValueError):
+        clef_i4.QuantizedProjections.for_precision("int8")
