@@ -40,8 +40,11 @@ GEMM_TRAFFIC_BYTES = 269.1e6
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=5)
+    # The board's power management settles within ~0.1 s of sustained MFMA
+    # load (the first ~100 launches run up to 25 % slower); the default warmup
+    # runs well past that so the timed steps measure the sustained rate.
+    p.add_argument("--steps", type=int, default=400)
+    p.add_argument("--warmup", type=int, default=600)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--only", choices=["gemm", "moe", "mlp", "copy"], default=None,
                    help="run one leg; 'copy' is a plain 512 MiB device copy, the known-size "

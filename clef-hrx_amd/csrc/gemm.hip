@@ -11,6 +11,7 @@
 #include "gemm_core.hpp"
 #include "gemm_dma.hpp"
 #include "gemm_persist.hpp"
+#include "gemm_dmah.hpp"
 #include "kernels.hpp"
 
 namespace clef {
@@ -252,6 +253,36 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dma_kernel(
 #endif
 }
 
+// Same contraction on the half-k-step core: 4 waves, 72 KiB of LDS, two
+// workgroups per CU.
+template <class T, bool RESID>
+__global__ __launch_bounds__(T::THREADS, 2) void gemm_dmah_kernel(
+    const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
+    const uint32_t* __restrict__ w, const float* __restrict__ ws, int64_t M, int N, int kb,
+    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  extern __shared__ __align__(16) char lds[];
+  int64_t tm;
+  int tn;
+  tile_of_block(blockIdx.x, (int64_t)gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = tm * T::BM;
+  const int n0 = tn * T::BN;
+  const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a + m0 * a_words, (uint32_t)(rows_here * a_words * 4));
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      make_rsrc(w + (int64_t)(n0 / 128) * kb * 4096, (uint32_t)((T::BN / 128) * kb * 16384));
+  v16i acc[T::TM][T::TN];
+  int voff_a[T::A_INST];
+  {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int ql = 0; ql < T::A_INST; ++ql) voff_a[ql] = (lane >> 2) * a_words * 4 + dmah_chunk16(lane);
+  }
+  dmah_mainloop<T>(a_rsrc, voff_a, a_words * 4, b_rsrc, kb, lds, acc);
+  dense_epilogue<T, RESID>(acc, as, ws, M, N, kb * 256, m0, n0, residual, out, lds);
+#endif
+}
+
 // G1 epilogue of the persistent kernel: same values as dense_epilogue, stored
 // straight from the accumulators with exactly TM * TN * 4 buffer stores per
 // wave (rows past M fall outside the output range and are dropped), so the
@@ -405,22 +436,36 @@ hipError_t launch_persistent_any(const uint32_t* a, int a_words, const float* as
   return launch_persistent<T, false>(a, a_words, as, w, ws, m, n, k, residual, out, per_cu, stream);
 }
 
+template <class T>
+struct IsHalfStage : std::false_type {};
+template <int A, int B, int C, int D, int E>
+struct IsHalfStage<DmaHTile<A, B, C, D, E>> : std::true_type {};
+
 template <class T, bool RESID>
 hipError_t launch_dma(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
                       const float* ws, int64_t m, int n, int k, const uint16_t* residual,
                       uint16_t* out, hipStream_t stream) {
+  constexpr bool H = IsHalfStage<T>::value;
+  const void* kern;
+  if constexpr (H)
+    kern = reinterpret_cast<const void*>(&gemm_dmah_kernel<T, RESID>);
+  else
+    kern = reinterpret_cast<const void*>(&gemm_dma_kernel<T, RESID>);
   static bool configured = false;
   if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_kernel<T, RESID>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
+    hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
     if (e != hipSuccess) return e;
     configured = true;
   }
   const int tiles_n = n / T::BN;
   const int64_t tiles_m = (m + T::BM - 1) / T::BM;
   const int64_t blocks = tiles_m * tiles_n;
-  gemm_dma_kernel<T, RESID><<<(unsigned)blocks, T::THREADS, T::LDS_BYTES, stream>>>(
-      a, a_words, as, w, ws, m, n, k / 256, residual, out, (int)tiles_m, tiles_n);
+  if constexpr (H)
+    gemm_dmah_kernel<T, RESID><<<(unsigned)blocks, T::THREADS, T::LDS_BYTES, stream>>>(
+        a, a_words, as, w, ws, m, n, k / 256, residual, out, (int)tiles_m, tiles_n);
+  else
+    gemm_dma_kernel<T, RESID><<<(unsigned)blocks, T::THREADS, T::LDS_BYTES, stream>>>(
+        a, a_words, as, w, ws, m, n, k / 256, residual, out, (int)tiles_m, tiles_n);
   return hipGetLastError();
 }
 
@@ -435,11 +480,16 @@ hipError_t launch_dma_any(const uint32_t* a, int a_words, const float* as, const
 using Dma256x256 = DmaTile<128, 128, 2, 2>;
 using Dma256x128 = DmaTile<128, 64, 2, 2>;
 using Dma128x128 = DmaTile<64, 64, 2, 2>;
-using Dma256x256NoHint = DmaTile<128, 128, 2, 2, false>;
-using Dma128x128NoHint = DmaTile<64, 64, 2, 2, false>;
-using Dma256x256W8 = DmaTile<128, 64, 2, 4, false>;
-using Dma256x256W8b = DmaTile<64, 128, 4, 2, false>;
-using Dma256x256W8Hint = DmaTile<128, 64, 2, 4, true>;
+using Dma256x256NoHint = DmaTile<128, 128, 2, 2, kSchedFree>;
+using Dma128x128NoHint = DmaTile<64, 64, 2, 2, kSchedFree>;
+using Dma256x256W8 = DmaTile<128, 64, 2, 4, kSchedFree>;
+using Dma256x256W8b = DmaTile<64, 128, 4, 2, kSchedFree>;
+using Dma256x256W8Hint = DmaTile<128, 64, 2, 4, kSchedHint>;
+using Dma256x256Pin = DmaTile<128, 128, 2, 2, kSchedPin>;
+using Dma256x256W8Pin = DmaTile<128, 64, 2, 4, kSchedPin>;
+using DmaH256x128 = DmaHTile<128, 64, 2, 2, kSchedFree>;
+using DmaH128x256 = DmaHTile<128, 64, 1, 4, kSchedFree>;
+using DmaH256x128Pin = DmaHTile<128, 64, 2, 2, kSchedPin>;
 
 template <class T, bool RESID>
 hipError_t launch_dense(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
@@ -645,7 +695,7 @@ static_assert(ExpertDmaTile::BM == kExpertBM, "expert schedule tile height");
 
 }  // namespace
 
-int gemm_config_count() { return 14; }
+int gemm_config_count() { return 19; }
 
 hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
                           const float* ws, int64_t m, int n, int k, const uint16_t* residual,
@@ -653,9 +703,10 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
   if (config < 0) config = (n % 256 == 0 && m >= 1024) ? 9 : 6;
   // Configurations with a 256-wide N tile need n % 256 == 0; the others
   // (N tile 128) take any n % 128 == 0.
-  const bool wide_n = config == 2 || config == 4 || config == 7 || (config >= 9 && config <= 12);
+  const bool wide_n = config == 2 || config == 4 || config == 7 || (config >= 9 && config <= 12) || config == 14 ||
+                      config == 15 || config == 17;
   // The persistent loop needs at least two k-steps.
-  if (k < 512 && config >= 12) config = config == 12 ? 9 : 6;
+  if (k < 512 && (config == 12 || config == 13)) config = config == 12 ? 9 : 6;
   if (wide_n && n % 256 != 0) config = 5;
   switch (config) {
     case 0: return launch_dense_any<Tile128x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
@@ -672,6 +723,11 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
     case 11: return launch_dma_any<Dma256x256W8Hint>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case 12: return launch_persistent_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, 1, stream);
     case 13: return launch_persistent_any<Dma128x128>(a, a_words, as, w, ws, m, n, k, residual, out, 2, stream);
+    case 14: return launch_dma_any<Dma256x256Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 15: return launch_dma_any<Dma256x256W8Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 16: return launch_dma_any<DmaH256x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 17: return launch_dma_any<DmaH128x256>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 18: return launch_dma_any<DmaH256x128Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -39,10 +39,15 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 
-template <int WM_, int WN_, int WAVES_M_, int WAVES_N_, bool HINT_ = true>
+// Main-loop instruction scheduling: the compiler's own order, interleaving
+// hints (sched_group_barrier), or an order pinned by sched_barrier fences.
+enum DmaSched { kSchedFree = 0, kSchedHint = 1, kSchedPin = 2 };
+
+template <int WM_, int WN_, int WAVES_M_, int WAVES_N_, int SCHED_ = kSchedHint>
 struct DmaTile {
   static constexpr int WM = WM_, WN = WN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
-  static constexpr bool HINT = HINT_;
+  static constexpr int SCHED = SCHED_;
+  static constexpr bool HINT = SCHED_ == kSchedHint;
   static constexpr int NW = WAVES_M * WAVES_N;  // waves per workgroup
   static constexpr int THREADS = 64 * NW;
   static constexpr int BM = WM * WAVES_M, BN = WN * WAVES_N;
@@ -91,32 +96,42 @@ __device__ __forceinline__ int dma_chunk16(int wave, int lane) {
 //
 // b_rsrc covers the tile's BN/128 retile block rows for all k-steps (block
 // (b, kt) at (b * ksteps + kt) * 16 KiB).
+//
+// Per-lane state of the main loop: fragment registers, read offsets and the
+// DMA addressing. Every LDS access takes its stage pointer as an argument so
+// that the k-step bodies below can pass the stage being loaded and the stage
+// being read as distinct restrict pointers.
 template <class T>
-__device__ __forceinline__ void dma_mainloop(__amdgpu_buffer_rsrc_t a_rsrc, const int (&voff_a)[T::A_INST],
-                                             int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc, int ksteps,
-                                             char* lds, v16i (&acc)[T::TM][T::TN]) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  // Wave-uniform by construction; readfirstlane lets the compiler keep the
-  // DMA scalar offsets and LDS bases in SGPRs.
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
-  const int h = lane >> 5, lr = lane & 31;
+struct DmaCore {
+  static constexpr int NF = T::TM + T::TN;
+  static constexpr int MF = T::TM * T::TN;
+  int wave, voff_b, a_row, b_row;
+  int offs[4];
+  uint4 raw[2][NF];
+  v4i u[2][NF];
 
+  __device__ __forceinline__ DmaCore() {
+    const int lane = threadIdx.x & 63;
+    // Wave-uniform by construction; readfirstlane lets the compiler keep the
+    // DMA scalar offsets and LDS bases in SGPRs.
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+    const int h = lane >> 5, lr = lane & 31;
+    voff_b = (lane >> 3) * 128 + dma_chunk16(wave, lane);
+    a_row = (wm * T::WM + lr) * 128;
+    b_row = (wn * T::WN + lr) * 128;
 #pragma unroll
-  for (int i = 0; i < T::TM; ++i)
-#pragma unroll
-    for (int j = 0; j < T::TN; ++j) acc[i][j] = v16i{};
+    for (int p = 0; p < 4; ++p) offs[p] = ((4 * h + p) ^ ((lr >> 1) & 7)) << 4;
+  }
 
-  const int voff_b = (lane >> 3) * 128 + dma_chunk16(wave, lane);
-
-  auto issue = [&](int kt, int stage) {
-    char* sa = lds + stage * T::STAGE_BYTES;
-    char* sb = sa + T::A_BYTES;
+  // DMA of k-step kt (A rows and B panel) into `stage`.
+  __device__ __forceinline__ void issue(char* stage, __amdgpu_buffer_rsrc_t a_rsrc, const int (&voff_a)[T::A_INST],
+                                        int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc, int ksteps, int kt) {
+    char* sb = stage + T::A_BYTES;
 #pragma unroll
     for (int ql = 0; ql < T::A_INST; ++ql) {
       const int q = wave + T::NW * ql;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(sa + q * 1024), 16, voff_a[ql],
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(stage + q * 1024), 16, voff_a[ql],
                                                8 * q * a_q_stride + kt * 128, 0, 0);
     }
 #pragma unroll
@@ -126,96 +141,151 @@ __device__ __forceinline__ void dma_mainloop(__amdgpu_buffer_rsrc_t a_rsrc, cons
       __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_ptr_t)(sb + q * 1024), 16, voff_b,
                                                (blk * ksteps + kt) * 16384 + row_in * 128, 0, 0);
     }
-  };
+  }
 
-  // Chunk-pair read offsets (within a region) for pair p = substeps 2p, 2p+1.
-  const int a_row = (wm * T::WM + lr) * 128;
-  const int b_row = (wn * T::WN + lr) * 128;
-  int offs[4];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) offs[p] = ((4 * h + p) ^ ((lr >> 1) & 7)) << 4;
-
-  constexpr int NF = T::TM + T::TN;
-  uint4 raw[2][NF];
-  auto read = [&](int buf, int stage, int p) {
-    const char* sa = lds + stage * T::STAGE_BYTES;
-    const char* sb = sa + T::A_BYTES;
+  // Chunk pair p (substeps 2p, 2p+1) of every fragment of `stage` -> raw[buf].
+  __device__ __forceinline__ void read(const char* stage, int buf, int p) {
+    const char* sb = stage + T::A_BYTES;
 #pragma unroll
     for (int i = 0; i < T::TM; ++i)
-      raw[buf][i] = *reinterpret_cast<const uint4*>(sa + a_row + i * 4096 + offs[p]);
+      raw[buf][i] = *reinterpret_cast<const uint4*>(stage + a_row + i * 4096 + offs[p]);
 #pragma unroll
     for (int j = 0; j < T::TN; ++j)
       raw[buf][T::TM + j] = *reinterpret_cast<const uint4*>(sb + b_row + j * 4096 + offs[p]);
-  };
+  }
 
-  v4i u[2][NF];
-  auto unpack = [&](int dst, int buf, int half) {
+  __device__ __forceinline__ void unpack_one(int dst, int buf, int half, int f) {
+    u[dst][f] = half == 0 ? unpack_pair(raw[buf][f].x, raw[buf][f].y) : unpack_pair(raw[buf][f].z, raw[buf][f].w);
+  }
+  __device__ __forceinline__ void unpack(int dst, int buf, int half) {
 #pragma unroll
-    for (int f = 0; f < NF; ++f)
-      u[dst][f] = half == 0 ? unpack_pair(raw[buf][f].x, raw[buf][f].y)
-                            : unpack_pair(raw[buf][f].z, raw[buf][f].w);
-  };
-  auto mma = [&](int src) {
+    for (int f = 0; f < NF; ++f) unpack_one(dst, buf, half, f);
+  }
+  __device__ __forceinline__ void mma(v16i (&acc)[T::TM][T::TN], int src) {
 #pragma unroll
     for (int i = 0; i < T::TM; ++i)
 #pragma unroll
       for (int j = 0; j < T::TN; ++j) acc[i][j] = mfma32_i8(u[src][T::TM + j], u[src][i], acc[i][j]);
-  };
+  }
 
-  // Scheduling of one substep: the chunk reads it issues first, then
-  // {1 MFMA, VPM VALU} repeated, so the unpack (and address arithmetic) of
-  // the next substep fills the MFMA shadow instead of trailing it.
-  constexpr int MF = T::TM * T::TN;
-  constexpr int VPM = (6 * NF + MF - 1) / MF + 1;
-  auto hint = [&](auto reads) {
-    if constexpr (T::HINT) {
-      if constexpr (decltype(reads)::value > 0)
-        __builtin_amdgcn_sched_group_barrier(0x100, decltype(reads)::value, 0);
+  // One substep on u[src] with the unpack of raw[buf] (half) into u[dst] for
+  // the next substep (UNPACK = false: MFMAs only).
+  //  kSchedPin: MFMA q is followed by the unpack of the fragments assigned to
+  //    it (fragment f after MFMA f * MF / NF), each group fenced, so the MFMA
+  //    stream never waits behind a block of VALU.
+  //  kSchedHint: `reads` chunk reads first, then {1 MFMA, VPM VALU} repeated.
+  template <bool UNPACK, int READS>
+  __device__ __forceinline__ void substep(v16i (&acc)[T::TM][T::TN], int src, int dst, int buf, int half) {
+    if constexpr (T::SCHED == kSchedPin) {
 #pragma unroll
       for (int q = 0; q < MF; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
-      }
-    }
-  };
-
-  // The steady-state body is branch-free (one basic block per k-step) so the
-  // accumulators stay in place: the DMA for step kt + 2 and the read of step
-  // kt + 1 are issued even past the last step. Those loads are range-checked
-  // buffer reads (row padding or zeros, never a fault) into a stage that is
-  // not read again; the final wait drains them before the epilogue.
-  issue(0, 0);
-  issue(1, 1);
-  wait_vmcnt<T::A_INST + T::B_INST>();
-  __syncthreads();
-  read(0, 0, 0);
-  unpack(0, 0, 0);
-
-  for (int kt = 0; kt < ksteps; ++kt) {
-    const int st = kt & 1;
+        const int i = q / T::TN, j = q % T::TN;
+        acc[i][j] = mfma32_i8(u[src][T::TM + j], u[src][i], acc[i][j]);
+        if constexpr (UNPACK) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int cur = p & 1;
-      // substep 2p: prefetch the next chunk pair, MFMAs on u[0], unpack the
-      // odd half of this pair into u[1].
-      if (p < 3) {
-        read(cur ^ 1, st, p + 1);
-      } else {
-        wait_vmcnt<0>();
-        __syncthreads();
-        issue(kt + 2, st);
-        read(cur ^ 1, st ^ 1, 0);
+          for (int f = 0; f < NF; ++f)
+            if (f * MF / NF == q) unpack_one(dst, buf, half, f);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      mma(0);
-      unpack(1, cur, 1);
-      hint(std::integral_constant<int, NF>{});
-      // substep 2p+1: MFMAs on u[1], unpack the even half of the next pair.
-      mma(1);
-      unpack(0, cur ^ 1, 0);
-      hint(std::integral_constant<int, 0>{});
+    } else {
+      mma(acc, src);
+      if constexpr (UNPACK) unpack(dst, buf, half);
+      if constexpr (T::SCHED == kSchedHint) {
+        constexpr int VPM = (6 * NF + MF - 1) / MF + 1;
+        if constexpr (READS > 0) __builtin_amdgcn_sched_group_barrier(0x100, READS, 0);
+#pragma unroll
+        for (int q = 0; q < MF; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+        }
+      }
     }
   }
+
+  // Pairs 0..2 of a k-step read from `rd` (pair 0 already in raw[0] and its
+  // even half in u[0]): each prefetches the next chunk pair, runs its two
+  // substeps and unpacks ahead. Leaves pair 3 in raw[1], its even half in u[0].
+  __device__ __forceinline__ void pairs012(v16i (&acc)[T::TM][T::TN], const char* rd) {
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      const int cur = p & 1;
+      read(rd, cur ^ 1, p + 1);
+      substep<true, NF>(acc, 0, 1, cur, 1);
+      substep<true, 0>(acc, 1, 0, cur ^ 1, 0);
+    }
+  }
+};
+
+// The k-step bodies. LDS DMA is tracked by the same counter as other vector
+// memory operations, and the compiler makes an LDS read wait for every
+// outstanding DMA it cannot prove disjoint from it. Passing the stage being
+// loaded and the stage being read as distinct restrict pointers of one
+// inlined call is that proof: the prefetch then stays in flight across the
+// whole k-step instead of being drained at the first read.
+
+// k-step 0: DMA of k-steps 0 and 1, then pairs 0..2 of k-step 0.
+template <class T>
+__device__ __forceinline__ void dma_kstep_first(DmaCore<T>& c, v16i (&acc)[T::TM][T::TN],
+                                                char* __restrict__ rd, char* __restrict__ dma,
+                                                __amdgpu_buffer_rsrc_t a_rsrc, const int (&voff_a)[T::A_INST],
+                                                int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc, int ksteps) {
+  c.issue(rd, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, 0);
+  c.issue(dma, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, 1);
+  wait_vmcnt<T::A_INST + T::B_INST>();
+  __syncthreads();
+  c.read(rd, 0, 0);
+  c.unpack(0, 0, 0);
+  c.pairs012(acc, rd);
   wait_vmcnt<0>();
+  __syncthreads();
+}
+
+// k-step kt >= 1: DMA of k-step kt + 1 into the stage freed by k-step kt - 1,
+// the last pair of k-step kt - 1 (registers only), then pairs 0..2 of k-step
+// kt from `rd`; ends once the DMA of kt + 1 has landed and every wave is done
+// reading `rd`.
+template <class T>
+__device__ __forceinline__ void dma_kstep_next(DmaCore<T>& c, v16i (&acc)[T::TM][T::TN],
+                                               const char* __restrict__ rd, char* __restrict__ dma,
+                                               __amdgpu_buffer_rsrc_t a_rsrc, const int (&voff_a)[T::A_INST],
+                                               int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc, int ksteps,
+                                               int kt) {
+  c.issue(dma, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, kt + 1);
+  c.read(rd, 0, 0);
+  if constexpr (T::SCHED == kSchedPin) __builtin_amdgcn_sched_barrier(0);
+  c.template substep<true, DmaCore<T>::NF>(acc, 0, 1, 1, 1);
+  c.template substep<true, 0>(acc, 1, 0, 0, 0);
+  c.pairs012(acc, rd);
+  wait_vmcnt<0>();
+  __syncthreads();
+}
+
+// Full contraction over `ksteps` 256-k steps into acc (zeroed here). The
+// DMA of k-step kt + 1 is issued at the start of k-step kt and waited for at
+// its end; two LDS stages alternate. The body is branch-free (one basic block
+// per k-step) so the accumulators stay in place: the last k-step also loads
+// k-step `ksteps`, a range-checked buffer read (row padding, zeros or the next
+// panel, never a fault) into a stage that is not read again, drained by the
+// final wait.
+template <class T>
+__device__ __forceinline__ void dma_mainloop(__amdgpu_buffer_rsrc_t a_rsrc, const int (&voff_a)[T::A_INST],
+                                             int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc, int ksteps,
+                                             char* lds, v16i (&acc)[T::TM][T::TN]) {
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j) acc[i][j] = v16i{};
+  DmaCore<T> c;
+  dma_kstep_first<T>(c, acc, lds, lds + T::STAGE_BYTES, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps);
+  for (int kt = 1; kt < ksteps; ++kt) {
+    char* rd = lds + (kt & 1) * T::STAGE_BYTES;
+    char* dma = lds + ((kt & 1) ^ 1) * T::STAGE_BYTES;
+    dma_kstep_next<T>(c, acc, rd, dma, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, kt);
+  }
+  // Last pair of the last k-step.
+  c.template substep<true, 0>(acc, 0, 1, 1, 1);
+  c.template substep<false, 0>(acc, 1, 0, 0, 0);
 }
 
 }  // namespace clef
