@@ -48,6 +48,8 @@ SIGNATURES = {
     "clef_moe_group_routes": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _SZ, _P]),
     "clef_moe_expert_tasks": (ctypes.c_int, [_P, _I64, _P, _P]),
     "clef_moe_expert_workspace_bytes": (_SZ, [_I64, _I32]),
+    "clef_moe_expert_gate_up_i4": (ctypes.c_int, [_P, _I32, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P,
+                                                  _P, _SZ, _P]),
     "clef_moe_expert_i4": (ctypes.c_int, [_P, _I32, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P,
                                           _P, _SZ, _P]),
     "clef_swiglu": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
@@ -333,6 +335,20 @@ def omni_expert(a: Prepared, w: QuantizedWeight, groups: torch.Tensor, tokens: i
                                     _ptr(w.scales), _ptr(groups), tokens, topk, w.cols, n,
                                     int(input_routed), _ptr(out), _ptr(ws), ws_bytes, _stream()))
     return out
+
+
+def omni_gate_up(a: Prepared, gate: QuantizedWeight, up: QuantizedWeight, groups: torch.Tensor, tokens: int,
+                 topk: int) -> torch.Tensor:
+    """Engine::omni_gate_up (src/omni.rs:300-372): fused gate/up expert GEMMs
+    and SwiGLU over the routed rows; h bf16 [tokens * topk][n]."""
+    n = gate.rows // 128
+    h = torch.zeros((tokens * topk, n), dtype=torch.bfloat16, device=groups.device)
+    ws_bytes = int(lib().clef_moe_expert_workspace_bytes(tokens, topk))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=groups.device)
+    _check(lib().clef_moe_expert_gate_up_i4(_ptr(a.storage), a.stride, _ptr(a.scales), _ptr(gate.codes),
+                                            _ptr(gate.scales), _ptr(up.codes), _ptr(up.scales), _ptr(groups),
+                                            tokens, topk, gate.cols, n, _ptr(h), _ptr(ws), ws_bytes, _stream()))
+    return h
 
 
 def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:

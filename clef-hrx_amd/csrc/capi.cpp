@@ -244,6 +244,27 @@ int clef_moe_expert_i4(const uint32_t* a, int32_t stride, const float* a_scales,
                                            tokens, topk, k, n, input_routed ? 1 : 0, out, hs(stream)));
 }
 
+int clef_moe_expert_gate_up_i4(const uint32_t* a, int32_t stride, const float* a_scales, const uint32_t* gate_w,
+                               const float* gate_s, const uint32_t* up_w, const float* up_s,
+                               const float* groups, int64_t tokens, int32_t topk, int32_t k, int32_t n,
+                               uint16_t* h, void* workspace, size_t workspace_bytes, clef_stream_t stream) {
+  // src/omni.rs:309-320, 333-344.
+  if (!(tokens >= 1 && tokens <= 1048576 && topk >= 1 && topk <= 128))
+    return fail("fused gate/up requires regular grouped routes");
+  if (!(k % 256 == 0 && k >= 256 && n % 128 == 0 && n >= 128 && stride >= k && stride % 32 == 0 &&
+        tokens * (int64_t)(stride / 8) * 4 < ((int64_t)1 << 31)))
+    return fail("incompatible fused expert weights");
+  if (!aligned(a, 16) || !aligned(a_scales, 4) || !aligned(gate_w, 16) || !aligned(gate_s, 16) ||
+      !aligned(up_w, 16) || !aligned(up_s, 16) || !aligned(groups, 4) || !aligned(h, 16) ||
+      !aligned(workspace, 16))
+    return fail(kAlign);
+  if (workspace_bytes < clef_moe_expert_workspace_bytes(tokens, topk)) return fail(kWorkspace);
+  int32_t* schedule = static_cast<int32_t*>(workspace);
+  if (int rc = hip_status(clef::launch_expert_schedule(groups, tokens, schedule, hs(stream)))) return rc;
+  return hip_status(clef::launch_expert_gate_up(a, stride / 8, a_scales, gate_w, gate_s, up_w, up_s, groups,
+                                                schedule, tokens, topk, k, n, h, hs(stream)));
+}
+
 int clef_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h, clef_stream_t stream) {
   if (n < 0) return fail("SwiGLU shape/dtype mismatch");
   if (n == 0) return CLEF_OK;
@@ -345,13 +366,23 @@ int clef_moe_layer(const uint16_t* x, const void* logits, int32_t logits_dtype, 
   CLEF_STEP(clef::launch_group_routes(routes, tokens, topk, groups, order, ws + l.group_ws, s));
   CLEF_STEP(clef::launch_expert_schedule(groups, tokens, schedule, s));
   CLEF_STEP(clef::launch_prepare(x, tokens, hidden, sx, 4, ax, s));
-  CLEF_STEP(clef::launch_expert_i4(ax, sx / 8, axs, gate_w, gate_s, groups, schedule, tokens, topk,
-                                   hidden, inter, 0, gate, s));
-  CLEF_STEP(clef::launch_expert_i4(ax, sx / 8, axs, up_w, up_s, groups, schedule, tokens, topk,
-                                   hidden, inter, 0, up, s));
-  // SwiGLU fused into the quantizer of h: bit-equal to swiglu then prepare
-  // (src/quantized.rs:1189-1266).
-  CLEF_STEP(clef::launch_prepare_swiglu(gate, up, routed, inter, sh, 4, ah, s));
+  if (tokens * (int64_t)(sx / 8) * 4 < ((int64_t)1 << 31)) {
+    // Gate and up share one pass over the gathered x rows and SwiGLU runs in
+    // their epilogue; h is then quantized per routed row. Bit-equal to the
+    // separate gate, up, swiglu and prepare (each lane applies the same E1
+    // rounding and S1 to the same bf16 values).
+    CLEF_STEP(clef::launch_expert_gate_up(ax, sx / 8, axs, gate_w, gate_s, up_w, up_s, groups, schedule, tokens,
+                                          topk, hidden, inter, gate, s));
+    CLEF_STEP(clef::launch_prepare(gate, routed, inter, sh, 4, ah, s));
+  } else {
+    CLEF_STEP(clef::launch_expert_i4(ax, sx / 8, axs, gate_w, gate_s, groups, schedule, tokens, topk,
+                                     hidden, inter, 0, gate, s));
+    CLEF_STEP(clef::launch_expert_i4(ax, sx / 8, axs, up_w, up_s, groups, schedule, tokens, topk,
+                                     hidden, inter, 0, up, s));
+    // SwiGLU fused into the quantizer of h: bit-equal to swiglu then prepare
+    // (src/quantized.rs:1189-1266).
+    CLEF_STEP(clef::launch_prepare_swiglu(gate, up, routed, inter, sh, 4, ah, s));
+  }
   CLEF_STEP(clef::launch_expert_i4(ah, sh / 8, ahs, down_w, down_s, groups, schedule, tokens, topk,
                                    inter, hidden, 1, values, s));
   CLEF_STEP(clef::launch_combine(values, routes, order, tokens, hidden, topk, out, s));

@@ -57,12 +57,24 @@ __device__ __forceinline__ float cephes_expf(float x) {
   return __builtin_ldexpf(p, (int)n);
 }
 
-// S1: h = bf16(f32(bf16(g / (1 + exp(-g)))) * u). kernels/swiglu.loom:43-51.
-__device__ __forceinline__ float swiglu1(float g, float u) {
+// The activation half of S1: bf16(g / (1 + exp(-g))). kernels/swiglu.loom:43-47.
+__device__ __forceinline__ float silu_bf16(float g) {
   float e = cephes_expf(-g);
   float d = 1.0f + e;
-  float act = g / d;
-  return bf16_round(bf16_round(act) * u);
+  return bf16_round(g / d);
+}
+
+// S1: h = bf16(f32(bf16(g / (1 + exp(-g)))) * u). kernels/swiglu.loom:43-51.
+__device__ __forceinline__ float swiglu1(float g, float u) { return bf16_round(silu_bf16(g) * u); }
+
+// silu_bf16 tabulated for every bf16 g with 2^-25 <= |g| < 2^7 (exponent field
+// 102..133), as bf16 bits at index sign * 4096 + (exponent - 102) * 128 +
+// mantissa. Other g (tiny, large, inf, NaN) are computed directly.
+constexpr int kSiluLutExp0 = 102, kSiluLutBinades = 32;
+constexpr int kSiluLutSize = 2 * kSiluLutBinades * 128;
+__device__ __forceinline__ int silu_lut_index(uint32_t gbits) {
+  const uint32_t e = ((gbits >> 7) & 0xFFu) - kSiluLutExp0;
+  return e < (uint32_t)kSiluLutBinades ? (int)(((gbits >> 15) << 12) | (e << 7) | (gbits & 127u)) : -1;
 }
 
 // One radix-4 stage of the reference rotation on a quad (a, b, c, d) taken at

@@ -8,6 +8,8 @@
 // E1 (kernels/omni_expert_i4.loom:113-125, 436-462): for expert e and slot i,
 // route = groups[e][1+i], xr = input_routed ? route : route / topk,
 // out[route][c] = bf16(RN(f32(acc) * RN(as[xr] * ws[e*n + c]))), no clamp.
+#include <mutex>
+
 #include "gemm_core.hpp"
 #include "gemm_dma.hpp"
 #include "gemm_persist.hpp"
@@ -278,7 +280,7 @@ __global__ __launch_bounds__(T::THREADS, 2) void gemm_dmah_kernel(
 #pragma unroll
     for (int ql = 0; ql < T::A_INST; ++ql) voff_a[ql] = (lane >> 2) * a_words * 4 + dmah_chunk16(lane);
   }
-  dmah_mainloop<T>(a_rsrc, voff_a, a_words * 4, b_rsrc, kb, lds, acc);
+  dmah_mainloop<T>(a_rsrc, voff_a, a_words * 4, b_rsrc, b_rsrc, kb, lds, acc);
   dense_epilogue<T, RESID>(acc, as, ws, M, N, kb * 256, m0, n0, residual, out, lds);
 #endif
 }
@@ -438,8 +440,8 @@ hipError_t launch_persistent_any(const uint32_t* a, int a_words, const float* as
 
 template <class T>
 struct IsHalfStage : std::false_type {};
-template <int A, int B, int C, int D, int E>
-struct IsHalfStage<DmaHTile<A, B, C, D, E>> : std::true_type {};
+template <int A, int B, int C, int D, int E, bool F>
+struct IsHalfStage<DmaHTile<A, B, C, D, E, F>> : std::true_type {};
 
 template <class T, bool RESID>
 hipError_t launch_dma(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
@@ -693,6 +695,225 @@ __global__ __launch_bounds__(T::THREADS) void expert_dma_kernel(
 using ExpertDmaTile = DmaTile<64, 64, 2, 2>;
 static_assert(ExpertDmaTile::BM == kExpertBM, "expert schedule tile height");
 
+// Grouped expert GEMM on the half-k-step core: 128 expert slots x 256 weight
+// rows per workgroup, four 64 x 128 waves, two workgroups per CU.
+//  GU = false: E1 over 256 output columns of one weight set.
+//  GU = true:  the fused gate/up/SwiGLU producer: weight rows are 128 gate
+//    rows and the same 128 up rows; each lane holds gate and up of the same
+//    output column, applies E1 to both (bf16), then S1, and writes h.
+// A wave whose 64 slots are all past the expert's count runs the DMA and
+// barrier schedule only. Work items, XCD chunking and the gathered A rows
+// are as in expert_dma_kernel.
+// silu_bf16 of the bf16 values tabulated by silu_lut_index (16 KiB), built
+// once per device by silu_lut_kernel with the same device arithmetic.
+__device__ uint16_t g_silu_lut[kSiluLutSize];
+
+__global__ __launch_bounds__(256) void silu_lut_kernel() {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= kSiluLutSize) return;
+  const uint32_t bits = ((uint32_t)(idx >> 12) << 15) | ((uint32_t)(kSiluLutExp0 + ((idx >> 7) & 31)) << 7) |
+                        (uint32_t)(idx & 127);
+  g_silu_lut[idx] = (uint16_t)f32_to_bf16(silu_bf16(bf16_to_f32(bits)));
+}
+
+using ExpertHTile = DmaHTile<64, 128, 2, 2, kSchedFree, false>;
+using ExpertGUTile = DmaHTile<64, 128, 2, 2, kSchedFree, true>;
+static_assert(ExpertHTile::BM == kExpertBM && ExpertGUTile::BM == kExpertBM, "expert schedule tile height");
+
+// Dynamic LDS of expert_dmah_kernel: stages / staged output, the SiLU table
+// (GU), the slots' routes and the tile's weight scales.
+template <class T, bool GU>
+constexpr int expert_lds_bytes() {
+  constexpr int cols = GU ? T::BN / 2 : T::BN;
+  constexpr int base = GU ? 2 * T::STAGE_BYTES + kSiluLutSize * 2
+                          : (T::LDS_BYTES > 2 * T::STAGE_BYTES ? T::LDS_BYTES : 2 * T::STAGE_BYTES);
+  return base + T::BM * 4 + (GU ? 2 : 1) * (cols * 4 > 1024 ? cols * 4 : 1024);
+}
+
+template <class T, bool GU>
+__global__ __launch_bounds__(T::THREADS, 2) void expert_dmah_kernel(
+    const uint32_t* __restrict__ a, int a_words, uint32_t a_bytes, const float* __restrict__ as,
+    const uint32_t* __restrict__ w, const float* __restrict__ ws, const uint32_t* __restrict__ w2,
+    const float* __restrict__ ws2, const float* __restrict__ groups, const int32_t* __restrict__ schedule,
+    int64_t tokens, int topk, int kb, int n, int input_routed, uint16_t* __restrict__ out, int tiles_n) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  extern __shared__ __align__(16) char lds[];
+  const int64_t items = (int64_t)schedule[0] * tiles_n;
+  const int64_t chunk = (items + 7) / 8;
+  const int64_t local = blockIdx.x / 8;
+  if (local >= chunk) return;
+  const int64_t item = (blockIdx.x % 8) * chunk + local;
+  if (item >= items) return;
+  const int tile = (int)(item / tiles_n);
+  const int tn = (int)(item - (int64_t)tile * tiles_n);
+  const int e = schedule[1 + 2 * tile];
+  const int row0 = schedule[2 + 2 * tile];
+  const float* list = groups + (int64_t)e * (tokens + 1);
+  const int count = (int)list[0];
+  constexpr int COLS = GU ? T::BN / 2 : T::BN;  // output columns per tile
+  const int n0 = tn * COLS;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+
+  // LDS: the two stages (the staged output tile reuses them), then for GU the
+  // SiLU table, then per-tile metadata: the 128 slots' routes (int) and the
+  // tile's weight scales (f32, COLS each for gate and up).
+  constexpr int LUT_OFF = 2 * T::STAGE_BYTES;
+  constexpr int META_OFF = GU ? LUT_OFF + kSiluLutSize * 2 : (T::LDS_BYTES > LUT_OFF ? T::LDS_BYTES : LUT_OFF);
+  constexpr int WS_SLOT = COLS * 4 > 1024 ? COLS * 4 : 1024;
+  int* routes_lds = reinterpret_cast<int*>(lds + META_OFF);
+  char* ws_lds = lds + META_OFF + T::BM * 4;
+  // Weight scales of the tile's columns by DMA (1 KiB per instruction).
+  {
+    // A DMA instruction writes 1 KiB whatever the source range (lanes past
+    // it write zeros), so each scale vector gets a whole 1 KiB slot.
+    constexpr int WS_INST = COLS * 4 / 1024 > 0 ? COLS * 4 / 1024 : 1;
+    static_assert(COLS * 4 % 1024 == 0 || COLS * 4 == 512, "scale DMA granularity");
+    const uint32_t ws_bytes = COLS * 4;
+    const __amdgpu_buffer_rsrc_t ws_rsrc = make_rsrc(ws + (int64_t)e * n + n0, ws_bytes);
+    const __amdgpu_buffer_rsrc_t ws2_rsrc = make_rsrc((GU ? ws2 : ws) + (int64_t)e * n + n0, ws_bytes);
+    if (wave < WS_INST)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ws_rsrc, (lds_ptr_t)(ws_lds + wave * 1024), 16, lane * 16,
+                                               wave * 1024, 0, 0);
+    if (GU && wave >= 2 && wave < 2 + WS_INST)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ws2_rsrc, (lds_ptr_t)(ws_lds + WS_SLOT + (wave - 2) * 1024), 16,
+                                               lane * 16, (wave - 2) * 1024, 0, 0);
+  }
+  int voff_a[T::A_INST];
+#pragma unroll
+  for (int ql = 0; ql < T::A_INST; ++ql) {
+    const int r = 16 * (wave + T::NW * ql) + (lane >> 2);
+    const int slot = row0 + r;
+    int route = -1;
+    if (slot < count) {
+      route = (int)list[1 + slot];
+      const int64_t xr = input_routed ? (int64_t)route : (int64_t)route / topk;
+      voff_a[ql] = (int)(xr * a_words * 4) + dmah_chunk16(lane);
+    } else {
+      voff_a[ql] = (int)0x80000000u;
+    }
+    if ((lane & 3) == 0) routes_lds[r] = route;
+  }
+  // The SiLU table goes to LDS after the two stages; its DMA is issued before
+  // the stages', so the main loop's first wait covers it.
+  if constexpr (GU) {
+    static_assert(LUT_OFF + kSiluLutSize * 2 <= T::LDS_BYTES, "SiLU table in LDS");
+    const __amdgpu_buffer_rsrc_t lut_rsrc = make_rsrc(g_silu_lut, kSiluLutSize * 2);
+#pragma unroll
+    for (int i = 0; i < kSiluLutSize * 2 / 1024 / T::NW; ++i) {
+      const int q = wave * (kSiluLutSize * 2 / 1024 / T::NW) + i;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(lut_rsrc, (lds_ptr_t)(lds + LUT_OFF + q * 1024), 16, lane * 16,
+                                               q * 1024, 0, 0);
+    }
+  }
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a, a_bytes);
+  const int64_t blk0 = ((int64_t)e * n + n0) / 128;
+  const uint32_t b_bytes = (uint32_t)((COLS / 128) * kb * 16384);
+  const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(w + blk0 * kb * 4096, b_bytes);
+  const __amdgpu_buffer_rsrc_t b_rsrc2 = GU ? make_rsrc(w2 + blk0 * kb * 4096, b_bytes) : b_rsrc;
+  // Epilogue inputs that depend on a chain of loads (slot -> route -> scale)
+  // are fetched before the main loop.
+  const int h = lane >> 5, lr = lane & 31;
+  float asr[T::TM];
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    const int slot = row0 + wm * T::WM + 32 * i + lr;
+    asr[i] = 0.0f;
+    if (slot < count) {
+      const int64_t route = (int64_t)list[1 + slot];
+      asr[i] = as[input_routed ? route : route / topk];
+    }
+  }
+  v16i acc[T::TM][T::TN];
+  if (row0 + wm * T::WM < count)
+    dmah_mainloop<T, true>(a_rsrc, voff_a, 0, b_rsrc, b_rsrc2, kb, lds, acc);
+  else
+    dmah_mainloop<T, false>(a_rsrc, voff_a, 0, b_rsrc, b_rsrc2, kb, lds, acc);
+
+  // Values -> bf16 tile in LDS (over the drained stages; rows of COLS * 2
+  // bytes, 8-byte blocks XOR-swizzled by row), then whole 16-byte row pieces
+  // to the routed output rows.
+  static_assert(T::BM * COLS * 2 <= (GU ? 2 * T::STAGE_BYTES : T::LDS_BYTES), "staged output tile");
+  constexpr int RP = COLS * 2;  // staged row pitch, bytes
+  __syncthreads();              // every wave is done with the stages
+  auto stage = [&](int row, int col, uint32_t p0, uint32_t p1) {
+    const int blk = (col >> 2) ^ (row & 15);
+    *reinterpret_cast<uint2*>(lds + row * RP + blk * 8) = make_uint2(p0, p1);
+  };
+  constexpr int JN = GU ? T::TN / 2 : T::TN;  // output fragments per lane row
+#pragma unroll
+  for (int j = 0; j < JN; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int col = wn * (GU ? T::WN / 2 : T::WN) + 32 * j + 8 * q + 4 * h;  // within the tile
+      const float4 wsv = *reinterpret_cast<const float4*>(ws_lds + col * 4);
+      float4 wsu = wsv;
+      if constexpr (GU) wsu = *reinterpret_cast<const float4*>(ws_lds + WS_SLOT + col * 4);
+      const float wg[4] = {wsv.x, wsv.y, wsv.z, wsv.w}, wu[4] = {wsu.x, wsu.y, wsu.z, wsu.w};
+      float y[T::TM][4];
+#pragma unroll
+      for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) y[i][t] = (float)(acc[i][j][4 * q + t] >> 8) * (asr[i] * wg[t]);
+      if constexpr (GU) {
+        // SiLU from the LDS table for all 4 * TM values at once (their reads
+        // overlap), then one wave-uniform branch for the rare values outside
+        // the table, computed directly.
+        const uint16_t* lut = reinterpret_cast<const uint16_t*>(lds + LUT_OFF);
+        float act[T::TM][4];
+        bool slow = false;
+#pragma unroll
+        for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            y[i][t] = bf16_round(y[i][t]);
+            const int li = silu_lut_index(as_uint(y[i][t]) >> 16);
+            slow |= li < 0;
+            act[i][t] = bf16_to_f32(lut[li < 0 ? 0 : li]);
+          }
+        if (__any(slow)) {
+#pragma unroll
+          for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (silu_lut_index(as_uint(y[i][t]) >> 16) < 0) act[i][t] = silu_bf16(y[i][t]);
+        }
+#pragma unroll
+        for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float u = bf16_round((float)(acc[i][j + JN][4 * q + t] >> 8) * (asr[i] * wu[t]));
+            y[i][t] = bf16_round(act[i][t] * u);
+          }
+      }
+#pragma unroll
+      for (int i = 0; i < T::TM; ++i)
+        stage(wm * T::WM + 32 * i + lr, col, pack_bf16x2(y[i][0], y[i][1]), pack_bf16x2(y[i][2], y[i][3]));
+    }
+  __syncthreads();
+  constexpr int LPR = COLS / 8;              // lanes per row (16 bytes each)
+  constexpr int RPP = T::THREADS / LPR;      // rows per pass
+  const int c = threadIdx.x % LPR;
+#pragma unroll
+  for (int pass = 0; pass < T::BM / RPP; ++pass) {
+    const int row = RPP * pass + threadIdx.x / LPR;
+    const int route = routes_lds[row];
+    if (route < 0) continue;
+    const int x = row & 15;
+    uint4 v = *reinterpret_cast<const uint4*>(lds + row * RP + ((c ^ (x >> 1)) << 4));
+    if (x & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+    *reinterpret_cast<uint4*>(out + (int64_t)route * n + n0 + 8 * c) = v;
+  }
+#endif
+}
+
+template <class T, bool GU>
+hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, const float* as, const uint32_t* w,
+                              const float* ws, const uint32_t* w2, const float* ws2, const float* groups,
+                              const int32_t* schedule, int64_t tokens, int topk, int k, int n, int input_routed,
+                              uint16_t* out, hipStream_t stream);
+
 }  // namespace
 
 int gemm_config_count() { return 19; }
@@ -734,6 +955,59 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
 
 int64_t expert_max_tiles(int64_t routes) { return (routes + kExpertBM - 1) / kExpertBM + 128; }
 
+namespace {
+template <class T, bool GU>
+hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, const float* as, const uint32_t* w,
+                              const float* ws, const uint32_t* w2, const float* ws2, const float* groups,
+                              const int32_t* schedule, int64_t tokens, int topk, int k, int n, int input_routed,
+                              uint16_t* out, hipStream_t stream) {
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&expert_dmah_kernel<T, GU>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, expert_lds_bytes<T, GU>());
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const int tiles_n = n / (GU ? T::BN / 2 : T::BN);
+  const int64_t blocks = 8 * ((expert_max_tiles(tokens * topk) * tiles_n + 7) / 8);
+  expert_dmah_kernel<T, GU><<<(unsigned)blocks, T::THREADS, expert_lds_bytes<T, GU>(), stream>>>(
+      a, a_words, (uint32_t)a_bytes, as, w, ws, w2, ws2, groups, schedule, tokens, topk, k / 256, n, input_routed,
+      out, tiles_n);
+  return hipGetLastError();
+}
+}  // namespace
+
+namespace {
+// Builds g_silu_lut on the current device the first time it is needed. The
+// build waits for completion, so every later launch on any stream reads a
+// complete table (the first call therefore cannot be captured into a graph).
+hipError_t ensure_silu_lut(hipStream_t stream) {
+  static std::mutex mu;
+  static bool ready[256] = {};
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev)) return e;
+  if (dev < 0 || dev >= 256) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (ready[dev]) return hipSuccess;
+  silu_lut_kernel<<<(kSiluLutSize + 255) / 256, 256, 0, stream>>>();
+  if (hipError_t e = hipGetLastError()) return e;
+  if (hipError_t e = hipStreamSynchronize(stream)) return e;
+  ready[dev] = true;
+  return hipSuccess;
+}
+}  // namespace
+
+hipError_t launch_expert_gate_up(const uint32_t* a, int a_words, const float* as, const uint32_t* gate_w,
+                                 const float* gate_s, const uint32_t* up_w, const float* up_s, const float* groups,
+                                 const int32_t* schedule, int64_t tokens, int topk, int k, int n, uint16_t* h,
+                                 hipStream_t stream) {
+  const int64_t a_bytes = tokens * a_words * 4;
+  if (a_bytes >= ((int64_t)1 << 31) || n % 128 != 0) return hipErrorInvalidValue;
+  if (hipError_t e = ensure_silu_lut(stream)) return e;
+  return launch_expert_dmah<ExpertGUTile, true>(a, a_words, a_bytes, as, gate_w, gate_s, up_w, up_s, groups,
+                                                schedule, tokens, topk, k, n, 0, h, stream);
+}
+
 size_t expert_schedule_bytes(int64_t routes) {
   return (size_t)(1 + 2 * expert_max_tiles(routes)) * sizeof(int32_t);
 }
@@ -755,6 +1029,9 @@ hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* as, con
                             hipStream_t stream) {
   const int64_t a_rows = input_routed ? tokens * topk : tokens;
   const int64_t a_bytes = a_rows * a_words * 4;
+  if (a_bytes < ((int64_t)1 << 31) && n % 256 == 0)
+    return launch_expert_dmah<ExpertHTile, false>(a, a_words, a_bytes, as, w, ws, w, ws, groups, schedule, tokens,
+                                                  topk, k, n, input_routed, out, stream);
   if (a_bytes < ((int64_t)1 << 31)) {
     using T = ExpertDmaTile;
     static bool configured = false;

@@ -143,6 +143,28 @@ struct DmaCore {
     }
   }
 
+  // DMA instruction `idx` of k-step kt (A slots first, then B slots).
+  __device__ __forceinline__ void issue_one(char* stage, __amdgpu_buffer_rsrc_t a_rsrc,
+                                            const int (&voff_a)[T::A_INST], int a_q_stride,
+                                            __amdgpu_buffer_rsrc_t b_rsrc, int ksteps, int kt, int idx) {
+    if (idx < T::A_INST) {
+      const int q = wave + T::NW * idx;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(stage + q * 1024), 16, voff_a[idx],
+                                               8 * q * a_q_stride + kt * 128, 0, 0);
+    } else {
+      const int q = wave + T::NW * (idx - T::A_INST);
+      const int blk = (8 * q) >> 7, row_in = (8 * q) & 127;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_ptr_t)(stage + T::A_BYTES + q * 1024), 16, voff_b,
+                                               (blk * ksteps + kt) * 16384 + row_in * 128, 0, 0);
+    }
+  }
+
+  // Chunk pair p of fragment f of `stage` -> raw[buf][f].
+  __device__ __forceinline__ void read_one(const char* stage, int buf, int p, int f) {
+    raw[buf][f] = f < T::TM ? *reinterpret_cast<const uint4*>(stage + a_row + f * 4096 + offs[p])
+                            : *reinterpret_cast<const uint4*>(stage + T::A_BYTES + b_row + (f - T::TM) * 4096 + offs[p]);
+  }
+
   // Chunk pair p (substeps 2p, 2p+1) of every fragment of `stage` -> raw[buf].
   __device__ __forceinline__ void read(const char* stage, int buf, int p) {
     const char* sb = stage + T::A_BYTES;
@@ -203,10 +225,57 @@ struct DmaCore {
     }
   }
 
+  // Pinned substep with memory work spread over the MFMA slots: after MFMA q
+  // come the unpacks assigned to q and `extra(q)` (the chunk reads and DMA
+  // instructions given to that slot). A wave that issues its LDS reads in a
+  // burst stalls its own MFMA issue (measured: 8 back-to-back ds_read per 16
+  // MFMAs cost a third of the MFMA rate on one wave per SIMD); one or two per
+  // slot cost almost nothing.
+  template <bool UNPACK, class Extra>
+  __device__ __forceinline__ void substep_spread(v16i (&acc)[T::TM][T::TN], int src, int dst, int buf, int half,
+                                                 Extra extra) {
+#pragma unroll
+    for (int q = 0; q < MF; ++q) {
+      const int i = q / T::TN, j = q % T::TN;
+      acc[i][j] = mfma32_i8(u[src][T::TM + j], u[src][i], acc[i][j]);
+      extra(q);
+      if constexpr (UNPACK) {
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          if (f * MF / NF == q) unpack_one(dst, buf, half, f);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // extra(q) that reads chunk pair p of `stage` into raw[rbuf], fragment f
+  // after MFMA f * MF / NF.
+  struct SpreadReads {
+    DmaCore* c;
+    const char* stage;
+    int rbuf, p;
+    __device__ __forceinline__ void operator()(int q) const {
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+        if (f * MF / NF == q) c->read_one(stage, rbuf, p, f);
+    }
+  };
+  struct NoExtra {
+    __device__ __forceinline__ void operator()(int) const {}
+  };
+
   // Pairs 0..2 of a k-step read from `rd` (pair 0 already in raw[0] and its
   // even half in u[0]): each prefetches the next chunk pair, runs its two
   // substeps and unpacks ahead. Leaves pair 3 in raw[1], its even half in u[0].
   __device__ __forceinline__ void pairs012(v16i (&acc)[T::TM][T::TN], const char* rd) {
+    if constexpr (T::SCHED == kSchedPin) {
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        const int cur = p & 1;
+        substep_spread<true>(acc, 0, 1, cur, 1, SpreadReads{this, rd, cur ^ 1, p + 1});
+        substep_spread<true>(acc, 1, 0, cur ^ 1, 0, NoExtra{});
+      }
+      return;
+    }
 #pragma unroll
     for (int p = 0; p < 3; ++p) {
       const int cur = p & 1;
@@ -251,11 +320,26 @@ __device__ __forceinline__ void dma_kstep_next(DmaCore<T>& c, v16i (&acc)[T::TM]
                                                __amdgpu_buffer_rsrc_t a_rsrc, const int (&voff_a)[T::A_INST],
                                                int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc, int ksteps,
                                                int kt) {
-  c.issue(dma, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, kt + 1);
-  c.read(rd, 0, 0);
-  if constexpr (T::SCHED == kSchedPin) __builtin_amdgcn_sched_barrier(0);
-  c.template substep<true, DmaCore<T>::NF>(acc, 0, 1, 1, 1);
-  c.template substep<true, 0>(acc, 1, 0, 0, 0);
+  if constexpr (T::SCHED == kSchedPin) {
+    // The DMA instructions and the reads of pair 0 ride on the MFMA slots of
+    // the previous k-step's last substep.
+    constexpr int INST = T::A_INST + T::B_INST, MF = DmaCore<T>::MF, NF = DmaCore<T>::NF;
+    auto extra = [&](int q) {
+#pragma unroll
+      for (int d = 0; d < INST; ++d)
+        if (d * MF / INST == q) c.issue_one(dma, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, kt + 1, d);
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+        if (f * MF / NF == q) c.read_one(rd, 0, 0, f);
+    };
+    c.template substep_spread<true>(acc, 0, 1, 1, 1, extra);
+    c.template substep_spread<true>(acc, 1, 0, 0, 0, typename DmaCore<T>::NoExtra{});
+  } else {
+    c.issue(dma, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, kt + 1);
+    c.read(rd, 0, 0);
+    c.template substep<true, DmaCore<T>::NF>(acc, 0, 1, 1, 1);
+    c.template substep<true, 0>(acc, 1, 0, 0, 0);
+  }
   c.pairs012(acc, rd);
   wait_vmcnt<0>();
   __syncthreads();

@@ -28,10 +28,15 @@
 
 namespace clef {
 
-template <int WM_, int WN_, int WAVES_M_, int WAVES_N_, int SCHED_ = kSchedFree>
+// SPLIT_B: the B tile is two panels of BN/2 rows from two buffers (rows
+// [0, BN/2) from b_rsrc, [BN/2, BN) from b_rsrc2), and wave wn takes columns
+// [wn * WN/2, +WN/2) of each half, so fragment j and j + TN/2 of a lane hold the
+// same output column of the two panels (fused gate/up).
+template <int WM_, int WN_, int WAVES_M_, int WAVES_N_, int SCHED_ = kSchedFree, bool SPLIT_B_ = false>
 struct DmaHTile {
   static constexpr int WM = WM_, WN = WN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
   static constexpr int SCHED = SCHED_;
+  static constexpr bool SPLIT_B = SPLIT_B_;
   static constexpr int NW = WAVES_M * WAVES_N;
   static constexpr int THREADS = 64 * NW;
   static constexpr int BM = WM * WAVES_M, BN = WN * WAVES_N;
@@ -39,6 +44,7 @@ struct DmaHTile {
   static_assert(WM % 32 == 0 && WN % 32 == 0 && BN % 128 == 0, "tile shape");
   static_assert(BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "whole DMA instructions per wave");
   static constexpr int TM = WM / 32, TN = WN / 32;
+  static_assert(!SPLIT_B_ || (TN % 2 == 0 && BN % 256 == 0), "split B: whole 128-row panels per half");
   static constexpr int A_INST = BM / (16 * NW);  // DMA instructions per wave per half-step
   static constexpr int B_INST = BN / (16 * NW);
   static constexpr int INST = A_INST + B_INST;
@@ -60,7 +66,8 @@ template <class T>
 struct DmaHCore {
   static constexpr int NF = T::TM + T::TN;
   static constexpr int MF = T::TM * T::TN;
-  int wave, voff_b, a_row, b_row;
+  int wave, voff_b, a_row;
+  int b_row[T::TN];
   int offs[2];
   uint4 raw[2][NF];
   v4i u[2][NF];
@@ -72,7 +79,12 @@ struct DmaHCore {
     const int h = lane >> 5, lr = lane & 31;
     voff_b = (lane >> 2) * 128 + dmah_chunk16(lane);
     a_row = (wm * T::WM + lr) * 64;
-    b_row = (wn * T::WN + lr) * 64;
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j) {
+      const int col = T::SPLIT_B ? (j < T::TN / 2 ? 0 : T::BN / 2) + wn * (T::WN / 2) + 32 * (j % (T::TN / 2))
+                                 : wn * T::WN + 32 * j;
+      b_row[j] = (col + lr) * 64;
+    }
 #pragma unroll
     for (int p = 0; p < 2; ++p) offs[p] = ((2 * h + p) ^ ((lr >> 2) & 3)) << 4;
   }
@@ -81,8 +93,11 @@ struct DmaHCore {
   // voff_a[ql]: the lane's row offset plus dmah_chunk16 (contiguous rows:
   // (lane / 4) * row_bytes + chunk with a_q_stride = row_bytes; gathered rows:
   // the row's offset in the whole buffer + chunk, a_q_stride = 0).
+  // SPLIT_B: B slots of the second half read b_rsrc2 (their panel's blocks
+  // counted from 0); the half a slot belongs to is fixed per slot index.
   __device__ __forceinline__ void issue(char* stage, __amdgpu_buffer_rsrc_t a_rsrc, const int (&voff_a)[T::A_INST],
-                                        int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc, int ksteps, int j) {
+                                        int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc,
+                                        __amdgpu_buffer_rsrc_t b_rsrc2, int ksteps, int j) {
     const int kt = j >> 1, half = (j & 1) * 32;
     char* sb = stage + T::A_BYTES;
 #pragma unroll
@@ -94,8 +109,15 @@ struct DmaHCore {
 #pragma unroll
     for (int ql = 0; ql < T::B_INST; ++ql) {
       const int q = wave + T::NW * ql;
-      const int blk = (16 * q) >> 7, row_in = (16 * q) & 127;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_ptr_t)(sb + q * 1024), 16, voff_b,
+      int blk = (16 * q) >> 7;
+      const int row_in = (16 * q) & 127;
+      bool second = false;
+      if constexpr (T::SPLIT_B) {
+        // q < NW * (ql + 1) and 16 q < 128 (ql + 1) * ...: the half follows from ql alone.
+        second = ql >= T::B_INST / 2;
+        blk -= second ? T::BN / 256 : 0;
+      }
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(second ? b_rsrc2 : b_rsrc, (lds_ptr_t)(sb + q * 1024), 16, voff_b,
                                                (blk * ksteps + kt) * 16384 + row_in * 128 + half, 0, 0);
     }
   }
@@ -108,7 +130,7 @@ struct DmaHCore {
       raw[buf][i] = *reinterpret_cast<const uint4*>(stage + a_row + i * 2048 + offs[p]);
 #pragma unroll
     for (int j = 0; j < T::TN; ++j)
-      raw[buf][T::TM + j] = *reinterpret_cast<const uint4*>(sb + b_row + j * 2048 + offs[p]);
+      raw[buf][T::TM + j] = *reinterpret_cast<const uint4*>(sb + b_row[j] + offs[p]);
   }
 
   __device__ __forceinline__ void unpack_one(int dst, int buf, int half, int f) {
@@ -154,21 +176,26 @@ struct DmaHCore {
 
 // Half-step bodies; as in gemm_dma.hpp, the stage being loaded and the
 // stage being read are distinct restrict pointers of one inlined call so that
-// the outstanding DMA is not drained by the reads.
+// the outstanding DMA is not drained by the reads. COMPUTE = false runs the
+// DMA and barrier schedule only (a wave whose rows are all past the end keeps
+// the workgroup's barriers without spending MFMA work on them).
 
 // Half-step 0: DMA of half-steps 0 and 1, pair 0 of half-step 0.
-template <class T>
+template <class T, bool COMPUTE>
 __device__ __forceinline__ void dmah_first(DmaHCore<T>& c, v16i (&acc)[T::TM][T::TN], char* __restrict__ rd,
                                            char* __restrict__ dma, __amdgpu_buffer_rsrc_t a_rsrc,
                                            const int (&voff_a)[T::A_INST], int a_q_stride,
-                                           __amdgpu_buffer_rsrc_t b_rsrc, int ksteps) {
-  c.issue(rd, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, 0);
-  c.issue(dma, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, 1);
+                                           __amdgpu_buffer_rsrc_t b_rsrc, __amdgpu_buffer_rsrc_t b_rsrc2,
+                                           int ksteps) {
+  c.issue(rd, a_rsrc, voff_a, a_q_stride, b_rsrc, b_rsrc2, ksteps, 0);
+  c.issue(dma, a_rsrc, voff_a, a_q_stride, b_rsrc, b_rsrc2, ksteps, 1);
   wait_vmcnt<T::INST>();
   __syncthreads();
-  c.read(rd, 0, 0);
-  c.unpack(0, 0, 0);
-  c.pair0(acc, rd);
+  if constexpr (COMPUTE) {
+    c.read(rd, 0, 0);
+    c.unpack(0, 0, 0);
+    c.pair0(acc, rd);
+  }
   wait_vmcnt<0>();
   __syncthreads();
 }
@@ -176,17 +203,20 @@ __device__ __forceinline__ void dmah_first(DmaHCore<T>& c, v16i (&acc)[T::TM][T:
 // Half-step j >= 1 reading `rd`: DMA of half-step j + 1 into `dma` (freed by
 // half-step j - 1), the last pair of half-step j - 1 (registers only), pair 0
 // of j; ends once half-step j + 1 has landed and every wave is done with `rd`.
-template <class T>
+template <class T, bool COMPUTE>
 __device__ __forceinline__ void dmah_next(DmaHCore<T>& c, v16i (&acc)[T::TM][T::TN], const char* __restrict__ rd,
                                           char* __restrict__ dma, __amdgpu_buffer_rsrc_t a_rsrc,
                                           const int (&voff_a)[T::A_INST], int a_q_stride,
-                                          __amdgpu_buffer_rsrc_t b_rsrc, int ksteps, int j) {
-  c.issue(dma, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, j + 1);
-  c.read(rd, 0, 0);
-  if constexpr (T::SCHED == kSchedPin) __builtin_amdgcn_sched_barrier(0);
-  c.template substep<true>(acc, 0, 1, 1, 1);
-  c.template substep<true>(acc, 1, 0, 0, 0);
-  c.pair0(acc, rd);
+                                          __amdgpu_buffer_rsrc_t b_rsrc, __amdgpu_buffer_rsrc_t b_rsrc2, int ksteps,
+                                          int j) {
+  c.issue(dma, a_rsrc, voff_a, a_q_stride, b_rsrc, b_rsrc2, ksteps, j + 1);
+  if constexpr (COMPUTE) {
+    c.read(rd, 0, 0);
+    if constexpr (T::SCHED == kSchedPin) __builtin_amdgcn_sched_barrier(0);
+    c.template substep<true>(acc, 0, 1, 1, 1);
+    c.template substep<true>(acc, 1, 0, 0, 0);
+    c.pair0(acc, rd);
+  }
   wait_vmcnt<0>();
   __syncthreads();
 }
@@ -196,23 +226,26 @@ __device__ __forceinline__ void dmah_next(DmaHCore<T>& c, v16i (&acc)[T::TM][T::
 // end (a range-checked buffer read: zeros, row padding or the next panel,
 // never a fault) into the stage that is not read again, drained by its
 // closing wait.
-template <class T>
+template <class T, bool COMPUTE = true>
 __device__ __forceinline__ void dmah_mainloop(__amdgpu_buffer_rsrc_t a_rsrc, const int (&voff_a)[T::A_INST],
-                                              int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc, int ksteps, char* lds,
+                                              int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc,
+                                              __amdgpu_buffer_rsrc_t b_rsrc2, int ksteps, char* lds,
                                               v16i (&acc)[T::TM][T::TN]) {
 #pragma unroll
   for (int i = 0; i < T::TM; ++i)
 #pragma unroll
     for (int j = 0; j < T::TN; ++j) acc[i][j] = v16i{};
   DmaHCore<T> c;
-  dmah_first<T>(c, acc, lds, lds + T::STAGE_BYTES, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps);
+  dmah_first<T, COMPUTE>(c, acc, lds, lds + T::STAGE_BYTES, a_rsrc, voff_a, a_q_stride, b_rsrc, b_rsrc2, ksteps);
   for (int j = 1; j < 2 * ksteps; ++j) {
     char* rd = lds + (j & 1) * T::STAGE_BYTES;
     char* dma = lds + ((j & 1) ^ 1) * T::STAGE_BYTES;
-    dmah_next<T>(c, acc, rd, dma, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, j);
+    dmah_next<T, COMPUTE>(c, acc, rd, dma, a_rsrc, voff_a, a_q_stride, b_rsrc, b_rsrc2, ksteps, j);
   }
-  c.template substep<true>(acc, 0, 1, 1, 1);
-  c.template substep<false>(acc, 1, 0, 0, 0);
+  if constexpr (COMPUTE) {
+    c.template substep<true>(acc, 0, 1, 1, 1);
+    c.template substep<false>(acc, 1, 0, 0, 0);
+  }
 }
 
 }  // namespace clef

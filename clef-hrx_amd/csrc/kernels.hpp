@@ -41,6 +41,13 @@ hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* a_scale
                             const int32_t* schedule, int64_t tokens, int topk, int k, int n,
                             int input_routed, uint16_t* out, hipStream_t stream);
 
+// Fused gate/up expert GEMMs with SwiGLU: h[route][c] = S1(E1(gate), E1(up)),
+// routed rows gathered from `a` by route / topk; n % 128 == 0.
+hipError_t launch_expert_gate_up(const uint32_t* a, int a_words, const float* as, const uint32_t* gate_w,
+                                 const float* gate_s, const uint32_t* up_w, const float* up_s, const float* groups,
+                                 const int32_t* schedule, int64_t tokens, int topk, int k, int n, uint16_t* h,
+                                 hipStream_t stream);
+
 hipError_t launch_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h,
                          hipStream_t stream);
 hipError_t launch_combine(const uint16_t* values, const float* routes, const float* order,

@@ -197,6 +197,24 @@ int clef_moe_expert_i4(const uint32_t* a, int32_t stride, const float* a_scales,
                        uint16_t* out, void* workspace, size_t workspace_bytes,
                        clef_stream_t stream);
 
+/* Fused gate/up expert GEMMs with SwiGLU: for every routed row r of every
+ * expert e, h[r][c] = bf16(bf16(g/(1+exp(-g))) * u) where g and u are the E1
+ * outputs (as clef_moe_expert_i4, input_routed = 0) of gate_w and up_w for
+ * column c. One pass over the gathered activation rows feeds both weight
+ * sets; h (bf16 [tokens*topk][n]) is bit-equal to clef_moe_expert_i4 twice
+ * followed by clef_swiglu. Replaces Engine::omni_gate_up (src/omni.rs:300-372)
+ * and benches/kernels/omni_gate_up_i4.loom. Workspace: as clef_moe_expert_i4.
+ * Preconditions: 1 <= tokens <= 1048576, 1 <= topk <= 128 -> "fused gate/up
+ * requires regular grouped routes"; k % 256 == 0, n % 128 == 0 (the tiled
+ * weight layout's 128-row panels; the reference accepts n % 64 == 0),
+ * stride >= k, stride % 32 == 0 and tokens * stride / 2 < 2 GiB ->
+ * "incompatible fused expert weights". */
+int clef_moe_expert_gate_up_i4(const uint32_t* a, int32_t stride, const float* a_scales,
+                               const uint32_t* gate_w, const float* gate_s, const uint32_t* up_w,
+                               const float* up_s, const float* groups, int64_t tokens, int32_t topk,
+                               int32_t k, int32_t n, uint16_t* h, void* workspace,
+                               size_t workspace_bytes, clef_stream_t stream);
+
 /* h = bf16(bf16(g/(1+exp(-g))) * u) elementwise over n values. Replaces
  * Engine::swiglu (src/ops.rs:9-29) and kernels/swiglu.loom. Precondition:
  * n >= 0 -> "SwiGLU shape/dtype mismatch". */

@@ -107,6 +107,18 @@ def test_expert_rejects(k, n, stride):
     assert rc == -1 and msg == "unsupported Omni expert tile shape"
 
 
+@pytest.mark.parametrize("k,n,stride,tokens,msg", [
+    (512, 96, 512, 4, "incompatible fused expert weights"),
+    (500, 128, 512, 4, "incompatible fused expert weights"),
+    (512, 128, 256, 4, "incompatible fused expert weights"),
+    (512, 128, 512, 0, "fused gate/up requires regular grouped routes"),
+])
+def test_gate_up_rejects(k, n, stride, tokens, msg):
+    rc, got = call("clef_moe_expert_gate_up_i4", FAKE, stride, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, tokens, 8, k, n,
+                   FAKE, FAKE, 1 << 20, None)
+    assert rc == -1 and got == msg
+
+
 def test_combine_rejects():
     rc, msg = call("clef_moe_combine", FAKE, FAKE, FAKE, 4, 12, 8, FAKE, None)
     assert rc == -1 and msg == "unsupported ordered Omni accumulation"

@@ -406,6 +406,38 @@ def test_expert_gemm_matches_oracle(tokens):
     assert_same_u16(bf16_host(got), want, "expert down")
 
 
+@pytest.mark.parametrize("tokens,wide", [(3, False), (64, False), (300, False), (300, True)])
+def test_expert_gate_up_swiglu_matches_oracle(tokens, wide):
+    """Fused gate/up + SwiGLU (Engine::omni_gate_up, src/omni.rs:300-372) equals
+    E1(gate), E1(up) then S1 of the oracle, bit for bit; inter = 512 gives four
+    128-column tiles and skewed routes leave experts empty, partial and
+    multi-tile."""
+    rng = np.random.default_rng(100 + tokens)
+    hidden, inter, topk = 512, 512, 8
+    routes = random_routes(rng, tokens, skew=2.0)
+    groups, _ = oracle.group_routes(routes)
+    x = randn_bf16(rng, (tokens, hidden))
+    sx = oracle.activation_stride(hidden)
+    ax_codes, ax_scales, _ = oracle.prepare(x, sx)
+    gw, gs = packed_experts(rng, inter, hidden)
+    uw, us = packed_experts(rng, inter, hidden)
+    if wide:
+        # gate scales over 82 decades: gate values from bf16 denormals to
+        # overflow, through every range the SiLU table covers and beyond it
+        gs = (10.0 ** rng.uniform(-44, 38, size=gs.shape)).astype(np.float32)
+    g = oracle.expert_i4(ax_codes, ax_scales, gw, gs, groups, tokens, topk, hidden, inter, False)
+    u = oracle.expert_i4(ax_codes, ax_scales, uw, us, groups, tokens, topk, hidden, inter, False)
+    want = oracle.swiglu(g, u)
+    got = clef_i4.omni_gate_up(dev_prepared(x, sx), dev_weight(gw, gs, 128 * inter, hidden),
+                               dev_weight(uw, us, 128 * inter, hidden), to_dev_f32(groups), tokens, topk)
+    if wide:
+        # overflowing gates meet zero up values (inf * 0): NaN payload signs
+        # differ between the host oracle and the GPU
+        assert_same_bf16_nan_aware(bf16_host(got), want, "fused gate/up swiglu, wide scales")
+    else:
+        assert_same_u16(bf16_host(got), want, "fused gate/up swiglu")
+
+
 def test_swiglu_every_bf16_gate():
     """swiglu_preserves_materialized_rounding (src/ops.rs:482-520) over all
     65536 gate bit patterns."""
