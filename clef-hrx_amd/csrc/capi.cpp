@@ -363,8 +363,8 @@ int clef_moe_layer(const uint16_t* x, const void* logits, int32_t logits_dtype, 
 #define CLEF_STEP(call) \
   if (int rc = hip_status(call)) return rc
   CLEF_STEP(clef::launch_route(logits, logits_dtype, tokens, experts, topk, routes, s));
-  CLEF_STEP(clef::launch_group_routes(routes, tokens, topk, groups, order, ws + l.group_ws, s));
-  CLEF_STEP(clef::launch_expert_schedule(groups, tokens, schedule, s));
+  CLEF_STEP(clef::launch_group_routes(routes, tokens, topk, groups, order, ws + l.group_ws, s, schedule,
+                                      clef::expert_tile_rows()));
   CLEF_STEP(clef::launch_prepare(x, tokens, hidden, sx, 4, ax, s));
   if (tokens * (int64_t)(sx / 8) * 4 < ((int64_t)1 << 31)) {
     // Gate and up share one pass over the gathered x rows and SwiGLU runs in

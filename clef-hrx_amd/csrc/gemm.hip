@@ -954,6 +954,7 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
 }
 
 int64_t expert_max_tiles(int64_t routes) { return (routes + kExpertBM - 1) / kExpertBM + 128; }
+int expert_tile_rows() { return kExpertBM; }
 
 namespace {
 template <class T, bool GU>

@@ -26,12 +26,17 @@ int gemm_config_count();
 hipError_t launch_route(const void* logits, int dtype, int64_t tokens, int experts, int topk,
                         float* routes, hipStream_t stream);
 size_t group_workspace_bytes(int64_t tokens);
+// With `schedule` non-NULL the scan also writes the grouped expert GEMM's tile
+// schedule (as launch_expert_schedule, tiles of schedule_bm slots).
 hipError_t launch_group_routes(const float* routes, int64_t tokens, int topk, float* groups,
-                               float* order, void* workspace, hipStream_t stream);
+                               float* order, void* workspace, hipStream_t stream,
+                               int32_t* schedule = nullptr, int schedule_bm = 0);
 hipError_t launch_expert_tasks(const float* groups, int64_t tokens, float* tasks,
                                hipStream_t stream);
 
-// Tile schedule of the grouped expert GEMM: int32 [1 + 2 * max_tiles].
+// Tile schedule of the grouped expert GEMM: int32 [1 + 2 * max_tiles], tiles
+// of expert_tile_rows() slots.
+int expert_tile_rows();
 int64_t expert_max_tiles(int64_t routes);
 size_t expert_schedule_bytes(int64_t routes);
 hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int32_t* schedule,

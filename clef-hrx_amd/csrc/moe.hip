@@ -57,43 +57,53 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
     }
   }
   float* out = routes + t * 2 * topk;
+  // Rank r is kept by lane r % 64 (slot r / 64): selected value and id.
+  float rv[2] = {0.0f, 0.0f};
+  int rid[2] = {0, 0};
   for (int r = 0; r < topk; ++r) {
     const float best = wave_max(__builtin_fmaxf(v[0], v[1]));
     int cand = kInvalidId;
     if (valid[1] && v[1] == best) cand = 2 * lane + 1;
     if (valid[0] && v[0] == best) cand = 2 * lane;
     const int id = wave_min(cand);
-    if (lane == 0) {
-      out[r] = (float)id;
-      out[topk + r] = best;
+    if (lane == (r & 63)) {
+      rv[r >> 6] = best;
+      rid[r >> 6] = id;
     }
     if (id == 2 * lane) v[0] = kNegMax;
     if (id == 2 * lane + 1) v[1] = kNegMax;
   }
-  if (lane == 0) {
-    const float vmax = out[topk];
-    float sum = 0.0f;
-    for (int j = 0; j < topk; ++j) {
-      const float p = cephes_expf(out[topk + j] - vmax);
-      out[topk + j] = p;
-      sum = sum + p;
+  // exp of every rank in parallel, the sum in rank order (as the reference's
+  // sequential loop), the divisions in parallel.
+  const float vmax = __shfl(rv[0], 0, 64);
+  float p[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) p[s] = 64 * s + lane < topk ? cephes_expf(rv[s] - vmax) : 0.0f;
+  float sum = 0.0f;
+  for (int r = 0; r < topk; ++r) sum = sum + __shfl(p[r >> 6], r & 63, 64);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int r = 64 * s + lane;
+    if (r < topk) {
+      out[r] = (float)rid[s];
+      out[topk + r] = bf16_round(p[s] / sum);
     }
-    for (int j = 0; j < topk; ++j) out[topk + j] = bf16_round(out[topk + j] / sum);
   }
 }
 
 // ---------------------------------------------------------------- grouping
 //
-// Three passes over blocks of 256 tokens (one token per thread):
-//   count:   per-wave 64-bit lane masks per expert (LDS atomic OR), block
-//            counts per expert -> workspace [blocks][128]
+// Three passes over blocks of 64 tokens (one wave, one token per lane):
+//   count:   64-bit lane mask per expert (LDS atomic OR), block counts per
+//            expert -> workspace [blocks][128]
 //   scan:    per expert, exclusive prefix over blocks; counts -> groups[e][0]
-//   scatter: rank of (t, r) within expert e = block prefix + earlier waves'
-//            counts + popcount of the wave mask below this lane
+//   scatter: rank of (t, r) within expert e = block prefix + popcount of the
+//            block's mask below this lane
 // Every position is computed, not claimed, so the lists are in ascending
-// token order exactly.
+// token order exactly. One-wave blocks give T/64 workgroups: enough to spread
+// the scattered writes over the whole GPU.
 
-constexpr int kGroupBlock = 256;
+constexpr int kGroupBlock = 64;
 
 // Expert id of route slot r, or -1 when the slot names no expert in 0..127
 // (the oracle compares (int32_t)id against each expert).
@@ -109,44 +119,45 @@ __device__ __forceinline__ bool last_slot(const float* rt, int topk, int r, int 
 }
 
 __device__ void build_masks(const float* __restrict__ routes, int64_t tokens, int topk,
-                            unsigned long long (*masks)[128], int* wave_counts /* [4][128] */) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int i = tid; i < 4 * 128; i += 256) (&masks[0][0])[i] = 0ull;
+                            unsigned long long* masks /* [128] */) {
+  const int lane = threadIdx.x;
+  masks[lane] = 0ull;
+  masks[64 + lane] = 0ull;
   __syncthreads();
-  const int64_t t = (int64_t)blockIdx.x * kGroupBlock + tid;
+  const int64_t t = (int64_t)blockIdx.x * kGroupBlock + lane;
   if (t < tokens) {
     const float* rt = routes + t * 2 * topk;
     for (int r = 0; r < topk; ++r) {
       const int e = route_expert(rt[r]);
-      if (e >= 0) atomicOr(&masks[wave][e], 1ull << lane);
+      if (e >= 0) atomicOr(&masks[e], 1ull << lane);
     }
   }
   __syncthreads();
-  for (int i = tid; i < 4 * 128; i += 256) wave_counts[i] = __popcll((&masks[0][0])[i]);
-  __syncthreads();
 }
 
-__global__ __launch_bounds__(256) void group_count_kernel(const float* __restrict__ routes,
-                                                          int64_t tokens, int topk,
-                                                          int* __restrict__ block_counts) {
-  __shared__ unsigned long long masks[4][128];
-  __shared__ int wave_counts[4 * 128];
-  build_masks(routes, tokens, topk, masks, wave_counts);
-  const int e = threadIdx.x;
-  if (e < 128) {
-    block_counts[(int64_t)blockIdx.x * 128 + e] =
-        wave_counts[e] + wave_counts[128 + e] + wave_counts[256 + e] + wave_counts[384 + e];
-  }
+__global__ __launch_bounds__(64) void group_count_kernel(const float* __restrict__ routes, int64_t tokens,
+                                                         int topk, int* __restrict__ block_counts) {
+  __shared__ unsigned long long masks[128];
+  build_masks(routes, tokens, topk, masks);
+  const int lane = threadIdx.x;
+  int* dst = block_counts + (int64_t)blockIdx.x * 128;
+  dst[lane] = __popcll(masks[lane]);
+  dst[64 + lane] = __popcll(masks[64 + lane]);
 }
 
 // One workgroup of 1024 threads: 8 threads per expert, each summing a
-// contiguous run of blocks, then an 8-way scan.
+// contiguous run of blocks, then an 8-way scan. With `schedule` non-NULL it
+// also writes the expert GEMM's tile list: [count] then (expert, first slot)
+// pairs, tiles of `bm` slots, experts ascending.
 __global__ __launch_bounds__(1024) void group_scan_kernel(int* __restrict__ block_counts, int64_t blocks,
-                                                          int64_t tokens, float* __restrict__ groups) {
+                                                          int64_t tokens, float* __restrict__ groups,
+                                                          int32_t* __restrict__ schedule, int bm) {
   __shared__ int part[8][128];
+  __shared__ int tiles_scan[128];
   const int e = threadIdx.x & 127, j = threadIdx.x >> 7;
   const int64_t per = (blocks + 7) / 8;
-  const int64_t b0 = j * per, b1 = b0 + per < blocks ? b0 + per : blocks;
+  const int64_t b0 = j * per < blocks ? j * per : blocks;
+  const int64_t b1 = b0 + per < blocks ? b0 + per : blocks;
   int sum = 0;
   for (int64_t b = b0; b < b1; ++b) sum += block_counts[b * 128 + e];
   part[j][e] = sum;
@@ -159,27 +170,75 @@ __global__ __launch_bounds__(1024) void group_scan_kernel(int* __restrict__ bloc
     run += c;
   }
   if (j == 7) groups[(int64_t)e * (tokens + 1)] = (float)run;
+  if (schedule == nullptr) return;
+  // run of thread j == 7 is expert e's count
+  int tiles = 0;
+  if (j == 7) {
+    tiles = (run + bm - 1) / bm;
+    tiles_scan[e] = tiles;
+  }
+  __syncthreads();
+  for (int off = 1; off < 128; off <<= 1) {
+    int v = 0;
+    if (j == 7 && e >= off) v = tiles_scan[e - off];
+    __syncthreads();
+    if (j == 7) tiles_scan[e] += v;
+    __syncthreads();
+  }
+  if (j == 7) {
+    const int start = tiles_scan[e] - tiles;
+    for (int t = 0; t < tiles; ++t) {
+      schedule[1 + 2 * (start + t)] = e;
+      schedule[2 + 2 * (start + t)] = t * bm;
+    }
+    if (e == 127) schedule[0] = tiles_scan[127];
+  }
 }
 
-__global__ __launch_bounds__(256) void group_scatter_kernel(const float* __restrict__ routes,
-                                                            int64_t tokens, int topk,
-                                                            const int* __restrict__ block_offsets,
-                                                            float* __restrict__ groups,
-                                                            float* __restrict__ order) {
-  __shared__ unsigned long long masks[4][128];
-  __shared__ int wave_counts[4 * 128];
-  build_masks(routes, tokens, topk, masks, wave_counts);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t t = (int64_t)blockIdx.x * kGroupBlock + tid;
+// KT > 0: topk == KT, the token's route ids held in registers; KT == 0: any
+// topk, read from memory.
+template <int KT>
+__global__ __launch_bounds__(64) void group_scatter_kernel(const float* __restrict__ routes, int64_t tokens,
+                                                           int topk, const int* __restrict__ block_offsets,
+                                                           float* __restrict__ groups, float* __restrict__ order) {
+  __shared__ unsigned long long masks[128];
+  build_masks(routes, tokens, topk, masks);
+  const int lane = threadIdx.x;
+  const int64_t t = (int64_t)blockIdx.x * kGroupBlock + lane;
   if (t >= tokens) return;
   const float* rt = routes + t * 2 * topk;
   const unsigned long long below = (1ull << lane) - 1ull;
+  const int* offsets = block_offsets + (int64_t)blockIdx.x * 128;
+  if constexpr (KT > 0) {
+    float id[KT];
+    int ex[KT];
+#pragma unroll
+    for (int r = 0; r < KT; ++r) {
+      id[r] = rt[r];
+      ex[r] = route_expert(id[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < KT; ++r) {
+      const int e = ex[r];
+      bool last = e >= 0;
+#pragma unroll
+      for (int q = r + 1; q < KT; ++q) last = last && ex[q] != e;
+      if (!last) continue;
+      const int rank = offsets[e] + __popcll(masks[e] & below);
+      groups[(int64_t)e * (tokens + 1) + 1 + rank] = (float)(t * KT + r);
+      if (order) {
+        int less = 0;
+#pragma unroll
+        for (int q = 0; q < KT; ++q) less += id[q] < (float)e ? 1 : 0;
+        order[t * KT + less] = (float)r;
+      }
+    }
+    return;
+  }
   for (int r = 0; r < topk; ++r) {
     const int e = route_expert(rt[r]);
     if (e < 0 || !last_slot(rt, topk, r, e)) continue;
-    int rank = block_offsets[(int64_t)blockIdx.x * 128 + e];
-    for (int w = 0; w < wave; ++w) rank += wave_counts[w * 128 + e];
-    rank += __popcll(masks[wave][e] & below);
+    const int rank = offsets[e] + __popcll(masks[e] & below);
     groups[(int64_t)e * (tokens + 1) + 1 + rank] = (float)(t * topk + r);
     if (order) {
       int less = 0;
@@ -273,12 +332,16 @@ size_t group_workspace_bytes(int64_t tokens) {
 }
 
 hipError_t launch_group_routes(const float* routes, int64_t tokens, int topk, float* groups,
-                               float* order, void* workspace, hipStream_t stream) {
+                               float* order, void* workspace, hipStream_t stream, int32_t* schedule,
+                               int schedule_bm) {
   const int64_t blocks = (tokens + kGroupBlock - 1) / kGroupBlock;
   int* counts = static_cast<int*>(workspace);
-  group_count_kernel<<<(unsigned)blocks, 256, 0, stream>>>(routes, tokens, topk, counts);
-  group_scan_kernel<<<1, 1024, 0, stream>>>(counts, blocks, tokens, groups);
-  group_scatter_kernel<<<(unsigned)blocks, 256, 0, stream>>>(routes, tokens, topk, counts, groups, order);
+  group_count_kernel<<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts);
+  group_scan_kernel<<<1, 1024, 0, stream>>>(counts, blocks, tokens, groups, schedule, schedule_bm);
+  if (topk == 8)
+    group_scatter_kernel<8><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts, groups, order);
+  else
+    group_scatter_kernel<0><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts, groups, order);
   return hipGetLastError();
 }
 

@@ -28,15 +28,23 @@ constexpr int kGroupLds = 16 * kPitch; // LDS floats per 256-column group
 
 struct PlainSource {
   const uint16_t* x;
-  __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
+  struct Raw {
+    u4 a, b;
+  };
+  __device__ __forceinline__ Raw fetch(int64_t row, int width, int col) const {
     const u4* p = reinterpret_cast<const u4*>(x + row * width + col);
-    u4 a = p[0], b = p[1];
-    uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    return Raw{p[0], p[1]};
+  }
+  __device__ __forceinline__ void convert(const Raw& r, float* v) const {
+    uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       v[2 * i] = bf16_lo(w[i]);
       v[2 * i + 1] = bf16_hi(w[i]);
     }
+  }
+  __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
+    convert(fetch(row, width, col), v);
   }
 };
 
@@ -45,17 +53,25 @@ struct PlainSource {
 struct SwigluSource {
   const uint16_t* gate;
   const uint16_t* up;
-  __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
+  struct Raw {
+    u4 ga, gb, ua, ub;
+  };
+  __device__ __forceinline__ Raw fetch(int64_t row, int width, int col) const {
     const u4* pg = reinterpret_cast<const u4*>(gate + row * width + col);
     const u4* pu = reinterpret_cast<const u4*>(up + row * width + col);
-    u4 ga = pg[0], gb = pg[1], ua = pu[0], ub = pu[1];
-    uint32_t g[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
-    uint32_t u[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+    return Raw{pg[0], pg[1], pu[0], pu[1]};
+  }
+  __device__ __forceinline__ void convert(const Raw& r, float* v) const {
+    uint32_t g[8] = {r.ga.x, r.ga.y, r.ga.z, r.ga.w, r.gb.x, r.gb.y, r.gb.z, r.gb.w};
+    uint32_t u[8] = {r.ua.x, r.ua.y, r.ua.z, r.ua.w, r.ub.x, r.ub.y, r.ub.z, r.ub.w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       v[2 * i] = swiglu1(bf16_lo(g[i]), bf16_lo(u[i]));
       v[2 * i + 1] = swiglu1(bf16_hi(g[i]), bf16_hi(u[i]));
     }
+  }
+  __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
+    convert(fetch(row, width, col), v);
   }
 };
 
@@ -74,18 +90,21 @@ __device__ __forceinline__ uint32_t pack_codes(const float* v, float inv, bool v
   constexpr int per = 32 / BITS;
   constexpr float qmax = BITS == 8 ? 127.0f : 7.0f;
   constexpr uint32_t mask = BITS == 8 ? 0xffu : 0xfu;
+  // Round to nearest even by adding 1.5 * 2^23: when valid, |v * inv| <= qmax
+  // (times 1 + 2^-22), so the sum lies in [2^23, 2^24), where the f32 spacing is
+  // 1 and the addend is even; the add then rounds exactly as rint does, and
+  // the integer n sits two's complement in the low mantissa bits (the addend's
+  // mantissa is 0x400000). Clamping the biased value to magic +- qmax is the
+  // clamp of n.
+  constexpr float magic = 12582912.0f;
   uint32_t word = 0;
 #pragma unroll
   for (int p = 0; p < per; ++p) {
-    float scaled = v[p] * inv;
-    float s = valid ? scaled : 0.0f;
-    float r = __builtin_rintf(s);
-    float lo = __builtin_fmaxf(r, -qmax);
-    float hi = __builtin_fminf(lo, qmax);
-    int code = (int)hi;
-    word |= ((uint32_t)code & mask) << (p * BITS);
+    float t = v[p] * inv + magic;
+    t = __builtin_fminf(__builtin_fmaxf(t, magic - qmax), magic + qmax);
+    word |= (as_uint(t) & mask) << (p * BITS);
   }
-  return word;
+  return valid ? word : 0u;
 }
 
 template <int P, int BITS, class Src>
@@ -200,14 +219,120 @@ __global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int
   }
 }
 
+// Rows of G <= 16 groups, as prepare_kernel<1> but persistent: a workgroup
+// walks row blocks (16 / G rows each) with a grid stride and fetches the next
+// block's inputs before rotating and packing the current one, so HBM latency
+// overlaps the work instead of being paid once per workgroup.
+template <int BITS, class Src>
+__global__ __launch_bounds__(256) void prepare_loop_kernel(Src src, int64_t rows, int width, int out_words,
+                                                           uint32_t* __restrict__ out) {
+  // 20 KiB: eight workgroups fill a CU's LDS. Each group's maximum goes to
+  // the padding float of its first LDS row, which the transposes never touch.
+  __shared__ __align__(16) float lds[16 * kGroupLds];
+  uint32_t* gmax = reinterpret_cast<uint32_t*>(lds) + 16;
+  const int tid = threadIdx.x;
+  const int lg = tid >> 4;
+  const int L = tid & 15;
+  const int G = width >> 8;
+  const int rows_per_block = 16 / G;
+  const int row_local = lg / G;
+  const int grp = lg - row_local * G;
+  const bool lane_on = row_local < rows_per_block;
+  const int64_t nblk = (rows + rows_per_block - 1) / rows_per_block;
+  float* buf = lds + lg * kGroupLds;
+  constexpr int per = 32 / BITS;
+  constexpr float qmax = BITS == 8 ? 127.0f : 7.0f;
+
+  int64_t blk = blockIdx.x;
+  typename Src::Raw raw{};
+  {
+    const int64_t row = blk * rows_per_block + row_local;
+    if (lane_on && row < rows) raw = src.fetch(row, width, grp * 256 + 16 * L);
+  }
+  for (; blk < nblk; blk += gridDim.x) {
+    const int64_t row = blk * rows_per_block + row_local;
+    const bool on = lane_on && row < rows;
+    float v[16];
+    if (on) {
+      src.convert(raw, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+    }
+    {
+      const int64_t nrow = (blk + gridDim.x) * rows_per_block + row_local;
+      if (lane_on && nrow < rows) raw = src.fetch(nrow, width, grp * 256 + 16 * L);
+    }
+    radix4x2(v);  // strides 1 and 4
+    float4* wrow = reinterpret_cast<float4*>(buf + L * kPitch);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) wrow[c] = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = buf[k * kPitch + L];
+    __syncthreads();
+    radix4x2(v);  // strides 16 and 64 (value k holds index L + 16k)
+    uint32_t mbits = 0;
+    if (on) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        uint32_t a = as_uint(v[k]) & 0x7fffffffu;
+        mbits = mbits > a ? mbits : a;
+      }
+    }
+    mbits = group_max16(mbits);
+    if (L == 0) gmax[lg * kGroupLds] = mbits;
+    __syncthreads();
+    uint32_t m = 0;
+    for (int g = 0; g < G; ++g) {
+      uint32_t o = gmax[((lane_on ? row_local : 0) * G + g) * kGroupLds];
+      m = m > o ? m : o;
+    }
+    const float mf = m >= 0x7f800000u ? __builtin_huge_valf() : as_float(m);
+    const float normal = mf * 0.0625f;
+    const float safe = __builtin_fmaxf(normal, 1e-30f);
+    const float scale = safe / qmax;
+    const bool valid = scale < __builtin_huge_valf();
+    const float inv = 0.0625f / scale;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) buf[k * kPitch + L] = v[k];
+    __syncthreads();
+    float nat[16];
+    const float4* rrow = reinterpret_cast<const float4*>(buf + L * kPitch);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float4 t = rrow[c];
+      nat[4 * c] = t.x;
+      nat[4 * c + 1] = t.y;
+      nat[4 * c + 2] = t.z;
+      nat[4 * c + 3] = t.w;
+    }
+    __syncthreads();
+    if (on) {
+      uint32_t* dst = out + row * out_words + (grp * 256 + 16 * L) / per;
+      if (BITS == 4) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(pack_codes<4>(nat, inv, valid), pack_codes<4>(nat + 8, inv, valid));
+      } else {
+        *reinterpret_cast<uint4*>(dst) = make_uint4(pack_codes<8>(nat, inv, valid), pack_codes<8>(nat + 4, inv, valid),
+                                                    pack_codes<8>(nat + 8, inv, valid),
+                                                    pack_codes<8>(nat + 12, inv, valid));
+      }
+      if (grp == 0 && L == 0) reinterpret_cast<float*>(out + rows * out_words)[row] = scale;
+    }
+  }
+}
+
 template <int BITS, class Src>
 hipError_t launch_prepare_bits(const Src& src, int64_t rows, int width, int out_words,
                                uint32_t* out, hipStream_t stream) {
   const int G = width / 256;
   if (G <= 16) {
     const int per_block = 16 / G;
-    const unsigned grid = (unsigned)((rows + per_block - 1) / per_block);
-    prepare_kernel<1, BITS, Src><<<grid, 256, 0, stream>>>(src, rows, width, out_words, out);
+    const int64_t blocks = (rows + per_block - 1) / per_block;
+    // Up to 8 resident workgroups per CU on 256 CUs; more row blocks than
+    // that are walked by the grid stride.
+    const unsigned grid = (unsigned)(blocks < 2048 ? blocks : 2048);
+    prepare_loop_kernel<BITS, Src><<<grid, 256, 0, stream>>>(src, rows, width, out_words, out);
   } else {
     const int passes = (G + 15) / 16;
     const unsigned grid = (unsigned)rows;
