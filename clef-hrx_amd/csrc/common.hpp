@@ -77,6 +77,18 @@ __device__ __forceinline__ int silu_lut_index(uint32_t gbits) {
   return e < (uint32_t)kSiluLutBinades ? (int)(((gbits >> 15) << 12) | (e << 7) | (gbits & 127u)) : -1;
 }
 
+// Byte offset in the table of the bf16 value held in the high half of w (low
+// half zero): 2 * silu_lut_index. Bits 28..30 of t = w - (kSiluLutExp0 << 23)
+// are zero exactly when the exponent field lies in the table's range, for
+// either sign; then t >> 15 holds (exponent - kSiluLutExp0) << 8 | mantissa << 1
+// in its low 13 bits and the sign bit moves to bit 13. Outside the range
+// `inside` is false and the offset is still within the 16 KiB table.
+__device__ __forceinline__ uint32_t silu_lut_offset(uint32_t w, bool& inside) {
+  const uint32_t t = w - ((uint32_t)kSiluLutExp0 << 23);
+  inside = (t & 0x70000000u) == 0;
+  return ((t >> 15) & 0x1FFFu) | ((w >> 18) & ~0x1FFFu);  // w >> 18 < 2^14: bit 13 is the sign
+}
+
 // One radix-4 stage of the reference rotation on a quad (a, b, c, d) taken at
 // stride s: s01=a+b, s23=c+d, d01=a-b, d23=c-d; a'=s01+d23, b'=s01-d23,
 // c'=d01+s23, d'=s23-d01. Separate f32 adds, no contraction.

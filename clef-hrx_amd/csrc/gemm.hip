@@ -842,6 +842,34 @@ __global__ __launch_bounds__(T::THREADS, 2) void expert_dmah_kernel(
     *reinterpret_cast<uint2*>(lds + row * RP + blk * 8) = make_uint2(p0, p1);
   };
   constexpr int JN = GU ? T::TN / 2 : T::TN;  // output fragments per lane row
+  // f32(acc) is 256 * dot exactly (dot has at most 17 significant bits).
+  // When every row and column scale of the tile is at least 2^-59, the row
+  // scale taken times 2^-8 gives RN(asr * w) * 2^-8 exactly (all normal), so
+  // RN(f32(acc) * RN(asr * 2^-8 * w)) = RN(dot * RN(asr * w)) and the shift
+  // by 8 is not needed; otherwise the shift path runs. Only the gate/up
+  // epilogue (two accumulators per output) gains more than the check costs.
+  bool fast = false;
+  if constexpr (GU) {
+    constexpr float kMinScale = 0x1p-59f;
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)  // rows past the group's end are never stored
+      ok = ok && (row0 + wm * T::WM + 32 * i + lr >= count || asr[i] >= kMinScale);
+    // each wave checks all of the tile's column scales (COLS per matrix)
+#pragma unroll
+    for (int c = lane; c < COLS; c += 64) {
+      ok = ok && *reinterpret_cast<const float*>(ws_lds + c * 4) >= kMinScale;
+      if constexpr (GU) ok = ok && *reinterpret_cast<const float*>(ws_lds + WS_SLOT + c * 4) >= kMinScale;
+    }
+    fast = __all(ok);
+  }
+  float asr8[T::TM];
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) asr8[i] = asr[i] * 0x1p-8f;
+  auto scaled = [&](int i, int jj, int r, float w) -> float {
+    const int a = acc[i][jj][r];
+    return fast ? (float)a * (asr8[i] * w) : (float)(a >> 8) * (asr[i] * w);
+  };
 #pragma unroll
   for (int j = 0; j < JN; ++j)
 #pragma unroll
@@ -855,37 +883,36 @@ __global__ __launch_bounds__(T::THREADS, 2) void expert_dmah_kernel(
 #pragma unroll
       for (int i = 0; i < T::TM; ++i)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) y[i][t] = (float)(acc[i][j][4 * q + t] >> 8) * (asr[i] * wg[t]);
+        for (int t = 0; t < 4; ++t) y[i][t] = scaled(i, j, 4 * q + t, wg[t]);
       if constexpr (GU) {
         // SiLU from the LDS table for all 4 * TM values at once (their reads
         // overlap), then one wave-uniform branch for the rare values outside
         // the table, computed directly.
-        const uint16_t* lut = reinterpret_cast<const uint16_t*>(lds + LUT_OFF);
         float act[T::TM][4];
+        bool inside[T::TM][4];
         bool slow = false;
 #pragma unroll
         for (int i = 0; i < T::TM; ++i)
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            y[i][t] = bf16_round(y[i][t]);
-            const int li = silu_lut_index(as_uint(y[i][t]) >> 16);
-            slow |= li < 0;
-            act[i][t] = bf16_to_f32(lut[li < 0 ? 0 : li]);
+            const uint32_t wb = pack_bf16x2(0.0f, y[i][t]);  // bf16(y) in the high half, low half zero
+            y[i][t] = as_float(wb);
+            const uint32_t off = silu_lut_offset(wb, inside[i][t]);
+            slow |= !inside[i][t];
+            act[i][t] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(lds + LUT_OFF + off));
           }
         if (__any(slow)) {
 #pragma unroll
           for (int i = 0; i < T::TM; ++i)
 #pragma unroll
             for (int t = 0; t < 4; ++t)
-              if (silu_lut_index(as_uint(y[i][t]) >> 16) < 0) act[i][t] = silu_bf16(y[i][t]);
+              if (!inside[i][t]) act[i][t] = silu_bf16(y[i][t]);
         }
+        // h = bf16(act * bf16(u)); the packing below rounds to bf16
 #pragma unroll
         for (int i = 0; i < T::TM; ++i)
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float u = bf16_round((float)(acc[i][j + JN][4 * q + t] >> 8) * (asr[i] * wu[t]));
-            y[i][t] = bf16_round(act[i][t] * u);
-          }
+          for (int t = 0; t < 4; ++t) y[i][t] = act[i][t] * bf16_round(scaled(i, j + JN, 4 * q + t, wu[t]));
       }
 #pragma unroll
       for (int i = 0; i < T::TM; ++i)
