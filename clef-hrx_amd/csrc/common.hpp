@@ -11,8 +11,12 @@ namespace clef {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned u4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float as_float(uint32_t u) { return __uint_as_float(u); }
-__device__ __forceinline__ uint32_t as_uint(float f) { return __float_as_uint(f); }
+// Host-and-device helpers: the SiLU table is generated on the host at build
+// time from the same steps (see silu_table_gen.cpp).
+#define CLEF_HD __host__ __device__ __forceinline__
+
+CLEF_HD float as_float(uint32_t u) { return __builtin_bit_cast(float, u); }
+CLEF_HD uint32_t as_uint(float f) { return __builtin_bit_cast(uint32_t, f); }
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -22,15 +26,15 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 // (scalar.fptrunc f32 to bf16). gfx950's v_cvt_pk_bf16_f32 computes exactly
 // this for every f32 bit pattern (checked exhaustively on the device), so the
 // conversion is one instruction per pair.
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+CLEF_HD uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
-__device__ __forceinline__ uint32_t f32_to_bf16(float f) { return pack_bf16x2(f, 0.0f) & 0xffffu; }
+CLEF_HD uint32_t f32_to_bf16(float f) { return pack_bf16x2(f, 0.0f) & 0xffffu; }
 
-__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return as_float(h << 16); }
+CLEF_HD float bf16_to_f32(uint32_t h) { return as_float(h << 16); }
 __device__ __forceinline__ float bf16_lo(uint32_t pair) { return as_float(pair << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t pair) { return as_float(pair & 0xffff0000u); }
-__device__ __forceinline__ float bf16_round(float f) { return as_float(pack_bf16x2(0.0f, f) & 0xffff0000u); }
+CLEF_HD float bf16_round(float f) { return as_float(pack_bf16x2(0.0f, f) & 0xffff0000u); }
 
 // exp(x) by Cody-Waite reduction with ln 2 split as 0.693359375 - 2.12194440e-4
 // and the degree-5 minimax polynomial of the Cephes expf (S. L. Moshier, Cephes
@@ -38,7 +42,7 @@ __device__ __forceinline__ float bf16_round(float f) { return as_float(pack_bf16
 // host restatement in the oracle produces the same bits. Stands in for the
 // reference's approximate expf<afn> (kernels/swiglu.loom:46,
 // kernels/omni_route.loom:131).
-__device__ __forceinline__ float cephes_expf(float x) {
+CLEF_HD float cephes_expf(float x) {
   if (x != x) return x;
   if (x > 88.72283935546875f) return __builtin_huge_valf();
   if (x < -103.972076416015625f) return 0.0f;
@@ -58,7 +62,7 @@ __device__ __forceinline__ float cephes_expf(float x) {
 }
 
 // The activation half of S1: bf16(g / (1 + exp(-g))). kernels/swiglu.loom:43-47.
-__device__ __forceinline__ float silu_bf16(float g) {
+CLEF_HD float silu_bf16(float g) {
   float e = cephes_expf(-g);
   float d = 1.0f + e;
   return bf16_round(g / d);

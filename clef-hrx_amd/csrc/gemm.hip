@@ -8,7 +8,6 @@
 // E1 (kernels/omni_expert_i4.loom:113-125, 436-462): for expert e and slot i,
 // route = groups[e][1+i], xr = input_routed ? route : route / topk,
 // out[route][c] = bf16(RN(f32(acc) * RN(as[xr] * ws[e*n + c]))), no clamp.
-#include <mutex>
 
 #include "gemm_core.hpp"
 #include "gemm_dma.hpp"
@@ -704,17 +703,13 @@ static_assert(ExpertDmaTile::BM == kExpertBM, "expert schedule tile height");
 // A wave whose 64 slots are all past the expert's count runs the DMA and
 // barrier schedule only. Work items, XCD chunking and the gathered A rows
 // are as in expert_dma_kernel.
-// silu_bf16 of the bf16 values tabulated by silu_lut_index (16 KiB), built
-// once per device by silu_lut_kernel with the same device arithmetic.
-__device__ uint16_t g_silu_lut[kSiluLutSize];
-
-__global__ __launch_bounds__(256) void silu_lut_kernel() {
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= kSiluLutSize) return;
-  const uint32_t bits = ((uint32_t)(idx >> 12) << 15) | ((uint32_t)(kSiluLutExp0 + ((idx >> 7) & 31)) << 7) |
-                        (uint32_t)(idx & 127);
-  g_silu_lut[idx] = (uint16_t)f32_to_bf16(silu_bf16(bf16_to_f32(bits)));
-}
+// silu_bf16 of the bf16 values tabulated by silu_lut_index (16 KiB). The
+// entries are generated at build time on the host by silu_table_gen.cpp from
+// the same host-and-device steps, so the table is part of the code object and
+// needs no set-up launch.
+__device__ const uint16_t g_silu_lut[kSiluLutSize] __attribute__((unused)) = {
+#include "silu_table.inc"
+};
 
 using ExpertHTile = DmaHTile<64, 128, 2, 2, kSchedFree, false>;
 using ExpertGUTile = DmaHTile<64, 128, 2, 2, kSchedFree, true>;
@@ -1005,25 +1000,6 @@ hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, c
 }
 }  // namespace
 
-namespace {
-// Builds g_silu_lut on the current device the first time it is needed. The
-// build waits for completion, so every later launch on any stream reads a
-// complete table (the first call therefore cannot be captured into a graph).
-hipError_t ensure_silu_lut(hipStream_t stream) {
-  static std::mutex mu;
-  static bool ready[256] = {};
-  int dev = 0;
-  if (hipError_t e = hipGetDevice(&dev)) return e;
-  if (dev < 0 || dev >= 256) return hipErrorInvalidDevice;
-  std::lock_guard<std::mutex> lock(mu);
-  if (ready[dev]) return hipSuccess;
-  silu_lut_kernel<<<(kSiluLutSize + 255) / 256, 256, 0, stream>>>();
-  if (hipError_t e = hipGetLastError()) return e;
-  if (hipError_t e = hipStreamSynchronize(stream)) return e;
-  ready[dev] = true;
-  return hipSuccess;
-}
-}  // namespace
 
 hipError_t launch_expert_gate_up(const uint32_t* a, int a_words, const float* as, const uint32_t* gate_w,
                                  const float* gate_s, const uint32_t* up_w, const float* up_s, const float* groups,
@@ -1031,7 +1007,6 @@ hipError_t launch_expert_gate_up(const uint32_t* a, int a_words, const float* as
                                  hipStream_t stream) {
   const int64_t a_bytes = tokens * a_words * 4;
   if (a_bytes >= ((int64_t)1 << 31) || n % 128 != 0) return hipErrorInvalidValue;
-  if (hipError_t e = ensure_silu_lut(stream)) return e;
   return launch_expert_dmah<ExpertGUTile, true>(a, a_words, a_bytes, as, gate_w, gate_s, up_w, up_s, groups,
                                                 schedule, tokens, topk, k, n, 0, h, stream);
 }

@@ -189,3 +189,19 @@ def test_precision_policy_mlp_projection_subset():
     assert backbone.precision(name, 4100, 1024) is None
     with pytest.raises(ValueError):
         clef_i4.QuantizedProjections.for_precision("int8")
+
+
+def test_silu_table_matches_oracle():
+    """The fused gate/up epilogue's SiLU table, generated on the host at build
+    time, equals bf16(silu(g)) of the oracle (kernels/swiglu.loom:43-47) for
+    every tabulated bf16 g."""
+    import numpy as np
+
+    import oracle
+    path = os.path.join(ROOT, "clef-hrx_amd", "_build", "silu_table.inc")
+    body = open(path).read().split("\n", 1)[1]
+    table = np.array([int(v, 16) for v in re.findall(r"0x[0-9a-f]{4}", body)], dtype=np.uint16)
+    idx = np.arange(8192)
+    g = (((idx >> 12) << 15) | ((102 + ((idx >> 7) & 31)) << 7) | (idx & 127)).astype(np.uint16)
+    assert len(table) == 8192
+    assert np.array_equal(table, oracle.swiglu(g, np.full(8192, 0x3F80, dtype=np.uint16)))
