@@ -33,6 +33,9 @@ SIGNATURES = {
     "clef_i4_prepared_words": (_I64, [_I64, _I32, _I32]),
     "clef_i4_prepare": (ctypes.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P]),
     "clef_i4_prepare_swiglu": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P]),
+    "clef_i4_prepare_attention_gate": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P]),
+    "clef_i4_prepare_norm_words": (_I64, [_I64, _I32, _I32, _I32, _I32]),
+    "clef_i4_prepare_norm": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P]),
     "clef_i4_retile": (ctypes.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P]),
     "clef_i4_pack_weight_workspace_bytes": (_SZ, [_I64, _I32, _I32]),
     "clef_i4_pack_weight": (ctypes.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _SZ, _P]),
@@ -133,7 +136,8 @@ class Prepared:
 
     @property
     def scales(self) -> torch.Tensor:
-        return self.storage[self.rows * self.words:].view(torch.float32)
+        start = self.rows * self.words
+        return self.storage[start: start + self.rows].view(torch.float32)
 
 
 def prepare(x: torch.Tensor, bits: int = 4, stride: int | None = None, out: torch.Tensor | None = None
@@ -158,6 +162,41 @@ def prepare_swiglu(gate: torch.Tensor, up: torch.Tensor, bits: int = 4, stride: 
     _check(lib().clef_i4_prepare_swiglu(_ptr(gate), _ptr(up), rows, width, stride, bits, _ptr(out),
                                         _stream()))
     return Prepared(out, rows, width, stride, bits)
+
+
+def prepare_attention_gate(attention: torch.Tensor, q_gate: torch.Tensor, bits: int = 4,
+                           stride: int | None = None) -> Prepared:
+    """prepare_attention_gate_with_source (src/quantized.rs:615-635): packs
+    bf16(attention * bf16(sigmoid(gate))), q_gate bf16 [rows][2*width]."""
+    rows, width = attention.shape
+    if tuple(q_gate.shape) != (rows, 2 * width) or q_gate.dtype != attention.dtype:
+        raise ClefError(-1, "packing input shape/dtype mismatch")
+    stride = activation_stride(width, bits) if stride is None else stride
+    words = int(lib().clef_i4_prepared_words(rows, stride, bits))
+    out = torch.zeros(max(words, 1), dtype=torch.int32, device=attention.device)
+    _check(lib().clef_i4_prepare_attention_gate(_ptr(attention), _ptr(q_gate), rows, width, stride, bits,
+                                                _ptr(out), _stream()))
+    return Prepared(out, rows, width, stride, bits)
+
+
+def prepare_norm(x: torch.Tensor, weight: torch.Tensor, bits: int = 4, stride: int | None = None,
+                 store: bool = False):
+    """prepare_norm[_store]_with_source (src/quantized.rs:687-779): named RMSNorm
+    (weight + 1, eps 1e-6) fused into the quantizer. Returns (Prepared,
+    normalized bf16 [rows][width] view of the same storage, or None)."""
+    rows, width = x.shape
+    if weight.numel() != width:
+        raise ClefError(-1, "unsupported normalized packing shape")
+    stride = activation_stride(width, bits) if stride is None else stride
+    total = int(lib().clef_i4_prepare_norm_words(rows, width, stride, bits, int(store)))
+    out = torch.zeros(max(total, 1), dtype=torch.int32, device=x.device)
+    _check(lib().clef_i4_prepare_norm(_ptr(x), _ptr(weight.contiguous()), rows, width, stride, bits, int(store),
+                                      _ptr(out), _stream()))
+    normalized = None
+    if store:
+        first = total - rows * width // 2
+        normalized = out[first:].view(torch.bfloat16).view(rows, width)
+    return Prepared(out, rows, width, stride, bits), normalized
 
 
 def retile_codes(codes: torch.Tensor, rows: int, cols: int, bits: int = 4) -> torch.Tensor:
@@ -289,6 +328,16 @@ def project_quantized(x: torch.Tensor, w: QuantizedWeight, residual: torch.Tenso
     _check(lib().clef_i4_project(_ptr(x), m, k, _ptr(w.codes), _ptr(w.scales), w.rows, _ptr(residual),
                                  _ptr(out), _ptr(ws), ws_bytes, _stream()))
     return out
+
+
+def project_attention_gate(attention: torch.Tensor, q_gate: torch.Tensor, w: QuantizedWeight,
+                           residual: torch.Tensor) -> torch.Tensor:
+    """Engine::project_attention_gate (src/quantized.rs:440-468): gated
+    attention packed in one pass, then the residual projection."""
+    if attention.shape[1] != w.cols:
+        raise ClefError(-1, "attention projection width mismatch")
+    a = prepare_attention_gate(attention, q_gate, w.bits, w.stride)
+    return project_prepared(a, w, residual=residual)
 
 
 # ---------------------------------------------------------------- MoE

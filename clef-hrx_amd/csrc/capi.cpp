@@ -88,6 +88,44 @@ int clef_i4_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t row
   return hip_status(clef::launch_prepare_swiglu(gate, up, rows, width, stride, bits, out, hs(stream)));
 }
 
+int clef_i4_prepare_attention_gate(const uint16_t* attention, const uint16_t* q_gate, int64_t rows,
+                                   int32_t width, int32_t stride, int32_t bits, uint32_t* out,
+                                   clef_stream_t stream) {
+  if (int rc = check_prepare(rows, width, stride, bits)) return rc;
+  if (!aligned(attention, 16) || !aligned(q_gate, 16) || !aligned(out, 16)) return fail(kAlign);
+  return hip_status(
+      clef::launch_prepare_attention_gate(attention, q_gate, rows, width, stride, bits, out, hs(stream)));
+}
+
+namespace {
+// Byte offset of the stored normalized rows: the packed words rounded up to
+// 128 bytes (src/quantized.rs:733-734).
+int64_t norm_offset_bytes(int64_t rows, int32_t stride, int32_t bits) {
+  return (prepared_words(rows, stride, bits) * 4 + 127) / 128 * 128;
+}
+}  // namespace
+
+int64_t clef_i4_prepare_norm_words(int64_t rows, int32_t width, int32_t stride, int32_t bits,
+                                   int32_t store) {
+  if ((bits != 4 && bits != 8) || rows < 0 || width < 0) return -1;
+  if (!store) return prepared_words(rows, stride, bits);
+  return norm_offset_bytes(rows, stride, bits) / 4 + rows * width / 2;
+}
+
+int clef_i4_prepare_norm(const uint16_t* x, const uint16_t* weight, int64_t rows, int32_t width,
+                         int32_t stride, int32_t bits, int32_t store, uint32_t* out,
+                         clef_stream_t stream) {
+  if (!(width == 5120 && (bits == 4 || bits == 8) && rows >= 1 && rows <= 1048576 && stride >= width &&
+        stride <= 65536 && stride % (512 / bits) == 0))
+    return fail("unsupported normalized packing shape");
+  if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(out, 16)) return fail(kAlign);
+  uint16_t* normalized =
+      store ? reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(out) + norm_offset_bytes(rows, stride, bits))
+            : nullptr;
+  return hip_status(
+      clef::launch_prepare_norm(x, weight, rows, width, stride, bits, out, normalized, hs(stream)));
+}
+
 int clef_i4_retile(const uint32_t* codes, int64_t rows, int32_t in_words, int32_t cols, int32_t bits,
                    uint32_t* tiled, clef_stream_t stream) {
   if (bits != 4 && bits != 8) return fail("unsupported packed weight shape for tiling");

@@ -13,6 +13,10 @@ hipError_t launch_prepare(const uint16_t* x, int64_t rows, int width, int stride
                           uint32_t* out, hipStream_t stream);
 hipError_t launch_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t rows, int width,
                                  int stride, int bits, uint32_t* out, hipStream_t stream);
+hipError_t launch_prepare_attention_gate(const uint16_t* x, const uint16_t* q_gate, int64_t rows, int width,
+                                         int stride, int bits, uint32_t* out, hipStream_t stream);
+hipError_t launch_prepare_norm(const uint16_t* x, const uint16_t* weight, int64_t rows, int width, int stride,
+                               int bits, uint32_t* out, uint16_t* normalized, hipStream_t stream);
 hipError_t launch_retile(const uint32_t* codes, int64_t rows, int in_words, int words,
                          uint32_t* tiled, hipStream_t stream);
 hipError_t launch_tile_permute(const uint16_t* src, int64_t rows, int cols, uint16_t* dst,

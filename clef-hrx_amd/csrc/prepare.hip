@@ -27,6 +27,7 @@ constexpr int kPitch = 20;            // floats per 16-value LDS row (80 bytes)
 constexpr int kGroupLds = 16 * kPitch; // LDS floats per 256-column group
 
 struct PlainSource {
+  static constexpr bool kRowNorm = false;
   const uint16_t* x;
   struct Raw {
     u4 a, b;
@@ -51,6 +52,7 @@ struct PlainSource {
 // S1 applied on load (kernels/prepare_integer_register.loom:155-172): the
 // rotation sees f32(bf16(swiglu)) exactly as if h had been materialized.
 struct SwigluSource {
+  static constexpr bool kRowNorm = false;
   const uint16_t* gate;
   const uint16_t* up;
   struct Raw {
@@ -72,6 +74,98 @@ struct SwigluSource {
   }
   __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
     convert(fetch(row, width, col), v);
+  }
+};
+
+// Attention output times its sigmoid gate, applied on load
+// (kernels/prepare_integer_register.loom:137-155): the gate of column c is
+// column (c/256)*512 + 256 + c%256 of the [rows][2*width] q_gate row, and the
+// value is bf16(x * bf16(1 / (1 + exp(-g)))).
+struct AttentionGateSource {
+  static constexpr bool kRowNorm = false;
+  const uint16_t* x;
+  const uint16_t* q_gate;
+  struct Raw {
+    u4 xa, xb, ga, gb;
+  };
+  __device__ __forceinline__ Raw fetch(int64_t row, int width, int col) const {
+    const u4* px = reinterpret_cast<const u4*>(x + row * width + col);
+    const int gcol = (col >> 8) * 512 + 256 + (col & 255);  // 16 values stay inside one 256-column half
+    const u4* pg = reinterpret_cast<const u4*>(q_gate + row * 2 * width + gcol);
+    return Raw{px[0], px[1], pg[0], pg[1]};
+  }
+  __device__ __forceinline__ static float gated(float x, float g) {
+    const float sig = bf16_round(1.0f / (1.0f + cephes_expf(-g)));
+    return bf16_round(x * sig);
+  }
+  __device__ __forceinline__ void convert(const Raw& r, float* v) const {
+    uint32_t a[8] = {r.xa.x, r.xa.y, r.xa.z, r.xa.w, r.xb.x, r.xb.y, r.xb.z, r.xb.w};
+    uint32_t g[8] = {r.ga.x, r.ga.y, r.ga.z, r.ga.w, r.gb.x, r.gb.y, r.gb.z, r.gb.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[2 * i] = gated(bf16_lo(a[i]), bf16_lo(g[i]));
+      v[2 * i + 1] = gated(bf16_hi(a[i]), bf16_hi(g[i]));
+    }
+  }
+  __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
+    convert(fetch(row, width, col), v);
+  }
+};
+
+// Named RMSNorm applied to a whole row before the rotation
+// (kernels/prepare_integer_register.loom:63-80, 112-134; weight offset 1,
+// eps 1e-6): inv = 1 / sqrt(ss / width + 1e-6) with ss summed in a fixed
+// order (per thread fma over its own values, group p then value i; a
+// butterfly over the wave's lanes at offsets 32..1; the four wave sums in wave
+// order), then r = fma(x * inv, w + 1, 0) rounded to bf16; the bf16 rows are
+// optionally stored to `normalized`. Used by the one-row-per-workgroup kernel.
+struct NormSource {
+  static constexpr bool kRowNorm = true;
+  const uint16_t* x;
+  const uint16_t* weight;
+  uint16_t* normalized;  // nullable
+  __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
+    PlainSource{x}.load16(row, width, col, v);
+  }
+  template <int P>
+  __device__ __forceinline__ void normalize(float (&v)[P][16], int64_t row, int width, int grp0, int L,
+                                            bool active, float* red) const {
+    const int G = width >> 8;
+    float acc = 0.0f;
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+      if (active && grp0 + 16 * p < G)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc = __builtin_fmaf(v[p][i], v[p][i], acc);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    const float ss = ((red[0] + red[1]) + red[2]) + red[3];
+    const float inv = 1.0f / __builtin_sqrtf(ss / (float)width + 1e-6f);
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int grp = grp0 + 16 * p;
+      if (!(active && grp < G)) continue;
+      const int col = grp * 256 + 16 * L;
+      const u4* pw = reinterpret_cast<const u4*>(weight + col);
+      const u4 wa = pw[0], wb = pw[1];
+      const uint32_t ww[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+      uint32_t hb[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float r0 = __builtin_fmaf(v[p][2 * i] * inv, bf16_lo(ww[i]) + 1.0f, 0.0f);
+        const float r1 = __builtin_fmaf(v[p][2 * i + 1] * inv, bf16_hi(ww[i]) + 1.0f, 0.0f);
+        hb[i] = pack_bf16x2(r0, r1);
+        v[p][2 * i] = bf16_lo(hb[i]);
+        v[p][2 * i + 1] = bf16_hi(hb[i]);
+      }
+      if (normalized) {
+        u4* dst = reinterpret_cast<u4*>(normalized + row * width + col);
+        dst[0] = u4{hb[0], hb[1], hb[2], hb[3]};
+        dst[1] = u4{hb[4], hb[5], hb[6], hb[7]};
+      }
+    }
   }
 };
 
@@ -131,17 +225,26 @@ __global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int
   float* buf = lds + lg * kGroupLds;
 
   float v[P][16];
-  uint32_t mbits = 0;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int grp = grp0 + 16 * p;
-    const bool on = active && grp < G;
-    if (on) {
+    if (active && grp < G) {
       src.load16(row, width, grp * 256 + 16 * L, v[p]);
     } else {
 #pragma unroll
       for (int i = 0; i < 16; ++i) v[p][i] = 0.0f;
     }
+  }
+  if constexpr (Src::kRowNorm) {
+    static_assert(P > 1, "row normalization needs one row per workgroup");
+    src.template normalize<P>(v, row, width, grp0, L, active, reinterpret_cast<float*>(gmax));
+    __syncthreads();  // gmax is reused for the row maximum below
+  }
+  uint32_t mbits = 0;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int grp = grp0 + 16 * p;
+    const bool on = active && grp < G;
     radix4x2(v[p]);  // strides 1 and 4
     float4* wrow = reinterpret_cast<float4*>(buf + L * kPitch);
 #pragma unroll
@@ -326,13 +429,14 @@ template <int BITS, class Src>
 hipError_t launch_prepare_bits(const Src& src, int64_t rows, int width, int out_words,
                                uint32_t* out, hipStream_t stream) {
   const int G = width / 256;
-  if (G <= 16) {
+  if (G <= 16 && !Src::kRowNorm) {
     const int per_block = 16 / G;
     const int64_t blocks = (rows + per_block - 1) / per_block;
     // Up to 8 resident workgroups per CU on 256 CUs; more row blocks than
     // that are walked by the grid stride.
     const unsigned grid = (unsigned)(blocks < 2048 ? blocks : 2048);
-    prepare_loop_kernel<BITS, Src><<<grid, 256, 0, stream>>>(src, rows, width, out_words, out);
+    if constexpr (!Src::kRowNorm)
+      prepare_loop_kernel<BITS, Src><<<grid, 256, 0, stream>>>(src, rows, width, out_words, out);
   } else {
     const int passes = (G + 15) / 16;
     const unsigned grid = (unsigned)rows;
@@ -421,6 +525,17 @@ hipError_t launch_prepare(const uint16_t* x, int64_t rows, int width, int stride
 hipError_t launch_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t rows, int width,
                                  int stride, int bits, uint32_t* out, hipStream_t stream) {
   return launch_prepare_src(SwigluSource{gate, up}, rows, width, stride, bits, out, stream);
+}
+
+hipError_t launch_prepare_attention_gate(const uint16_t* x, const uint16_t* q_gate, int64_t rows, int width,
+                                         int stride, int bits, uint32_t* out, hipStream_t stream) {
+  return launch_prepare_src(AttentionGateSource{x, q_gate}, rows, width, stride, bits, out, stream);
+}
+
+hipError_t launch_prepare_norm(const uint16_t* x, const uint16_t* weight, int64_t rows, int width, int stride,
+                               int bits, uint32_t* out, uint16_t* normalized, hipStream_t stream) {
+  if (width / 256 <= 16) return hipErrorInvalidValue;
+  return launch_prepare_src(NormSource{x, weight, normalized}, rows, width, stride, bits, out, stream);
 }
 
 hipError_t launch_retile(const uint32_t* codes, int64_t rows, int in_words, int words,

@@ -82,6 +82,41 @@ int clef_i4_prepare(const uint16_t* x, int64_t rows, int32_t width, int32_t stri
 int clef_i4_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t rows, int32_t width,
                            int32_t stride, int32_t bits, uint32_t* out, clef_stream_t stream);
 
+/* Attention output gated by the sigmoid of its query-gate half, fused into
+ * the quantizer: quantizes bf16(x * bf16(1 / (1 + exp(-g)))) where g for
+ * column c is column (c/256)*512 + 256 + c%256 of q_gate (bf16
+ * [rows][2*width]: query and gate share each 512-column head block).
+ * Replaces prepare_attention_gate_with_source / h3_prepare_attention_gate_i4
+ * (src/quantized.rs:440-468, 615-635; kernels/prepare_integer_register.loom:
+ * 137-155). Same preconditions as clef_i4_prepare. */
+int clef_i4_prepare_attention_gate(const uint16_t* attention, const uint16_t* q_gate, int64_t rows,
+                                   int32_t width, int32_t stride, int32_t bits, uint32_t* out,
+                                   clef_stream_t stream);
+
+/* Size in u32 words of clef_i4_prepare_norm's output: rows * (stride/(32/bits)
+ * + 1), plus, when store is nonzero, the padding to a 128-byte boundary and
+ * the bf16 normalized rows [rows][width] (src/quantized.rs:731-740). -1 for
+ * bits other than 4 and 8. */
+int64_t clef_i4_prepare_norm_words(int64_t rows, int32_t width, int32_t stride, int32_t bits,
+                                   int32_t store);
+
+/* Named RMSNorm (weight offset 1, eps 1e-6) fused into the quantizer:
+ * r = bf16(fma(x * inv, weight + 1, 0)) with inv = 1/sqrt(sum(x^2)/width +
+ * 1e-6), then Q1 of r. With store nonzero the bf16 rows r are also written
+ * after the packed codes and scales, at the first 128-byte boundary. Replaces
+ * prepare_norm_with_source / prepare_norm_store_with_source and
+ * h3_prepare_norm[_store]_i4/_i8 (src/quantized.rs:687-779;
+ * kernels/prepare_integer_register.loom:63-80, 112-134). The reference sums
+ * the squares in an order of its compiler's choosing and uses an approximate
+ * rsqrt; here the order is fixed (documented in csrc/prepare.hip) and sqrt
+ * and division are correctly rounded. Preconditions (src/quantized.rs:
+ * 721-731): width == 5120, bits in {4,8}, 1 <= rows <= 1048576, width <=
+ * stride <= 65536, stride % (512/bits) == 0 -> else "unsupported normalized
+ * packing shape". */
+int clef_i4_prepare_norm(const uint16_t* x, const uint16_t* weight, int64_t rows, int32_t width,
+                         int32_t stride, int32_t bits, int32_t store, uint32_t* out,
+                         clef_stream_t stream);
+
 /* Row-major packed codes [rows][in_words] -> tiled blocks, dropping padding.
  * Replaces quantized::retile_codes (src/quantized.rs:542-572) and
  * kernels/retile_codes.loom. Preconditions: rows % 128 == 0, words =

@@ -43,6 +43,9 @@ def lib() -> ctypes.CDLL:
             "orc_rotate256": (None, [_P]),
             "orc_prepare": (ctypes.c_int, [_P, _I64, _I32, _I32, _I32, _P]),
             "orc_prepare_swiglu": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P]),
+            "orc_prepare_attention_gate": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P]),
+            "orc_prepare_norm": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P]),
+            "orc_rms_norm": (ctypes.c_int, [_P, _P, _I64, _I32, _P]),
             "orc_retile": (ctypes.c_int, [_P, _I64, _I32, _I32, _I32, _P]),
             "orc_gemm_acc": (ctypes.c_int, [_P, _I32, _P, _I64, _I32, _I32, _I32, _P]),
             "orc_gemm": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _P]),
@@ -136,6 +139,41 @@ def prepare_swiglu(gate: np.ndarray, up: np.ndarray, stride: int, bits: int = 4)
     out = np.zeros(rows * (words + 1), dtype=np.uint32)
     _check(lib().orc_prepare_swiglu(_ptr(gate), _ptr(up), rows, width, stride, bits, _ptr(out)))
     return out[: rows * words].reshape(rows, words), out[rows * words:].view(np.float32), out
+
+
+def prepare_attention_gate(x: np.ndarray, q_gate: np.ndarray, stride: int, bits: int = 4):
+    """Q1 of bf16(x * bf16(sigmoid(gate))); q_gate is [rows][2*width]
+    (kernels/prepare_integer_register.loom:137-155)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    q_gate = np.ascontiguousarray(q_gate, dtype=np.uint16)
+    rows, width = x.shape
+    assert q_gate.shape == (rows, 2 * width)
+    words = stride // (32 // bits)
+    out = np.zeros(rows * (words + 1), dtype=np.uint32)
+    _check(lib().orc_prepare_attention_gate(_ptr(x), _ptr(q_gate), rows, width, stride, bits, _ptr(out)))
+    return out[: rows * words].reshape(rows, words), out[rows * words:].view(np.float32), out
+
+
+def prepare_norm(x: np.ndarray, weight: np.ndarray, stride: int, bits: int = 4):
+    """Q1 of the named RMSNorm (width 5120, weight + 1, eps 1e-6) ->
+    (codes, scales, storage, normalized bf16 [rows][5120])."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    weight = np.ascontiguousarray(weight, dtype=np.uint16)
+    rows, width = x.shape
+    words = stride // (32 // bits)
+    out = np.zeros(rows * (words + 1), dtype=np.uint32)
+    normalized = np.zeros((rows, width), dtype=np.uint16)
+    _check(lib().orc_prepare_norm(_ptr(x), _ptr(weight), rows, width, stride, bits, _ptr(out),
+                                  _ptr(normalized)))
+    return out[: rows * words].reshape(rows, words), out[rows * words:].view(np.float32), out, normalized
+
+
+def rms_norm(x: np.ndarray, weight: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    weight = np.ascontiguousarray(weight, dtype=np.uint16)
+    out = np.zeros_like(x)
+    _check(lib().orc_rms_norm(_ptr(x), _ptr(weight), x.shape[0], x.shape[1], _ptr(out)))
+    return out
 
 
 def retile(codes: np.ndarray, cols: int, bits: int = 4) -> np.ndarray:

@@ -21,6 +21,9 @@
  *   orc_swiglu        float64 SiLU within one bf16 step per rounding
  *   orc_combine       the reference's sparse MoE test formula
  *   orc_expf          float64 exp, <= 2 ulp
+ *   orc_prepare_attention_gate  Q1 of the float64-checked gate product (tests)
+ *   orc_prepare_norm  = Q1(orc_rms_norm) bit for bit; orc_rms_norm against a
+ *                     float64 RMSNorm within one bf16 step (tests)
  * exp bits: the reference uses expf<afn>, whose bits are those of the gfx1151
  * hardware approximation; orc_expf is the Cephes expf method (S. L. Moshier,
  * Cephes Math Library, expf.c), which the HIP kernels evaluate with the same
@@ -199,6 +202,124 @@ int orc_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t rows, i
         }
         free(h);
         free(v);
+    }
+    return 0;
+}
+
+/* Attention-gate producer then Q1 (kernels/prepare_integer_register.loom:137-155;
+ * src/quantized.rs:440-468, 626-635): the gate of column c is column
+ * (c/256)*512 + 256 + c%256 of the [rows][2*width] q_gate row (query and gate
+ * share each 512-column head block), s = bf16(1 / (1 + exp(-g))) and the
+ * packed value is bf16(x * s). */
+int orc_prepare_attention_gate(const uint16_t* x, const uint16_t* q_gate, int64_t rows, int32_t width,
+                               int32_t stride, int32_t bits, uint32_t* out) {
+    if (check_prepare(rows, width, stride, bits)) return -1;
+    const int64_t words = stride / (32 / bits);
+    float* scales = (float*)(out + rows * words);
+#pragma omp parallel
+    {
+        float* v = (float*)malloc(sizeof(float) * width);
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) {
+            for (int c = 0; c < width; ++c) {
+                const float g = orc_bf16_to_f32(q_gate[r * 2 * width + (c / 256) * 512 + 256 + c % 256]);
+                const float e = orc_expf(-g);
+                const float sig = bf16_round(1.0f / (1.0f + e));
+                v[c] = bf16_round(orc_bf16_to_f32(x[r * width + c]) * sig);
+            }
+            quantize_row(v, width, bits, out + r * words, &scales[r]);
+        }
+        free(v);
+    }
+    return 0;
+}
+
+/* Inverse RMS of one 5120-wide row in the fixed summation order of the fused
+ * producer kernel: thread t of 256 (group g = t/16 and g + 16, lane l = t%16)
+ * sums fma(x, x, acc) over columns g*256 + 16l .. +15 of each of its groups in
+ * turn; each 64-thread wave adds across lanes by the butterfly
+ * s[l] += s[l ^ o] for o = 32, 16, ..., 1; the four wave sums are added in wave
+ * order. The reference reduces in an order of its compiler's choosing
+ * (kernels/prepare_integer_register.loom:63-80: workgroup.reduce<addf>) and
+ * uses an approximate rsqrt; here inv = 1 / sqrt(ss / 5120 + 1e-6) with
+ * correctly rounded sqrt and division. */
+static float norm_row_inv(const uint16_t* x, int32_t width) {
+    float s[256];
+    const int groups = width / 256;
+    for (int t = 0; t < 256; ++t) {
+        const int g = t / 16, l = t % 16;
+        float acc = 0.0f;
+        for (int p = 0; p < 2; ++p) {
+            const int grp = g + 16 * p;
+            if (grp >= groups) continue;
+            for (int i = 0; i < 16; ++i) {
+                const float v = orc_bf16_to_f32(x[grp * 256 + 16 * l + i]);
+                acc = fmaf(v, v, acc);
+            }
+        }
+        s[t] = acc;
+    }
+    float wave[4];
+    for (int w = 0; w < 4; ++w) {
+        float* a = s + 64 * w;
+        for (int o = 32; o >= 1; o >>= 1) {
+            float b[64];
+            for (int l = 0; l < 64; ++l) b[l] = a[l] + a[l ^ o];
+            memcpy(a, b, sizeof(b));
+        }
+        wave[w] = a[0];
+    }
+    const float ss = ((wave[0] + wave[1]) + wave[2]) + wave[3];
+    const float var = ss / (float)width;
+    const float ve = var + 1e-6f;
+    return 1.0f / sqrtf(ve);
+}
+
+/* Named-RMSNorm producer then Q1 (kernels/prepare_integer_register.loom:63-80,
+ * 112-134; src/quantized.rs:713-779): width 5120, weight offset 1, eps 1e-6.
+ * n = x * inv, r = fma(n, w + 1, 0), the packed value is bf16(r); when
+ * normalized is not NULL the bf16 values are also written there ([rows][5120]). */
+int orc_prepare_norm(const uint16_t* x, const uint16_t* weight, int64_t rows, int32_t width,
+                     int32_t stride, int32_t bits, uint32_t* out, uint16_t* normalized) {
+    if (!(width == 5120 && (bits == 4 || bits == 8) && rows >= 1 && rows <= 1048576 && stride >= width &&
+          stride <= 65536 && stride % (512 / bits) == 0))
+        return fail("unsupported normalized packing shape");
+    const int64_t words = stride / (32 / bits);
+    float* scales = (float*)(out + rows * words);
+#pragma omp parallel
+    {
+        float* v = (float*)malloc(sizeof(float) * width);
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) {
+            const uint16_t* xr = x + r * width;
+            const float inv = norm_row_inv(xr, width);
+            for (int c = 0; c < width; ++c) {
+                const float n = orc_bf16_to_f32(xr[c]) * inv;
+                const float nw = orc_bf16_to_f32(weight[c]) + 1.0f;
+                const uint16_t h = orc_f32_to_bf16(fmaf(n, nw, 0.0f));
+                if (normalized) normalized[r * width + c] = h;
+                v[c] = orc_bf16_to_f32(h);
+            }
+            quantize_row(v, width, bits, out + r * words, &scales[r]);
+        }
+        free(v);
+    }
+    return 0;
+}
+
+/* Unfused named RMSNorm (kernels/norm.loom:57-95 without bias, weight offset
+ * 1): the same inverse RMS as orc_prepare_norm, out = bf16(fma(x * inv, w + 1, 0)).
+ * The fused producer must equal Q1 of this output. */
+int orc_rms_norm(const uint16_t* x, const uint16_t* weight, int64_t rows, int32_t width, uint16_t* out) {
+    if (width != 5120 || rows < 1) return fail("norm dimensions");
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint16_t* xr = x + r * width;
+        const float inv = norm_row_inv(xr, width);
+        for (int c = 0; c < width; ++c) {
+            const float n = orc_bf16_to_f32(xr[c]) * inv;
+            out[r * width + c] = orc_f32_to_bf16(fmaf(n, orc_bf16_to_f32(weight[c]) + 1.0f, 0.0f));
+        }
     }
     return 0;
 }

@@ -39,6 +39,15 @@ int orc_prepare(const uint16_t* x, int64_t rows, int32_t width, int32_t stride,
 /* Q1 after S1 (fused SwiGLU producer). */
 int orc_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t rows,
                        int32_t width, int32_t stride, int32_t bits, uint32_t* out);
+/* Q1 after the attention gate: x [rows][width], q_gate [rows][2*width]. */
+int orc_prepare_attention_gate(const uint16_t* x, const uint16_t* q_gate, int64_t rows,
+                               int32_t width, int32_t stride, int32_t bits, uint32_t* out);
+/* Q1 after the named RMSNorm (width 5120); normalized may be NULL. */
+int orc_prepare_norm(const uint16_t* x, const uint16_t* weight, int64_t rows, int32_t width,
+                     int32_t stride, int32_t bits, uint32_t* out, uint16_t* normalized);
+/* Named RMSNorm alone (weight offset 1, eps 1e-6, width 5120). */
+int orc_rms_norm(const uint16_t* x, const uint16_t* weight, int64_t rows, int32_t width,
+                 uint16_t* out);
 /* Q2: row-major packed codes -> 128x32-word tiles. */
 int orc_retile(const uint32_t* codes, int64_t rows, int32_t in_words,
                int32_t cols, int32_t bits, uint32_t* tiled);

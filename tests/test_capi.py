@@ -205,3 +205,30 @@ def test_silu_table_matches_oracle():
     g = (((idx >> 12) << 15) | ((102 + ((idx >> 7) & 31)) << 7) | (idx & 127)).astype(np.uint16)
     assert len(table) == 8192
     assert np.array_equal(table, oracle.swiglu(g, np.full(8192, 0x3F80, dtype=np.uint16)))
+
+
+@pytest.mark.parametrize("rows,width,stride,bits", [(4, 300, 384, 4), (0, 256, 256, 4), (4, 256, 200, 4),
+                                                    (4, 256, 256, 5)])
+def test_prepare_attention_gate_rejects(rows, width, stride, bits):
+    rc, msg = call("clef_i4_prepare_attention_gate", FAKE, FAKE, rows, width, stride, bits, FAKE, None)
+    assert rc == -1 and msg == "unsupported rotated integer operand"
+
+
+@pytest.mark.parametrize("rows,width,stride,bits", [(4, 4096, 4224, 4), (0, 5120, 5248, 4), (4, 5120, 5000, 4),
+                                                    (4, 5120, 5248, 5), (4, 5120, 5136, 4), (4, 5120, 70000, 4)])
+def test_prepare_norm_rejects(rows, width, stride, bits):
+    """src/quantized.rs:721-731: width 5120 only."""
+    rc, msg = call("clef_i4_prepare_norm", FAKE, FAKE, rows, width, stride, bits, 0, FAKE, None)
+    assert rc == -1 and msg == "unsupported normalized packing shape"
+
+
+def test_prepare_norm_storage_layout():
+    """Normalized rows start at the packed words rounded up to 128 bytes
+    (src/quantized.rs:731-740)."""
+    f = clef_i4.lib().clef_i4_prepare_norm_words
+    for rows, stride, bits in [(1, 5248, 4), (7, 5248, 4), (129, 5184, 8)]:
+        packed = rows * (stride // (32 // bits) + 1)
+        assert f(rows, 5120, stride, bits, 0) == packed
+        offset = -(-packed * 4 // 128) * 128
+        assert f(rows, 5120, stride, bits, 1) == offset // 4 + rows * 2560
+    assert f(4, 5120, 5248, 5, 0) == -1

@@ -464,3 +464,122 @@ def test_checkpoint_tiles_round_trip():
                 base = tile * 256 * cols + (ks * 256 + r) * 64
                 assert np.array_equal(flat[base:base + 64], w[tile * 256 + r, ks * 64:(ks + 1) * 64])
     assert np.array_equal(oracle.untile_rows(t), w)
+
+
+# ---------------------------------------------------------------- fused producers
+
+def norm_test_rows(rows: int, width: int = 5120) -> np.ndarray:
+    """Input rows of the reference's fused-norm packing test
+    (src/quantized.rs:1567-1598): eleven row classes cycling (+-0, tiny,
+    bf16::MAX, the smallest denormal, 1e15 scale, NaN / +Inf / -Inf at one
+    column, +-1, 1e-3 scale, the plain formula)."""
+    i = np.arange(rows * width, dtype=np.int64)
+    c = i % width
+    value = ((i * 37 % 1031).astype(np.float32) - 515.0) / 37.0
+    cls = (i // width) % 11
+    v = value.copy()
+    v[cls == 0] = np.where(c[cls == 0] % 2 == 0, 0.0, -0.0)
+    v[cls == 1] = value[cls == 1] * np.float32(1e-5)
+    v[cls == 2] = F(np.array([0x7F7F], dtype=np.uint16))[0]
+    v[cls == 3] = F(np.array([0x0001], dtype=np.uint16))[0]
+    v[cls == 4] = value[cls == 4] * np.float32(1e15)
+    v[(cls == 5) & (c == 37)] = np.nan
+    v[(cls == 6) & (c == 113)] = np.inf
+    v[(cls == 7) & (c == 259)] = -np.inf
+    v[cls == 8] = np.where(c[cls == 8] % 2 == 0, 1.0, -1.0)
+    v[cls == 9] = value[cls == 9] * np.float32(1e-3)
+    return BF(v.astype(np.float32)).reshape(rows, width)
+
+
+def norm_test_weight(width: int = 5120, exceptional: bool = False) -> np.ndarray:
+    """Weight row of the same test (row 2 of its 3-row buffer)."""
+    i = np.arange(3 * width)[2 * width:]
+    if exceptional:
+        m = i % 1009
+        w = np.where(m == 0, np.nan, np.where(m == 1, np.inf, np.where(m == 2, -np.inf, np.where(
+            m == 3, float(F(np.array([0x7F7F], dtype=np.uint16))[0]), 0.5))))
+    else:
+        m = i % 19
+        w = np.where(m == 0, -1.0, np.where(m == 1, -0.0, np.where(m == 2, 0.0, ((i * 13 % 127) - 63.0) / 128.0)))
+    return BF(w.astype(np.float32))
+
+
+def bf16_ulps(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Distance in bf16 steps along the ordered bit line."""
+    def ordered(h):
+        h = h.astype(np.int64)
+        return np.where(h & 0x8000, 0x8000 - (h & 0x7FFF), 0x8000 + h)
+    return np.abs(ordered(a) - ordered(b))
+
+
+@pytest.mark.parametrize("exceptional", [False, True])
+def test_rms_norm_within_one_bf16_step_of_float64(exceptional):
+    """The named RMSNorm (weight + 1, eps 1e-6) against float64 arithmetic: at
+    most one bf16 step apart wherever the float64 value is finite, the
+    reference test's own bound for normalized values (src/quantized.rs:1706-1716)."""
+    x = norm_test_rows(33)
+    w = norm_test_weight(exceptional=exceptional)
+    got = oracle.rms_norm(x, w)
+    xf = F(x).astype(np.float64)
+    with np.errstate(all="ignore"):
+        inv = 1.0 / np.sqrt(np.mean(xf * xf, axis=1, keepdims=True) + 1e-6)
+        want = BF((xf * inv * (F(w).astype(np.float64) + 1.0)).astype(np.float32))
+    wf = F(want)
+    # rows whose f32 sum of squares overflows (bf16::MAX rows) have inv = 0 in
+    # f32 arithmetic, as in the reference kernels, and normalize to zeros
+    overflow = np.isfinite(xf).all(axis=1) & (np.sum(xf * xf, axis=1) > np.finfo(np.float32).max)
+    wfin = np.isfinite(F(w))
+    assert overflow.any() and (F(got[overflow][:, wfin]) == 0).all()
+    fin = np.isfinite(wf) & ~overflow[:, None]
+    assert (bf16_ulps(got[fin], want[fin]) <= 1).all()
+    # non-finite float64 results stay non-finite (NaN where float64 is NaN)
+    assert np.isnan(F(got)[np.isnan(wf) & ~overflow[:, None]]).all()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_prepare_norm_is_quantizer_of_the_norm(bits):
+    """Fused RMSNorm packing equals Q1 of the separately normalized rows, code
+    for code and scale for scale, and stores those normalized rows: the
+    reference test's check 'storing normalization changed packed codes'
+    (src/quantized.rs:1664-1676) and its fused-vs-unfused comparison."""
+    x = norm_test_rows(22)
+    w = norm_test_weight()
+    stride = 5120 + 512 // bits
+    codes, scales, _, normalized = oracle.prepare_norm(x, w, stride, bits)
+    assert np.array_equal(normalized, oracle.rms_norm(x, w))
+    want_codes, want_scales, _ = oracle.prepare(normalized, stride, bits)
+    assert np.array_equal(codes[:, : 5120 * bits // 32], want_codes[:, : 5120 * bits // 32])
+    assert np.array_equal(scales.view(np.uint32), want_scales.view(np.uint32))
+    # rows holding NaN or +-Inf give zero codes and an infinite scale
+    bad = ~np.isfinite(F(x)).all(axis=1)
+    assert np.isinf(scales[bad]).all() and not codes[bad, : 5120 * bits // 32].any()
+    # an all-zero row normalizes to zeros (inv = 1 / sqrt(1e-6))
+    assert not normalized[0].any() or (F(normalized[0]) == 0).all()
+
+
+def test_prepare_norm_rejects_other_widths():
+    x = np.zeros((2, 4096), dtype=np.uint16)
+    with pytest.raises(oracle.OracleError, match="unsupported normalized packing shape"):
+        oracle.prepare_norm(x, np.zeros(4096, dtype=np.uint16), 4224)
+
+
+@pytest.mark.parametrize("width", [256, 768, 2048])
+def test_prepare_attention_gate_closed_forms(width):
+    """Attention-gate packing (kernels/prepare_integer_register.loom:137-155):
+    the gate of column c sits at (c/256)*512 + 256 + c%256 of the doubled row.
+    Gates of +100 give sigmoid 1 (x itself), 0 gives exactly 1/2 (x/2), -100
+    gives bf16 0; the query halves hold NaN, so reading a wrong column would
+    turn every row invalid."""
+    rng = np.random.default_rng(width)
+    rows = 5
+    x = BF(rng.standard_normal((rows, width)).astype(np.float32))
+    stride = oracle.activation_stride(width)
+    for gate, expect in ((100.0, x), (0.0, BF(F(x) * np.float32(0.5))),
+                         (-100.0, np.zeros_like(x))):
+        q = np.full((rows, 2 * width), 0x7FC0, dtype=np.uint16)  # NaN
+        for h in range(width // 256):
+            q[:, 512 * h + 256: 512 * h + 512] = BF(np.float32(gate))
+        got = oracle.prepare_attention_gate(x, q, stride)
+        want = oracle.prepare(expect, stride)
+        assert np.array_equal(got[0][:, : width // 8], want[0][:, : width // 8]), gate
+        assert np.array_equal(got[1].view(np.uint32), want[1].view(np.uint32)), gate
