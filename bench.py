@@ -46,7 +46,7 @@ def parse():
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=600)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--only", choices=["gemm", "moe", "mlp", "copy"], default=None,
+    p.add_argument("--only", choices=["gemm", "moe", "mlp", "i8", "copy"], default=None,
                    help="run one leg; 'copy' is a plain 512 MiB device copy, the known-size "
                         "kernel that scales HBM byte counters")
     return p.parse_args()
@@ -94,6 +94,22 @@ def gemm_leg(args):
     nbytes = m * k // 2 + 4 * m + n * k // 2 + 4 * n + 2 * m * n
     return {"m": m, "n": n, "k": k, "ms": ms, "tops": ops / ms / 1e9, "prepare_ms": prep_ms,
             "ops": ops, "bytes": nbytes}
+
+
+def i8_leg(args):
+    """INT8 x INT8 projection at the headline shape (h3_gemm_i8_256 path)."""
+    import torch
+
+    import clef_i4
+
+    m, k, n = 4096, 4096, 12288
+    x = bf16_randn((m, k), 1.0, 1002 * 16 + 0)
+    w = bf16_randn((n, k), 0.02, 1002 * 16 + 1)
+    qw = clef_i4.load_quantized_weight(w, bits=8)
+    a = clef_i4.prepare(x, bits=8)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    ms = timed(lambda: clef_i4.project_prepared(a, qw, out=out), max(1, args.steps // 4), args.warmup // 4)
+    return {"ms": ms, "tops": 2.0 * m * n * k / ms / 1e9}
 
 
 def mlp_leg(args):
@@ -222,6 +238,8 @@ def main():
         res["moe"] = moe_leg(args)
     if args.only in (None, "mlp"):
         res["mlp"] = mlp_leg(args)
+    if args.only in (None, "i8"):
+        res["i8"] = i8_leg(args)
     if args.only == "copy":
         c = copy_leg(args)
         print(json.dumps({"copy_bytes": c["bytes"], "copy_ms": round(c["ms"], 4),
@@ -261,6 +279,9 @@ def main():
     if "mlp" in res:
         line["mlp_block_ms"] = round(res["mlp"]["ms"], 4)
         line["mlp_tops"] = round(res["mlp"]["tops"], 1)
+    if "i8" in res:
+        line["int8_gemm_ms"] = round(res["i8"]["ms"], 4)
+        line["int8_gemm_tops"] = round(res["i8"]["tops"], 1)
     if cpu:
         line["cpu_baseline"] = cpu
         if "moe" in res:

@@ -44,6 +44,7 @@ SIGNATURES = {
     "clef_i4_gemm": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P]),
     "clef_i4_gemm_config": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I64, _I32, _I32, _P, _P, _I32, _P]),
     "clef_i4_gemm_configs": (ctypes.c_int, []),
+    "clef_i8_gemm": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P]),
     "clef_i4_project_workspace_bytes": (_SZ, [_I64, _I32]),
     "clef_i4_project": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _I32, _P, _P, _P, _SZ, _P]),
     "clef_moe_route": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _P, _P]),
@@ -312,6 +313,12 @@ def project_prepared(a: Prepared, w: QuantizedWeight, residual: torch.Tensor | N
     """Engine::project_prepared (src/quantized.rs:470-537)."""
     if out is None:
         out = _empty((a.rows, w.rows), torch.bfloat16, a.storage.device)
+    if a.bits != w.bits:
+        raise ClefError(-1, "unsupported integer projection shape")
+    if w.bits == 8:  # h3_gemm_i8_256
+        _check(lib().clef_i8_gemm(_ptr(a.storage), a.stride, _ptr(a.scales), _ptr(w.codes), _ptr(w.scales),
+                                  a.rows, w.rows, w.cols, _ptr(residual), _ptr(out), _stream()))
+        return out
     _check(lib().clef_i4_gemm_config(_ptr(a.storage), a.stride, _ptr(a.scales), _ptr(w.codes),
                                      _ptr(w.scales), a.rows, w.rows, w.cols, _ptr(residual), _ptr(out),
                                      config, _stream()))

@@ -201,6 +201,18 @@ int clef_i4_gemm(const uint32_t* a, int32_t k_stride, const float* a_scales, con
                              stream);
 }
 
+int clef_i8_gemm(const uint32_t* a, int32_t k_stride, const float* a_scales, const uint32_t* w_tiled,
+                 const float* w_scales, int64_t m, int32_t n, int32_t k, const uint16_t* residual,
+                 uint16_t* out, clef_stream_t stream) {
+  if (int rc = check_gemm(m, n, k, k_stride)) return rc;
+  if (k_stride % 64 != 0) return fail("unsupported integer projection shape");
+  if (!aligned(a, 16) || !aligned(w_tiled, 16) || !aligned(w_scales, 16) || !aligned(out, 16) ||
+      (residual && !aligned(residual, 16)))
+    return fail(kAlign);
+  return hip_status(
+      clef::launch_gemm_i8(a, k_stride / 4, a_scales, w_tiled, w_scales, m, n, k, residual, out, hs(stream)));
+}
+
 size_t clef_i4_project_workspace_bytes(int64_t m, int32_t k) {
   if (m < 0 || k < 0) return 0;
   return align256((size_t)prepared_words(m, stride_for(k, 4), 4) * 4);

@@ -21,8 +21,9 @@ namespace {
 
 constexpr float kBf16Max = 3.3895313892515355e38f;
 
+template <int SHIFT = 8>
 __device__ __forceinline__ uint32_t g1_value(int32_t acc, float ws, float as) {
-  float y = (float)(acc >> 8) * ws;
+  float y = (float)(acc >> SHIFT) * ws;
   y = y * as;
   y = y + 0.0f;
   float sat = __builtin_fmaxf(__builtin_fminf(y, kBf16Max), -kBf16Max);
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(256) void gemm_i4_kernel(
 // Stores: each wave stages its WM x WN bf16 tile in LDS (free after the main
 // loop; 8-byte blocks XOR-swizzled by row) and writes it back as 16-byte row
 // chunks, 8 lanes per 128-byte line; the residual is added on that pass.
-template <class T, bool RESID>
+template <class T, bool RESID, int SHIFT = 8>
 __device__ __forceinline__ void dense_epilogue(const v16i (&acc)[T::TM][T::TN], const float* __restrict__ as,
                                                const float* __restrict__ ws, int64_t M, int N, int K,
                                                int64_t m0, int n0, const uint16_t* __restrict__ residual,
@@ -120,6 +121,10 @@ __device__ __forceinline__ void dense_epilogue(const v16i (&acc)[T::TM][T::TN], 
   const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
   const int h = lane >> 5, lr = lane & 31;
   const float inf = __builtin_huge_valf();
+  // acc holds 2^SHIFT * dot: 256 * dot for INT4 (16 * code bytes), the dot
+  // itself for INT8. |dot| <= qmax^2 * K; the bound keeps a factor 2 margin.
+  constexpr float kShiftScale = (float)(1 << SHIFT), kUnshift = 1.0f / kShiftScale;
+  constexpr float kProdBound = SHIFT == 8 ? 98.0f : 32258.0f;
 
   float asr[T::TM];
   float mas = 0.0f;
@@ -142,12 +147,12 @@ __device__ __forceinline__ void dense_epilogue(const v16i (&acc)[T::TM][T::TN], 
       const float w4[4] = {wsr[j][q].x, wsr[j][q].y, wsr[j][q].z, wsr[j][q].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        exact = exact && (w4[e] * 0.00390625f) * 256.0f == w4[e];
+        exact = exact && (w4[e] * kUnshift) * kShiftScale == w4[e];
         const float a = __builtin_fabsf(w4[e]);
         mws = __builtin_fmaxf(mws, a < inf ? a : 0.0f);
       }
     }
-  const bool fast = __all(exact && mws * mas * (98.0f * (float)K) < kBf16Max);
+  const bool fast = __all(exact && mws * mas * (kProdBound * (float)K) < kBf16Max);
 
   // All waves are done reading the pipeline stages before LDS is reused.
   __syncthreads();
@@ -171,15 +176,15 @@ __device__ __forceinline__ void dense_epilogue(const v16i (&acc)[T::TM][T::TN], 
           float y[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            y[e] = (float)acc[i][j][4 * q + e] * (w4[e] * 0.00390625f);
+            y[e] = (float)acc[i][j][4 * q + e] * (w4[e] * kUnshift);
             y[e] = y[e] * asv;
             y[e] = y[e] + 0.0f;
           }
           p0 = pack_bf16x2(y[0], y[1]);
           p1 = pack_bf16x2(y[2], y[3]);
         } else {
-          p0 = g1_value(acc[i][j][4 * q + 0], wsv.x, asv) | (g1_value(acc[i][j][4 * q + 1], wsv.y, asv) << 16);
-          p1 = g1_value(acc[i][j][4 * q + 2], wsv.z, asv) | (g1_value(acc[i][j][4 * q + 3], wsv.w, asv) << 16);
+          p0 = g1_value<SHIFT>(acc[i][j][4 * q + 0], wsv.x, asv) | (g1_value<SHIFT>(acc[i][j][4 * q + 1], wsv.y, asv) << 16);
+          p1 = g1_value<SHIFT>(acc[i][j][4 * q + 2], wsv.z, asv) | (g1_value<SHIFT>(acc[i][j][4 * q + 3], wsv.w, asv) << 16);
         }
         stage(row, col, p0, p1);
       }
@@ -251,6 +256,36 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dma_kernel(
   }
   dma_mainloop<T>(a_rsrc, voff_a, a_words * 4, b_rsrc, kb, lds, acc);
   dense_epilogue<T, RESID>(acc, as, ws, M, N, kb * 256, m0, n0, residual, out, lds);
+#endif
+}
+
+// INT8 x INT8 (h3_gemm_i8_256, kernels/gemm_integer.loom:454-485): the same
+// tiles, DMA and G1 epilogue; `ksteps` 128-k steps of int8 codes.
+template <class T, bool RESID>
+__global__ __launch_bounds__(T::THREADS) void gemm_dma8_kernel(
+    const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
+    const uint32_t* __restrict__ w, const float* __restrict__ ws, int64_t M, int N, int ksteps,
+    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  extern __shared__ __align__(16) char lds[];
+  int64_t tm;
+  int tn;
+  tile_of_block(blockIdx.x, (int64_t)gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = tm * T::BM;
+  const int n0 = tn * T::BN;
+  const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a + m0 * a_words, (uint32_t)(rows_here * a_words * 4));
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      make_rsrc(w + (int64_t)(n0 / 128) * ksteps * 4096, (uint32_t)((T::BN / 128) * ksteps * 16384));
+  v16i acc[T::TM][T::TN];
+  int voff_a[T::A_INST];
+  {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int ql = 0; ql < T::A_INST; ++ql) voff_a[ql] = (lane >> 3) * a_words * 4 + dma_chunk16(wave, lane);
+  }
+  dma8_mainloop<T>(a_rsrc, voff_a, a_words * 4, b_rsrc, ksteps, lds, acc);
+  dense_epilogue<T, RESID, 0>(acc, as, ws, M, N, ksteps * 128, m0, n0, residual, out, lds);
 #endif
 }
 
@@ -476,6 +511,30 @@ hipError_t launch_dma_any(const uint32_t* a, int a_words, const float* as, const
                           uint16_t* out, hipStream_t stream) {
   if (residual) return launch_dma<T, true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
   return launch_dma<T, false>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+}
+
+template <class T, bool RESID>
+hipError_t launch_dma8(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                       int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma8_kernel<T, RESID>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const int tiles_n = n / T::BN;
+  const int64_t tiles_m = (m + T::BM - 1) / T::BM;
+  gemm_dma8_kernel<T, RESID><<<(unsigned)(tiles_m * tiles_n), T::THREADS, T::LDS_BYTES, stream>>>(
+      a, a_words, as, w, ws, m, n, k / 128, residual, out, (int)tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_dma8_any(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  if (residual) return launch_dma8<T, true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return launch_dma8<T, false>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
 }
 
 using Dma256x256 = DmaTile<128, 128, 2, 2>;
@@ -939,6 +998,13 @@ hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, c
 }  // namespace
 
 int gemm_config_count() { return 19; }
+
+hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                          int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  if (n % 256 == 0 && m >= 1024)
+    return launch_dma8_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return launch_dma8_any<Dma128x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+}
 
 hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
                           const float* ws, int64_t m, int n, int k, const uint16_t* residual,

@@ -372,4 +372,59 @@ __device__ __forceinline__ void dma_mainloop(__amdgpu_buffer_rsrc_t a_rsrc, cons
   c.template substep<false, 0>(acc, 1, 0, 0, 0);
 }
 
+// INT8 operands (h3_gemm_i8_256): a 16-byte chunk read is one MFMA operand as
+// it stands (16 int8 values per lane; lanes 32..63 read the chunk four
+// positions further on, so one substep covers chunks p and 4 + p, 32 k
+// values), the 128-byte row of a k-step holds 128 k values in four substeps,
+// and the accumulator is the dot product itself. The DMA and LDS layout are
+// those of the INT4 core.
+template <class T>
+__device__ __forceinline__ void mma8(DmaCore<T>& c, v16i (&acc)[T::TM][T::TN], int buf) {
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j)
+      acc[i][j] = mfma32_i8(__builtin_bit_cast(v4i, c.raw[buf][T::TM + j]), __builtin_bit_cast(v4i, c.raw[buf][i]),
+                            acc[i][j]);
+}
+
+// 128-k step kt read from `rd` while k-step kt + 1 is loaded into `dma`.
+template <class T>
+__device__ __forceinline__ void dma8_kstep(DmaCore<T>& c, v16i (&acc)[T::TM][T::TN], const char* __restrict__ rd,
+                                           char* __restrict__ dma, __amdgpu_buffer_rsrc_t a_rsrc,
+                                           const int (&voff_a)[T::A_INST], int a_q_stride,
+                                           __amdgpu_buffer_rsrc_t b_rsrc, int ksteps, int kt) {
+  c.issue(dma, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, kt + 1);
+  c.read(rd, 0, 0);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    if (p < 3) c.read(rd, (p + 1) & 1, p + 1);
+    mma8<T>(c, acc, p & 1);
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+}
+
+// Full INT8 contraction over `ksteps` 128-k steps into acc (zeroed here); the
+// last step's prefetch reads past the operands into a stage that is not read
+// again (range-checked, as in dma_mainloop).
+template <class T>
+__device__ __forceinline__ void dma8_mainloop(__amdgpu_buffer_rsrc_t a_rsrc, const int (&voff_a)[T::A_INST],
+                                              int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc, int ksteps,
+                                              char* lds, v16i (&acc)[T::TM][T::TN]) {
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j) acc[i][j] = v16i{};
+  DmaCore<T> c;
+  c.issue(lds, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, 0);
+  wait_vmcnt<0>();
+  __syncthreads();
+  for (int kt = 0; kt < ksteps; ++kt) {
+    char* rd = lds + (kt & 1) * T::STAGE_BYTES;
+    char* dma = lds + ((kt & 1) ^ 1) * T::STAGE_BYTES;
+    dma8_kstep<T>(c, acc, rd, dma, a_rsrc, voff_a, a_q_stride, b_rsrc, ksteps, kt);
+  }
+}
+
 }  // namespace clef

@@ -25,6 +25,9 @@ hipError_t launch_tile_permute(const uint16_t* src, int64_t rows, int cols, uint
 hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* a_scales,
                           const uint32_t* w_tiled, const float* w_scales, int64_t m, int n, int k,
                           const uint16_t* residual, uint16_t* out, int config, hipStream_t stream);
+// INT8 x INT8 G1 (codes 4 per word, weights tiled as retile_codes with bits 8).
+hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                          int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream);
 int gemm_config_count();
 
 hipError_t launch_route(const void* logits, int dtype, int64_t tokens, int experts, int topk,

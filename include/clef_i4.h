@@ -162,6 +162,17 @@ int clef_i4_gemm(const uint32_t* a, int32_t k_stride, const float* a_scales, con
                  const float* w_scales, int64_t m, int32_t n, int32_t k, const uint16_t* residual,
                  uint16_t* out, clef_stream_t stream);
 
+/* INT8 x INT8 -> i32 dense GEMM with the same epilogue, for INT8-packed
+ * activations (clef_i4_prepare with bits 8: 4 codes per word, row pitch
+ * k_stride/4 words) and INT8 weights (clef_i4_pack_weight with bits 8).
+ * Replaces the bits = 8 dispatch of Engine::project_prepared
+ * (src/quantized.rs:486-497) and h3_gemm_i8_256 (kernels/gemm_integer.loom:
+ * 444-485). Preconditions: m >= 1, n % 128 == 0, k % 256 == 0, k >= 256,
+ * k_stride >= k, k_stride % 64 == 0 -> "unsupported integer projection shape". */
+int clef_i8_gemm(const uint32_t* a, int32_t k_stride, const float* a_scales, const uint32_t* w_tiled,
+                 const float* w_scales, int64_t m, int32_t n, int32_t k, const uint16_t* residual,
+                 uint16_t* out, clef_stream_t stream);
+
 /* Same, with an explicit tile configuration (0..clef_i4_gemm_configs()-1;
  * -1 = automatic). For tuning and tests. */
 int clef_i4_gemm_config(const uint32_t* a, int32_t k_stride, const float* a_scales,

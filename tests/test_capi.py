@@ -232,3 +232,10 @@ def test_prepare_norm_storage_layout():
         offset = -(-packed * 4 // 128) * 128
         assert f(rows, 5120, stride, bits, 1) == offset // 4 + rows * 2560
     assert f(4, 5120, 5248, 5, 0) == -1
+
+
+@pytest.mark.parametrize("m,n,k,ks", [(0, 128, 256, 320), (4, 100, 256, 320), (4, 128, 300, 320),
+                                      (4, 128, 256, 288), (4, 128, 256, 200)])
+def test_i8_gemm_rejects(m, n, k, ks):
+    rc, msg = call("clef_i8_gemm", FAKE, ks, FAKE, FAKE, FAKE, m, n, k, None, FAKE, None)
+    assert rc == -1 and msg == "unsupported integer projection shape"
