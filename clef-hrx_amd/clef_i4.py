@@ -58,6 +58,9 @@ SIGNATURES = {
                                           _P, _SZ, _P]),
     "clef_swiglu": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
     "clef_moe_combine": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _I32, _P, _P]),
+    "clef_pack_cache_path": (ctypes.c_int, [_P, _P, _P, _SZ]),
+    "clef_pack_cache_read": (ctypes.c_int, [_P, _P, _P, _SZ, _P, _SZ, _P]),
+    "clef_pack_cache_write": (ctypes.c_int, [_P, _P, _P, _SZ, _P, _SZ]),
     "clef_moe_layer_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
     "clef_moe_layer": (ctypes.c_int, [_P, _P, _I32, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P,
                                       _P, _P, _P, _SZ, _P]),
@@ -271,9 +274,84 @@ class QuantizedProjections:
         return rows * cols * bits // 8 + rows * 4
 
 
-def load_quantized_weight(w: torch.Tensor, bits: int = 4, tiled_checkpoint: bool = False
-                          ) -> QuantizedWeight:
-    """Packing half of Engine::load_quantized_weight (src/quantized.rs:147-234)."""
+class _PackKey(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("rows", ctypes.c_int64), ("cols", ctypes.c_int64),
+                ("bits", ctypes.c_int32), ("compiler", ctypes.c_char_p), ("target", ctypes.c_char_p),
+                ("source", ctypes.c_void_p), ("source_bytes", ctypes.c_size_t)]
+
+
+class PackedWeightCache:
+    """PackedWeightCache (src/packed_cache.rs:68-190): "CLFPACK1" files of the
+    exact packed codes and scales, keyed by name, extent, bits, compiler,
+    target and the SHA-256 of the source bytes and of the packing definition.
+    The file format, hashing and checks are the library's (clef_pack_cache_*)."""
+
+    def __init__(self, directory: str, compiler: str = "clef-hrx_amd", target: str = "gfx950"):
+        self.directory = str(directory)
+        self.compiler = compiler
+        self.target = target
+        self.hits = 0
+        self.misses = 0
+
+    def key(self, name: str, rows: int, cols: int, bits: int, source: bytes):
+        source = bytes(source)
+        buf = ctypes.create_string_buffer(source, len(source))
+        k = _PackKey(name.encode(), rows, cols, bits, self.compiler.encode(), self.target.encode(),
+                     ctypes.cast(buf, ctypes.c_void_p), len(source))
+        k._source = buf  # keeps the bytes alive with the key
+        return k
+
+    def path(self, key) -> str:
+        out = ctypes.create_string_buffer(4096)
+        _check(lib().clef_pack_cache_path(self.directory.encode(), ctypes.byref(key), out, 4096))
+        return out.value.decode()
+
+    @staticmethod
+    def sizes(key) -> tuple[int, int]:
+        return key.rows * key.cols * key.bits // 8, key.rows * 4
+
+    def read(self, key):
+        """(codes bytes, scales bytes) of a hit, None on a miss."""
+        nc, ns = self.sizes(key)
+        codes = ctypes.create_string_buffer(max(nc, 1))
+        scales = ctypes.create_string_buffer(max(ns, 1))
+        hit = ctypes.c_int32(0)
+        _check(lib().clef_pack_cache_read(self.directory.encode(), ctypes.byref(key), codes, nc, scales, ns,
+                                          ctypes.byref(hit)))
+        if not hit.value:
+            self.misses += 1
+            return None
+        self.hits += 1
+        return codes.raw[:nc], scales.raw[:ns]
+
+    def write(self, key, codes: bytes, scales: bytes) -> None:
+        _check(lib().clef_pack_cache_write(self.directory.encode(), ctypes.byref(key), codes, len(codes), scales,
+                                           len(scales)))
+
+
+def load_quantized_weight(w: torch.Tensor, bits: int = 4, tiled_checkpoint: bool = False,
+                          cache: PackedWeightCache | None = None, name: str = "") -> QuantizedWeight:
+    """Packing half of Engine::load_quantized_weight (src/quantized.rs:147-234),
+    with the optional packed-weight cache of its bench builds (:169-190,
+    :212-220): a hit uploads the cached bytes, a miss packs and writes them."""
+    rows, cols = w.shape
+    key = None
+    if cache is not None:
+        source = w.contiguous().view(torch.int16).cpu().numpy().tobytes()
+        key = cache.key(name, rows, cols, bits, source)
+        cached = cache.read(key)
+        if cached is not None:
+            import numpy as np
+            codes = torch.from_numpy(np.frombuffer(cached[0], dtype=np.int32).copy()).to(w.device)
+            scales = torch.from_numpy(np.frombuffer(cached[1], dtype=np.float32).copy()).to(w.device)
+            return QuantizedWeight(codes, scales, rows, cols, activation_stride(cols, bits), bits)
+    packed = _pack(w, bits, tiled_checkpoint)
+    if key is not None:
+        cache.write(key, packed.codes.cpu().numpy().tobytes(), packed.scales.cpu().numpy().tobytes())
+    return packed
+
+
+def _pack(w: torch.Tensor, bits: int, tiled_checkpoint: bool) -> QuantizedWeight:
     rows, cols = w.shape
     if tiled_checkpoint:
         dense = torch.empty_like(w)
@@ -286,6 +364,22 @@ def load_quantized_weight(w: torch.Tensor, bits: int = 4, tiled_checkpoint: bool
     _check(lib().clef_i4_pack_weight(_ptr(w), rows, cols, bits, _ptr(codes), _ptr(scales), _ptr(ws),
                                      ws_bytes, _stream()))
     return QuantizedWeight(codes, scales, rows, cols, activation_stride(cols, bits), bits)
+
+
+def load_expert_layer(experts: list[torch.Tensor], rows: int, cols: int, bits: int = 4,
+                      tiled_checkpoint: bool = False, cache: PackedWeightCache | None = None,
+                      name: str = "") -> QuantizedWeight:
+    """omni::load_expert_layer (src/omni.rs:40-72): the 128 experts' [rows][cols]
+    weights of one projection concatenated row-wise into [128*rows][cols] and
+    packed as one weight. Concatenating whole 256-row tiles keeps a tiled
+    checkpoint's layout, so the untile happens once on the concatenation."""
+    if len(experts) != 128:
+        raise ClefError(-1, "Omni MoE requires 128 experts")
+    for t in experts:
+        if tuple(t.shape) != (rows, cols):
+            raise ClefError(-1, f"invalid Omni expert shape: {name}")
+    combined = torch.cat([t.contiguous() for t in experts], dim=0)
+    return load_quantized_weight(combined, bits=bits, tiled_checkpoint=tiled_checkpoint, cache=cache, name=name)
 
 
 def untile_rows(tiled: torch.Tensor) -> torch.Tensor:

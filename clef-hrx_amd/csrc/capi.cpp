@@ -14,7 +14,7 @@
 
 namespace {
 
-thread_local char g_error[256] = "";
+thread_local char g_error[1024] = "";
 
 int fail(const char* msg) {
   std::snprintf(g_error, sizeof g_error, "%s", msg);
@@ -60,6 +60,10 @@ int32_t stride_for(int32_t width, int32_t bits) {
 }
 
 }  // namespace
+
+namespace clef {
+int set_last_error(const char* msg) { return fail(msg); }
+}  // namespace clef
 
 extern "C" {
 

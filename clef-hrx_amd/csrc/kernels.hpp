@@ -28,6 +28,8 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* a_scales,
 // INT8 x INT8 G1 (codes 4 per word, weights tiled as retile_codes with bits 8).
 hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream);
+// Records msg as clef_last_error() of this thread; returns CLEF_EINVAL.
+int set_last_error(const char* msg);
 int gemm_config_count();
 
 hipError_t launch_route(const void* logits, int dtype, int64_t tokens, int experts, int topk,

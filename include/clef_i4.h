@@ -296,6 +296,46 @@ int clef_moe_layer(const uint16_t* x, const void* logits, int32_t logits_dtype, 
                    float* routes_out, uint16_t* out, void* workspace, size_t workspace_bytes,
                    clef_stream_t stream);
 
+/* ------------------------------------------------------- packed cache */
+
+/* Key of a packed-weight cache entry (src/packed_cache.rs:24-33): the weight
+ * name and extent, the compiler and target identities, and the source bytes
+ * (host memory, hashed with SHA-256). The packing definition's hash is
+ * supplied by the library. */
+typedef struct clef_pack_key {
+  const char* name;
+  int64_t rows;
+  int64_t cols;
+  int32_t bits;
+  const char* compiler;
+  const char* target;
+  const void* source;
+  size_t source_bytes;
+} clef_pack_key;
+
+/* Path of the entry of `key` under `directory`: hex SHA-256 of the compact
+ * JSON key + ".pack" (src/packed_cache.rs:101-105). Host-only, no device
+ * work. */
+int clef_pack_cache_path(const char* directory, const clef_pack_key* key, char* path, size_t path_bytes);
+
+/* Reads the "CLFPACK1" entry of `key` into host buffers of exactly
+ * rows*cols*bits/8 code bytes and rows*4 scale bytes. *hit = 0 and CLEF_OK
+ * when there is no entry (a miss). Replaces PackedWeightCache::read
+ * (src/packed_cache.rs:106-145) with its checks and messages: "invalid
+ * packed-cache extent", "truncated packed-cache prefix", "invalid
+ * packed-cache magic", "oversized packed-cache header", "packed-cache length
+ * mismatch", "packed-cache key mismatch", "packed-cache checksum mismatch:
+ * <path>". */
+int clef_pack_cache_read(const char* directory, const clef_pack_key* key, void* codes, size_t codes_bytes,
+                         void* scales, size_t scales_bytes, int32_t* hit);
+
+/* Writes the entry of `key` atomically (temporary file, then rename).
+ * Replaces PackedWeightCache::write (src/packed_cache.rs:146-190);
+ * "packed-cache data size mismatch" when the buffers do not match the key's
+ * extent. */
+int clef_pack_cache_write(const char* directory, const clef_pack_key* key, const void* codes, size_t codes_bytes,
+                          const void* scales, size_t scales_bytes);
+
 #ifdef __cplusplus
 }
 #endif
