@@ -47,6 +47,7 @@ SIGNATURES = {
     "clef_i8_gemm": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P]),
     "clef_i4_project_workspace_bytes": (_SZ, [_I64, _I32]),
     "clef_i4_project": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _I32, _P, _P, _P, _SZ, _P]),
+    "clef_moe_router_logits": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P]),
     "clef_moe_route": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _P, _P]),
     "clef_moe_group_workspace_bytes": (_SZ, [_I64]),
     "clef_moe_group_routes": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _SZ, _P]),
@@ -443,6 +444,19 @@ def project_attention_gate(attention: torch.Tensor, q_gate: torch.Tensor, w: Qua
 
 # ---------------------------------------------------------------- MoE
 
+def router_logits(x: torch.Tensor, gate_w: torch.Tensor) -> torch.Tensor:
+    """The Omni router gate, e.project(norm, "mlp.gate") (src/omni.rs:764):
+    bf16 logits [tokens][experts] = x @ gate_w.T with f32 accumulation."""
+    tokens, hidden = x.shape
+    experts = gate_w.shape[0]
+    if gate_w.shape[1] != hidden or x.dtype != torch.bfloat16 or gate_w.dtype != torch.bfloat16:
+        raise ClefError(-1, "linear shape/dtype mismatch")
+    out = _empty((tokens, experts), torch.bfloat16, x.device)
+    _check(lib().clef_moe_router_logits(_ptr(x.contiguous()), _ptr(gate_w.contiguous()), tokens, hidden, experts,
+                                        _ptr(out), _stream()))
+    return out
+
+
 def omni_route(logits: torch.Tensor, topk: int = 8) -> torch.Tensor:
     """Engine::omni_route (src/omni.rs:170-190)."""
     tokens, experts = logits.shape
@@ -528,8 +542,10 @@ class MoeLayer:
     The workspace is allocated once per (tokens) and reused by every call.
     """
 
-    def __init__(self, gate: QuantizedWeight, up: QuantizedWeight, down: QuantizedWeight, topk: int = 8):
+    def __init__(self, gate: QuantizedWeight, up: QuantizedWeight, down: QuantizedWeight, topk: int = 8,
+                 router: torch.Tensor | None = None):
         self.gate, self.up, self.down, self.topk = gate, up, down, topk
+        self.router = router  # bf16 [128][hidden] router gate, used when no logits are given
         self.hidden = gate.cols
         self.inter = gate.rows // 128
         self._ws = None
@@ -542,9 +558,13 @@ class MoeLayer:
             self._ws_tokens = tokens
         return self._ws
 
-    def __call__(self, x: torch.Tensor, logits: torch.Tensor, routes_out: torch.Tensor | None = None,
+    def __call__(self, x: torch.Tensor, logits: torch.Tensor | None = None, routes_out: torch.Tensor | None = None,
                  out: torch.Tensor | None = None) -> torch.Tensor:
         tokens = x.shape[0]
+        if logits is None:
+            if self.router is None:
+                raise ClefError(-1, "MoE layer needs router logits or a router gate weight")
+            logits = router_logits(x, self.router)  # e.project(norm, "mlp.gate"), src/omni.rs:764
         if out is None:
             out = _empty((tokens, self.hidden), torch.bfloat16, x.device)
         ws = self.workspace(tokens, x.device)

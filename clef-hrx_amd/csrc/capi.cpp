@@ -249,6 +249,14 @@ int clef_moe_route(const void* logits, int32_t logits_dtype, int64_t tokens, int
   return hip_status(clef::launch_route(logits, logits_dtype, tokens, experts, topk, routes, hs(stream)));
 }
 
+int clef_moe_router_logits(const uint16_t* x, const uint16_t* gate_w, int64_t tokens, int32_t hidden,
+                           int32_t experts, uint16_t* logits, clef_stream_t stream) {
+  if (!(tokens >= 1 && hidden >= 64 && hidden % 64 == 0 && experts >= 32 && experts <= 128 && experts % 32 == 0))
+    return fail("linear shape/dtype mismatch");
+  if (!aligned(x, 16) || !aligned(gate_w, 16) || !aligned(logits, 2)) return fail(kAlign);
+  return hip_status(clef::launch_router_gate(x, gate_w, tokens, hidden, experts, logits, hs(stream)));
+}
+
 size_t clef_moe_group_workspace_bytes(int64_t tokens) {
   if (tokens < 1) return 0;
   return align256(clef::group_workspace_bytes(tokens));

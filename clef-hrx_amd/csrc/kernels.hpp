@@ -32,6 +32,8 @@ hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const
 int set_last_error(const char* msg);
 int gemm_config_count();
 
+hipError_t launch_router_gate(const uint16_t* x, const uint16_t* w, int64_t tokens, int hidden, int experts,
+                              uint16_t* out, hipStream_t stream);
 hipError_t launch_route(const void* logits, int dtype, int64_t tokens, int experts, int topk,
                         float* routes, hipStream_t stream);
 size_t group_workspace_bytes(int64_t tokens);

@@ -319,6 +319,56 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
 
 }  // namespace
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// Router gate projection: logits[t][e] = bf16(sum_k x[t][k] * w[e][k]) with
+// f32 accumulation on the bf16 MFMA -- the bf16 linear that produces the
+// Omni router logits (src/omni.rs:764 -> Engine::linear, src/ops.rs:95-175,
+// kernels/gemm_bf16_reference.loom). One workgroup per 32 tokens; wave w
+// computes experts 32w..32w+31 (x in the MFMA A slot, so lane l holds expert
+// 32w + l%32 for tokens 8(i/4) + 4(l/32) + i%4, i < 16). No barriers: waves
+// past the expert count leave at once.
+__global__ __launch_bounds__(256) void router_gate_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ w, int64_t tokens,
+                                                          int hidden, int experts, uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e0 = wave * 32;
+  if (e0 >= experts) return;
+  const int64_t t0 = (int64_t)blockIdx.x * 32;
+  const int r = lane & 31, kb = (lane >> 5) * 8;
+  const bool tok_ok = t0 + r < tokens;
+  const uint16_t* xa = x + (tok_ok ? t0 + r : 0) * (int64_t)hidden + kb;
+  const uint16_t* wb = w + (int64_t)(e0 + r) * hidden + kb;
+  v16f acc = {};
+  // hidden % 64 == 0: four 16-k MFMAs per iteration, their loads issued first
+  for (int k = 0; k < hidden; k += 64) {
+    u4 a[4], b[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      a[s] = tok_ok ? *reinterpret_cast<const u4*>(xa + k + 16 * s) : u4{0u, 0u, 0u, 0u};
+      b[s] = *reinterpret_cast<const u4*>(wb + k + 16 * s);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a[s]),
+                                                    __builtin_bit_cast(bf16x8_t, b[s]), acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t t = t0 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    if (t < tokens) out[t * experts + e0 + r] = (uint16_t)f32_to_bf16(acc[i]);
+  }
+}
+
+hipError_t launch_router_gate(const uint16_t* x, const uint16_t* w, int64_t tokens, int hidden, int experts,
+                              uint16_t* out, hipStream_t stream) {
+  const int64_t blocks = (tokens + 31) / 32;
+  if (blocks == 0) return hipSuccess;
+  router_gate_kernel<<<(unsigned)blocks, 256, 0, stream>>>(x, w, tokens, hidden, experts, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_route(const void* logits, int dtype, int64_t tokens, int experts, int topk,
                         float* routes, hipStream_t stream) {
   const int64_t blocks = (tokens + 3) / 4;

@@ -296,6 +296,18 @@ int clef_moe_layer(const uint16_t* x, const void* logits, int32_t logits_dtype, 
                    float* routes_out, uint16_t* out, void* workspace, size_t workspace_bytes,
                    clef_stream_t stream);
 
+/* Router gate projection: logits[t][e] = bf16(sum_k x[t][k] * gate_w[e][k])
+ * with f32 accumulation (bf16 MFMA), x bf16 [tokens][hidden], gate_w bf16
+ * [experts][hidden] row-major, logits bf16 [tokens][experts] -- the input of
+ * clef_moe_route. Replaces the Omni MoE block's e.project(norm, "mlp.gate")
+ * (src/omni.rs:764) through Engine::linear (src/ops.rs:95-175,
+ * kernels/gemm_bf16_reference.loom). The summation order differs from the
+ * reference's WMMA order, so results agree within f32 rounding, not bit for
+ * bit. Preconditions: tokens >= 1, hidden % 64 == 0, 32 <= experts <= 128,
+ * experts % 32 == 0 -> "linear shape/dtype mismatch". */
+int clef_moe_router_logits(const uint16_t* x, const uint16_t* gate_w, int64_t tokens, int32_t hidden,
+                           int32_t experts, uint16_t* logits, clef_stream_t stream);
+
 /* ------------------------------------------------------- packed cache */
 
 /* Key of a packed-weight cache entry (src/packed_cache.rs:24-33): the weight

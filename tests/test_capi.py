@@ -239,3 +239,10 @@ def test_prepare_norm_storage_layout():
 def test_i8_gemm_rejects(m, n, k, ks):
     rc, msg = call("clef_i8_gemm", FAKE, ks, FAKE, FAKE, FAKE, m, n, k, None, FAKE, None)
     assert rc == -1 and msg == "unsupported integer projection shape"
+
+
+@pytest.mark.parametrize("tokens,hidden,experts", [(0, 2048, 128), (4, 100, 128), (4, 2048, 129), (4, 2048, 48),
+                                                   (4, 2048, 16)])
+def test_router_logits_rejects(tokens, hidden, experts):
+    rc, msg = call("clef_moe_router_logits", FAKE, FAKE, tokens, hidden, experts, FAKE, None)
+    assert rc == -1 and msg == "linear shape/dtype mismatch"

@@ -80,3 +80,34 @@ def test_attention_gate_projection_matches_oracle():
     qw = clef_i4.load_quantized_weight(dev_bf16(w))
     got = clef_i4.project_attention_gate(dev_bf16(x), dev_bf16(q), qw, dev_bf16(res))
     assert np.array_equal(host_u16(got), want)
+
+
+@pytest.mark.parametrize("tokens,experts", [(1, 128), (31, 128), (33, 64), (4096, 128), (70, 32)])
+def test_router_logits_within_f32_summation_bound(tokens, experts):
+    """Router gate projection (src/omni.rs:764): each logit within the f32
+    summation bound of the exact dot product (float64), plus half a bf16 step
+    for the final rounding. The reference's WMMA summation order is not
+    reproduced, so bits are compared only through this bound."""
+    hidden = 2048
+    rng = np.random.default_rng(tokens + experts)
+    x = BF(rng.standard_normal((tokens, hidden)).astype(np.float32))
+    w = BF((rng.standard_normal((experts, hidden)) * 0.02).astype(np.float32))
+    got = oracle.bf16_to_f32(host_u16(clef_i4.router_logits(dev_bf16(x), dev_bf16(w)))).astype(np.float64)
+    xf, wf = oracle.bf16_to_f32(x).astype(np.float64), oracle.bf16_to_f32(w).astype(np.float64)
+    exact = xf @ wf.T
+    bound = hidden * 2.0 ** -23 * (np.abs(xf) @ np.abs(wf).T) + np.abs(exact) * 2.0 ** -8 + 1e-30
+    assert (np.abs(got - exact) <= bound).all()
+
+
+def test_router_logits_one_hot_weights_are_exact():
+    """With one-hot gate rows every logit is a single exact product, so the
+    output is the selected input column bit for bit: pins the token/expert
+    indexing and the tail of a partial 32-token block."""
+    tokens, hidden, experts = 45, 256, 128
+    rng = np.random.default_rng(9)
+    x = BF(rng.standard_normal((tokens, hidden)).astype(np.float32))
+    w = np.zeros((experts, hidden), dtype=np.uint16)
+    cols = rng.permutation(hidden)[:experts]
+    w[np.arange(experts), cols] = 0x3F80  # 1.0
+    got = host_u16(clef_i4.router_logits(dev_bf16(x), dev_bf16(w)))
+    assert np.array_equal(got, x[:, cols])
