@@ -10,6 +10,7 @@
 // out[route][c] = bf16(RN(f32(acc) * RN(as[xr] * ws[e*n + c]))), no clamp.
 
 #include "gemm_core.hpp"
+#include "silu_table.hpp"
 #include "gemm_dma.hpp"
 #include "gemm_persist.hpp"
 #include "gemm_dmah.hpp"
@@ -762,13 +763,6 @@ static_assert(ExpertDmaTile::BM == kExpertBM, "expert schedule tile height");
 // A wave whose 64 slots are all past the expert's count runs the DMA and
 // barrier schedule only. Work items, XCD chunking and the gathered A rows
 // are as in expert_dma_kernel.
-// silu_bf16 of the bf16 values tabulated by silu_lut_index (16 KiB). The
-// entries are generated at build time on the host by silu_table_gen.cpp from
-// the same host-and-device steps, so the table is part of the code object and
-// needs no set-up launch.
-__device__ const uint16_t g_silu_lut[kSiluLutSize] __attribute__((unused)) = {
-#include "silu_table.inc"
-};
 
 using ExpertHTile = DmaHTile<64, 128, 2, 2, kSchedFree, false>;
 using ExpertGUTile = DmaHTile<64, 128, 2, 2, kSchedFree, true>;

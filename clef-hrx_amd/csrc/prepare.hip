@@ -17,6 +17,7 @@
 // words. A 256-thread workgroup holds 16 groups: 16/G rows of G groups when
 // the row has G <= 16 groups, else one row over P passes kept in registers.
 #include "common.hpp"
+#include "silu_table.hpp"
 #include "kernels.hpp"
 
 namespace clef {
@@ -64,12 +65,19 @@ struct SwigluSource {
     return Raw{pg[0], pg[1], pu[0], pu[1]};
   }
   __device__ __forceinline__ void convert(const Raw& r, float* v) const {
-    uint32_t g[8] = {r.ga.x, r.ga.y, r.ga.z, r.ga.w, r.gb.x, r.gb.y, r.gb.z, r.gb.w};
-    uint32_t u[8] = {r.ua.x, r.ua.y, r.ua.z, r.ua.w, r.ub.x, r.ub.y, r.ub.z, r.ub.w};
+    const uint32_t gw[8] = {r.ga.x, r.ga.y, r.ga.z, r.ga.w, r.gb.x, r.gb.y, r.gb.z, r.gb.w};
+    const uint32_t uw[8] = {r.ua.x, r.ua.y, r.ua.z, r.ua.w, r.ub.x, r.ub.y, r.ub.z, r.ub.w};
+    float g[16], act[16];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      v[2 * i] = swiglu1(bf16_lo(g[i]), bf16_lo(u[i]));
-      v[2 * i + 1] = swiglu1(bf16_hi(g[i]), bf16_hi(u[i]));
+      g[2 * i] = bf16_lo(gw[i]);
+      g[2 * i + 1] = bf16_hi(gw[i]);
+    }
+    silu_lut<16>(g, act);  // = silu_bf16(g), from the table where it covers g
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[2 * i] = bf16_round(act[2 * i] * bf16_lo(uw[i]));
+      v[2 * i + 1] = bf16_round(act[2 * i + 1] * bf16_hi(uw[i]));
     }
   }
   __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
@@ -124,8 +132,13 @@ struct NormSource {
   const uint16_t* x;
   const uint16_t* weight;
   uint16_t* normalized;  // nullable
+  using Raw = PlainSource::Raw;
+  __device__ __forceinline__ Raw fetch(int64_t row, int width, int col) const {
+    return PlainSource{x}.fetch(row, width, col);
+  }
+  __device__ __forceinline__ void convert(const Raw& r, float* v) const { PlainSource{x}.convert(r, v); }
   __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
-    PlainSource{x}.load16(row, width, col, v);
+    convert(fetch(row, width, col), v);
   }
   template <int P>
   __device__ __forceinline__ void normalize(float (&v)[P][16], int64_t row, int width, int grp0, int L,
