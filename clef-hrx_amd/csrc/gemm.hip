@@ -1003,7 +1003,13 @@ hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const
 hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
                           const float* ws, int64_t m, int n, int k, const uint16_t* residual,
                           uint16_t* out, int config, hipStream_t stream) {
-  if (config < 0) config = (n % 256 == 0 && m >= 1024) ? 9 : 6;
+  if (config < 0) {
+    // 256x256 tiles (8 waves) once there are enough of them to give most CUs
+    // one (measured: M2048 N4096 K4096 runs 33 us on 128x128 tiles against
+    // 48 us on 128 tiles of 256x256); 128x128 tiles otherwise.
+    const int64_t tiles256 = (m + 255) / 256 * (n / 256);
+    config = (n % 256 == 0 && m >= 1024 && tiles256 >= 192) ? 9 : 6;
+  }
   // Configurations with a 256-wide N tile need n % 256 == 0; the others
   // (N tile 128) take any n % 128 == 0.
   const bool wide_n = config == 2 || config == 4 || config == 7 || (config >= 9 && config <= 12) || config == 14 ||
