@@ -34,7 +34,7 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE and WRITE_SIZE passes over `bench.py --only gemm`, each scaled by
 # the reading for a plain 512 MiB copy (x2.000 fetch, x1.000 write); the runs
 # and raw readings are in profiles/int4_gemm_m4096_k4096_n12288.txt.
-GEMM_TRAFFIC_BYTES = 262.3e6
+GEMM_TRAFFIC_BYTES = 269.76e6
 
 
 def parse():
@@ -46,7 +46,7 @@ def parse():
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=600)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--only", choices=["gemm", "moe", "mlp", "i8", "copy"], default=None,
+    p.add_argument("--only", choices=["gemm", "moe", "mlp", "i8", "copy", "peaks"], default=None,
                    help="run one leg; 'copy' is a plain 512 MiB device copy, the known-size "
                         "kernel that scales HBM byte counters")
     return p.parse_args()
@@ -240,6 +240,12 @@ def main():
         res["mlp"] = mlp_leg(args)
     if args.only in (None, "i8"):
         res["i8"] = i8_leg(args)
+    if args.only == "peaks":
+        import subprocess
+        probe = os.path.join(ROOT, "clef-hrx_amd", "lib", "peaks")
+        proc = subprocess.run([probe], check=True, capture_output=True, text=True)
+        print(proc.stdout.strip())
+        return
     if args.only == "copy":
         c = copy_leg(args)
         print(json.dumps({"copy_bytes": c["bytes"], "copy_ms": round(c["ms"], 4),

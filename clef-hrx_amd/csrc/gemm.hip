@@ -324,27 +324,42 @@ __global__ __launch_bounds__(T::THREADS, 2) void gemm_dmah_kernel(
 // straight from the accumulators with exactly TM * TN * 4 buffer stores per
 // wave (rows past M fall outside the output range and are dropped), so the
 // next tile's k-step 0 can wait on its own DMA only.
-template <class T, bool RESID>
-__device__ __forceinline__ void direct_epilogue(const v16i (&acc)[T::TM][T::TN], const float* __restrict__ as,
-                                                const float* __restrict__ ws, int64_t M, int N, int K,
-                                                int64_t m0, int n0, const uint16_t* __restrict__ residual,
-                                                uint16_t* __restrict__ out) {
+// Scales and fast-path flag of a G1 tile epilogue, loaded ahead of the
+// epilogue (so no global load waits there).
+template <class T>
+struct EpiScales {
+  float asr[T::TM];
+  float4 wsr[T::TN][4];
+  bool fast;
+};
+
+// The loads only; epi_scales_finish computes the flag. Issued ahead of a DMA,
+// the loads can then be waited for without waiting for the DMA.
+template <class T>
+__device__ __forceinline__ void epi_scales_issue(EpiScales<T>& e, const float* __restrict__ as,
+                                                 const float* __restrict__ ws, int64_t M, int64_t m0, int n0) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
   const int h = lane >> 5, lr = lane & 31;
-  const float inf = __builtin_huge_valf();
-  const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
-  const __amdgpu_buffer_rsrc_t out_rsrc = make_rsrc(out + m0 * N, (uint32_t)(rows_here * N * 2));
-  const __amdgpu_buffer_rsrc_t res_rsrc =
-      make_rsrc(RESID ? residual + m0 * N : out, RESID ? (uint32_t)(rows_here * N * 2) : 0u);
-
-  float asr[T::TM];
-  float mas = 0.0f;
 #pragma unroll
   for (int i = 0; i < T::TM; ++i) {
     const int64_t m = m0 + wm * T::WM + 32 * i + lr;
-    asr[i] = m < M ? as[m] : 0.0f;
-    const float a = __builtin_fabsf(asr[i]);
+    e.asr[i] = m < M ? as[m] : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      e.wsr[j][q] = *reinterpret_cast<const float4*>(ws + n0 + wn * T::WN + 32 * j + 8 * q + 4 * h);
+}
+
+template <class T>
+__device__ __forceinline__ void epi_scales_finish(EpiScales<T>& e, int K) {
+  const float inf = __builtin_huge_valf();
+  float mas = 0.0f;
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    const float a = __builtin_fabsf(e.asr[i]);
     mas = __builtin_fmaxf(mas, a < inf ? a : 0.0f);
   }
   float mws = 0.0f;
@@ -353,20 +368,44 @@ __device__ __forceinline__ void direct_epilogue(const v16i (&acc)[T::TM][T::TN],
   for (int j = 0; j < T::TN; ++j)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int n = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
-      const float4 w = *reinterpret_cast<const float4*>(ws + n);
-      const float w4[4] = {w.x, w.y, w.z, w.w};
+      const float w4[4] = {e.wsr[j][q].x, e.wsr[j][q].y, e.wsr[j][q].z, e.wsr[j][q].w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        exact = exact && (w4[e] * 0.00390625f) * 256.0f == w4[e];
-        const float a = __builtin_fabsf(w4[e]);
+      for (int t = 0; t < 4; ++t) {
+        exact = exact && (w4[t] * 0.00390625f) * 256.0f == w4[t];
+        const float a = __builtin_fabsf(w4[t]);
         mws = __builtin_fmaxf(mws, a < inf ? a : 0.0f);
       }
     }
-  const bool fast = __all(exact && mws * mas * (98.0f * (float)K) < kBf16Max);
+  e.fast = __all(exact && mws * mas * (98.0f * (float)K) < kBf16Max);
+}
+
+template <class T>
+__device__ __forceinline__ EpiScales<T> epi_scales_load(const float* __restrict__ as, const float* __restrict__ ws,
+                                                        int64_t M, int K, int64_t m0, int n0) {
+  EpiScales<T> e;
+  epi_scales_issue<T>(e, as, ws, M, m0, n0);
+  epi_scales_finish<T>(e, K);
+  return e;
+}
+
+// G1 tile epilogue stored straight from the accumulators: TM * TN * 4 buffer
+// stores per wave (plus as many residual loads), rows past M fall outside the
+// output range and are dropped. Same values as dense_epilogue.
+template <class T, bool RESID>
+__device__ __forceinline__ void direct_epilogue_store(const v16i (&acc)[T::TM][T::TN], const EpiScales<T>& e,
+                                                      int64_t M, int N, int64_t m0, int n0,
+                                                      const uint16_t* __restrict__ residual,
+                                                      uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+  const int h = lane >> 5, lr = lane & 31;
+  const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
+  const __amdgpu_buffer_rsrc_t out_rsrc = make_rsrc(out + m0 * N, (uint32_t)(rows_here * N * 2));
+  const __amdgpu_buffer_rsrc_t res_rsrc =
+      make_rsrc(RESID ? residual + m0 * N : out, RESID ? (uint32_t)(rows_here * N * 2) : 0u);
 #pragma unroll
   for (int i = 0; i < T::TM; ++i) {
-    const float asv = asr[i];
+    const float asv = e.asr[i];
     const int row = wm * T::WM + 32 * i + lr;
 #pragma unroll
     for (int j = 0; j < T::TN; ++j)
@@ -374,16 +413,16 @@ __device__ __forceinline__ void direct_epilogue(const v16i (&acc)[T::TM][T::TN],
       for (int q = 0; q < 4; ++q) {
         const int col = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
         const int off = (row * N + col) * 2;
-        const float4 wsv = *reinterpret_cast<const float4*>(ws + col);
+        const float4 wsv = e.wsr[j][q];
         uint32_t p0, p1;
-        if (fast) {
+        if (e.fast) {
           const float w4[4] = {wsv.x, wsv.y, wsv.z, wsv.w};
           float y[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            y[e] = (float)acc[i][j][4 * q + e] * (w4[e] * 0.00390625f);
-            y[e] = y[e] * asv;
-            y[e] = y[e] + 0.0f;
+          for (int t = 0; t < 4; ++t) {
+            y[t] = (float)acc[i][j][4 * q + t] * (w4[t] * 0.00390625f);
+            y[t] = y[t] * asv;
+            y[t] = y[t] + 0.0f;
           }
           p0 = pack_bf16x2(y[0], y[1]);
           p1 = pack_bf16x2(y[2], y[3]);
@@ -399,6 +438,91 @@ __device__ __forceinline__ void direct_epilogue(const v16i (&acc)[T::TM][T::TN],
         __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)p0, (int)p1}, out_rsrc, off, 0, 0);
       }
   }
+}
+
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// Bytes of LDS each wave uses to turn one 32-row block of its accumulators
+// into whole output rows (32 rows of WN bf16).
+template <class T>
+constexpr int kEpiWaveLds = 32 * T::WN * 2;
+
+// G1 tile epilogue through a wave-private LDS block: for each 32-row block i
+// the wave writes its bf16 results (8 bytes per lane per 4 columns, 16-byte
+// chunks XOR-swizzled by row), reads them back as 16 bytes of one row per
+// lane and stores whole 128-byte row segments (TM * 4 stores of 16 bytes per
+// lane instead of TM * TN * 4 stores of 8 bytes across 32 rows). LDS
+// operations of one wave execute in order, so block i + 1 may overwrite the
+// rows block i has read without a barrier. Same values as dense_epilogue.
+template <class T, bool RESID>
+__device__ __forceinline__ void staged_epilogue_store(const v16i (&acc)[T::TM][T::TN], const EpiScales<T>& e,
+                                                      int64_t M, int N, int64_t m0, int n0,
+                                                      const uint16_t* __restrict__ residual,
+                                                      uint16_t* __restrict__ out, char* __restrict__ wlds) {
+  static_assert(T::WN == 64, "one 128-byte row segment per wave");
+  constexpr int kReads = kEpiWaveLds<T> / 1024;  // 16-byte reads per lane per block
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+  const int h = lane >> 5, lr = lane & 31;
+  const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
+  const __amdgpu_buffer_rsrc_t out_rsrc = make_rsrc(out + m0 * N, (uint32_t)(rows_here * N * 2));
+  const __amdgpu_buffer_rsrc_t res_rsrc =
+      make_rsrc(RESID ? residual + m0 * N : out, RESID ? (uint32_t)(rows_here * N * 2) : 0u);
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    const float asv = e.asr[i];
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 wsv = e.wsr[j][q];
+        uint32_t p0, p1;
+        if (e.fast) {
+          const float w4[4] = {wsv.x, wsv.y, wsv.z, wsv.w};
+          float y[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            y[t] = (float)acc[i][j][4 * q + t] * (w4[t] * 0.00390625f);
+            y[t] = y[t] * asv;
+            y[t] = y[t] + 0.0f;
+          }
+          p0 = pack_bf16x2(y[0], y[1]);
+          p1 = pack_bf16x2(y[2], y[3]);
+        } else {
+          p0 = g1_value(acc[i][j][4 * q + 0], wsv.x, asv) | (g1_value(acc[i][j][4 * q + 1], wsv.y, asv) << 16);
+          p1 = g1_value(acc[i][j][4 * q + 2], wsv.z, asv) | (g1_value(acc[i][j][4 * q + 3], wsv.w, asv) << 16);
+        }
+        const int chunk = 4 * j + q;  // 16-byte chunk of the row: columns 8 * chunk .. + 7
+        *reinterpret_cast<v2u*>(wlds + lr * 128 + ((chunk ^ (lr & 7)) << 4) + 8 * h) = v2u{p0, p1};
+      }
+#pragma unroll
+    for (int r = 0; r < kReads; ++r) {
+      const int row = 8 * r + (lane >> 3), chunk = lane & 7;
+      v4u v = *reinterpret_cast<const v4u*>(wlds + row * 128 + ((chunk ^ (lane >> 3)) << 4));
+      // lane part in the VGPR offset, the block's rows in the scalar offset
+      const int voff = ((wm * T::WM + (lane >> 3)) * N + n0 + wn * T::WN + 8 * chunk) * 2;
+      const int soff = (32 * i + 8 * r) * N * 2;
+      if (RESID) {
+        const v4i rv = __builtin_amdgcn_raw_buffer_load_b128(res_rsrc, voff, soff, 0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t p = v[t], rr = (uint32_t)rv[t];
+          v[t] = pack_bf16x2(bf16_lo(rr) + bf16_lo(p), bf16_hi(rr) + bf16_hi(p));
+        }
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]}, out_rsrc, voff, soff, 0);
+    }
+  }
+}
+
+template <class T, bool RESID>
+__device__ __forceinline__ void direct_epilogue(const v16i (&acc)[T::TM][T::TN], const float* __restrict__ as,
+                                                const float* __restrict__ ws, int64_t M, int N, int K,
+                                                int64_t m0, int n0, const uint16_t* __restrict__ residual,
+                                                uint16_t* __restrict__ out) {
+  const EpiScales<T> e = epi_scales_load<T>(as, ws, M, K, m0, n0);
+  direct_epilogue_store<T, RESID>(acc, e, M, N, m0, n0, residual, out);
 }
 
 template <class T, bool RESID>
@@ -433,6 +557,199 @@ __global__ __launch_bounds__(T::THREADS) void gemm_persistent_kernel(
   persistent_loop<T, T::TM * T::TN * 4, TileRsrc>(blockIdx.x, gridDim.x, total, kb, voff, a_words * 4, lds, get,
                                                   epi);
 #endif
+}
+
+// Last k-step of one tile and first k-step of the next, in one inlined body
+// so that `last` (read by the last k-step, then refilled with the next tile's
+// k-step 1) and `first` (filled with the next tile's k-step 0 during the last
+// k-step) are distinct restrict pointers throughout:
+//   DMA next k0 -> first; last k-step from `last`; drain + barrier;
+//   DMA next k1 -> last; last pair; epilogue (scales loaded before the k-step,
+//   stores straight from the accumulators);
+//   k-step 0 of the next tile from `first`, then wait only for the k1 DMA:
+//   the epilogue's stores, issued after it, keep draining under the MFMAs.
+template <class T, bool RESID>
+__device__ __forceinline__ void gemm_tile_turn(DmaCore<T>& c, v16i (&acc)[T::TM][T::TN], char* __restrict__ last,
+                                               char* __restrict__ first, __amdgpu_buffer_rsrc_t a_cur,
+                                               __amdgpu_buffer_rsrc_t b_cur, __amdgpu_buffer_rsrc_t a_next,
+                                               __amdgpu_buffer_rsrc_t b_next, const int (&voff_a)[T::A_INST],
+                                               int a_q_stride, int ksteps, const float* __restrict__ as,
+                                               const float* __restrict__ ws, int64_t M, int N, int64_t m0, int n0,
+                                               const uint16_t* __restrict__ residual, uint16_t* __restrict__ out,
+                                               char* __restrict__ wlds, bool more) {
+  (void)a_cur;
+  (void)b_cur;
+  constexpr int INST = T::A_INST + T::B_INST, MF = DmaCore<T>::MF, NF = DmaCore<T>::NF;
+  if constexpr (T::SCHED == kSchedPin) {
+    // The next tile's k-step-0 DMA and the reads of pair 0 ride on the MFMA
+    // slots of the previous k-step's last substep, as in dma_kstep_next.
+    auto extra = [&](int q) {
+#pragma unroll
+      for (int d = 0; d < INST; ++d)
+        if (more && d * MF / INST == q) c.issue_one(first, a_next, voff_a, a_q_stride, b_next, ksteps, 0, d);
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+        if (f * MF / NF == q) c.read_one(last, 0, 0, f);
+    };
+    c.template substep_spread<true>(acc, 0, 1, 1, 1, extra);
+    c.template substep_spread<true>(acc, 1, 0, 0, 0, typename DmaCore<T>::NoExtra{});
+  } else {
+    if (more) c.issue(first, a_next, voff_a, a_q_stride, b_next, ksteps, 0);
+    c.read(last, 0, 0);
+    c.template substep<true, NF>(acc, 0, 1, 1, 1);
+    c.template substep<true, 0>(acc, 1, 0, 0, 0);
+  }
+  c.pairs012(acc, last);
+  wait_vmcnt<0>();
+  __syncthreads();
+  // Scale loads first, then the k1 DMA: waiting for the loads leaves the DMA
+  // in flight (vector memory operations complete in issue order).
+  EpiScales<T> e;
+  epi_scales_issue<T>(e, as, ws, M, m0, n0);
+  if constexpr (T::SCHED == kSchedPin) {
+    auto extra = [&](int q) {
+#pragma unroll
+      for (int d = 0; d < INST; ++d)
+        if (more && d * MF / INST == q) c.issue_one(last, a_next, voff_a, a_q_stride, b_next, ksteps, 1, d);
+    };
+    c.template substep_spread<true>(acc, 0, 1, 1, 1, extra);
+  } else {
+    if (more) c.issue(last, a_next, voff_a, a_q_stride, b_next, ksteps, 1);
+    c.template substep<true, 0>(acc, 0, 1, 1, 1);
+  }
+  c.template substep<false, 0>(acc, 1, 0, 0, 0);
+  epi_scales_finish<T>(e, ksteps * 256);
+  // The scheduler must not start the next tile's MFMAs (fresh accumulators)
+  // while this tile's accumulators are still being stored.
+  __builtin_amdgcn_sched_barrier(0);
+  staged_epilogue_store<T, RESID>(acc, e, M, N, m0, n0, residual, out, wlds);
+  __builtin_amdgcn_sched_barrier(0);
+  if (!more) return;
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j) acc[i][j] = v16i{};
+  c.read(first, 0, 0);
+  c.unpack(0, 0, 0);
+  c.pairs012(acc, first);
+  // VMEM ops complete in issue order: with at most EPI outstanding, the k1
+  // DMA issued before the epilogue's EPI loads and stores has landed.
+  constexpr int EPI = T::TM * (kEpiWaveLds<T> / 1024) * (RESID ? 2 : 1);
+  wait_vmcnt<(EPI < 63 ? EPI : 63)>();
+  __syncthreads();
+}
+
+// Persistent G1 on the DMA core: a workgroup walks tiles b, b + grid, ...
+// (grid a multiple of 8, so all of a workgroup's tiles map to its XCD). The
+// last k-step of a tile loads the next tile's k-step 0 into the free stage
+// while it computes, the epilogue stores straight from the accumulators
+// (no LDS), and the next tile starts on data already in LDS; the epilogue's
+// stores drain under the next tile's first k-step. Needs ksteps >= 2.
+template <class T, bool RESID>
+__global__ __launch_bounds__(T::THREADS) void gemm_dma_persist_kernel(
+    const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
+    const uint32_t* __restrict__ w, const float* __restrict__ ws, int64_t M, int N, int kb,
+    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  extern __shared__ __align__(16) char lds[];
+  const int64_t total = (int64_t)tiles_m * tiles_n;
+  int64_t t = blockIdx.x;
+  if (t >= total) return;
+  struct Tile {
+    __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
+    int64_t m0;
+    int n0;
+  };
+  auto tile = [&](int64_t b) {
+    int64_t tm;
+    int tn;
+    tile_of_block(b, total, tiles_m, tiles_n, tm, tn);
+    Tile x;
+    x.m0 = tm * T::BM;
+    x.n0 = tn * T::BN;
+    const int64_t rows_here = M - x.m0 < T::BM ? M - x.m0 : T::BM;
+    x.a_rsrc = make_rsrc(a + x.m0 * a_words, (uint32_t)(rows_here * a_words * 4));
+    x.b_rsrc = make_rsrc(w + (int64_t)(x.n0 / 128) * kb * 4096, (uint32_t)((T::BN / 128) * kb * 16384));
+    return x;
+  };
+  int voff_a[T::A_INST];
+  {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int ql = 0; ql < T::A_INST; ++ql) voff_a[ql] = (lane >> 3) * a_words * 4 + dma_chunk16(wave, lane);
+  }
+  const int a_q_stride = a_words * 4;
+  DmaCore<T> c;
+  v16i acc[T::TM][T::TN];
+  Tile cur = tile(t);
+  int64_t g = 0;  // k-steps done by this workgroup: the stage of k-step kt is (g + kt) & 1
+  auto stage = [&](int64_t i) { return lds + (int)(i & 1) * T::STAGE_BYTES; };
+  auto zero = [&] {
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j) acc[i][j] = v16i{};
+  };
+  zero();
+  dma_kstep_first<T>(c, acc, stage(0), stage(1), cur.a_rsrc, voff_a, a_q_stride, cur.b_rsrc, kb);
+  while (true) {
+    const int64_t tn_next = t + gridDim.x;
+    const bool has_next = tn_next < total;
+    for (int kt = 1; kt + 1 < kb; ++kt)
+      dma_kstep_next<T>(c, acc, stage(g + kt), stage(g + kt + 1), cur.a_rsrc, voff_a, a_q_stride, cur.b_rsrc, kb,
+                        kt);
+    const Tile nxt = tile(has_next ? tn_next : t);
+    gemm_tile_turn<T, RESID>(c, acc, stage(g + kb - 1), stage(g + kb), cur.a_rsrc, cur.b_rsrc, nxt.a_rsrc,
+                             nxt.b_rsrc, voff_a, a_q_stride, kb, as, ws, M, N, cur.m0, cur.n0, residual, out,
+                             lds + T::LDS_BYTES + (threadIdx.x >> 6) * kEpiWaveLds<T>, has_next);
+    if (!has_next) break;
+    g += kb;
+    t = tn_next;
+    cur = nxt;
+  }
+#endif
+}
+
+template <class T, bool RESID>
+hipError_t launch_dma_persist(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                              int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  constexpr int kPersistLds = T::LDS_BYTES + T::NW * kEpiWaveLds<T>;
+  static_assert(kPersistLds <= 160 * 1024, "LDS per workgroup");
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_persist_kernel<T, RESID>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kPersistLds);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int nb = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &nb, reinterpret_cast<const void*>(&gemm_dma_persist_kernel<T, RESID>), T::THREADS, kPersistLds);
+    if (e != hipSuccess) return e;
+    per_cu = nb > 0 ? nb : 1;
+  }
+  int dev = 0, cus = 0;
+  if (hipError_t e = hipGetDevice(&dev)) return e;
+  if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) return e;
+  const int tiles_n = n / T::BN;
+  const int64_t tiles_m = (m + T::BM - 1) / T::BM;
+  const int64_t total = tiles_m * tiles_n;
+  int64_t grid = (int64_t)cus * per_cu / 8 * 8;
+  if (grid < 8) grid = 8;
+  if (grid > total) grid = total;
+  gemm_dma_persist_kernel<T, RESID><<<(unsigned)grid, T::THREADS, kPersistLds, stream>>>(
+      a, a_words, as, w, ws, m, n, k / 256, residual, out, (int)tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_dma_persist_any(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
+                                  const float* ws, int64_t m, int n, int k, const uint16_t* residual, uint16_t* out,
+                                  hipStream_t stream) {
+  if (residual) return launch_dma_persist<T, true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return launch_dma_persist<T, false>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
 }
 
 template <class T, bool RESID>
@@ -991,7 +1308,7 @@ hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, c
 
 }  // namespace
 
-int gemm_config_count() { return 19; }
+int gemm_config_count() { return 21; }
 
 hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
@@ -1006,16 +1323,20 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
   if (config < 0) {
     // 256x256 tiles (8 waves) once there are enough of them to give most CUs
     // one (measured: M2048 N4096 K4096 runs 33 us on 128x128 tiles against
-    // 48 us on 128 tiles of 256x256); 128x128 tiles otherwise.
+    // 48 us on 128 tiles of 256x256), walked by a persistent grid that loads
+    // each next tile's first k-steps under the current tile's last one
+    // (M4096 N12288 K4096: 154 us against 160 us with one workgroup per
+    // tile); 128x128 tiles otherwise.
     const int64_t tiles256 = (m + 255) / 256 * (n / 256);
-    config = (n % 256 == 0 && m >= 1024 && tiles256 >= 192) ? 9 : 6;
+    config = (n % 256 == 0 && m >= 1024 && tiles256 >= 192) ? 20 : 6;
   }
   // Configurations with a 256-wide N tile need n % 256 == 0; the others
   // (N tile 128) take any n % 128 == 0.
   const bool wide_n = config == 2 || config == 4 || config == 7 || (config >= 9 && config <= 12) || config == 14 ||
-                      config == 15 || config == 17;
+                      config == 15 || config == 17 || config == 19 || config == 20;
   // The persistent loop needs at least two k-steps.
-  if (k < 512 && (config == 12 || config == 13)) config = config == 12 ? 9 : 6;
+  if (k < 512 && (config == 12 || config == 13 || config == 19 || config == 20))
+    config = config == 13 ? 6 : config == 20 ? 15 : 9;
   if (wide_n && n % 256 != 0) config = 5;
   switch (config) {
     case 0: return launch_dense_any<Tile128x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
@@ -1037,6 +1358,8 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
     case 16: return launch_dma_any<DmaH256x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case 17: return launch_dma_any<DmaH128x256>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case 18: return launch_dma_any<DmaH256x128Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 19: return launch_dma_persist_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 20: return launch_dma_persist_any<Dma256x256W8Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     default: return hipErrorInvalidValue;
   }
 }

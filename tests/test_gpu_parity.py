@@ -211,6 +211,36 @@ def test_gemm_residual_matches_oracle(m):
         assert_same_u16(bf16_host(got), want, f"residual m={m} config={cfg}")
 
 
+@pytest.mark.parametrize("resid", [False, True])
+def test_gemm_several_tiles_per_workgroup(resid):
+    """M8292 N4096 K512: 33 x 16 = 528 tiles of 256x256, more than twice the
+    workgroups a persistent grid holds on 256 CUs, so persistent workgroups
+    run two or three tiles each (a tile then starts on k-steps loaded during
+    the previous tile's last k-step), and the last row tile is ragged. Every
+    configuration agrees with the first over the whole output; sampled rows
+    bit-exact against the oracle (with and without the residual,
+    src/quantized.rs:1411-1552)."""
+    m, n, k = 8292, 4096, 512
+    rng = np.random.default_rng(8292 + resid)
+    x, _, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
+    res = randn_bf16(rng, (m, n), std=4.0) if resid else None
+    rows = np.unique(np.concatenate([[0, 255, 256, 4095, 8191, 8192, m - 1], rng.choice(m, 40, replace=False)]))
+    want = oracle.gemm(a_codes[rows], a_scales[rows], w_tiled, w_scales, n, k,
+                       residual=None if res is None else res[rows])
+    a = dev_prepared(x, stride)
+    qw = dev_weight(w_tiled, w_scales, n, k)
+    res_dev = to_dev_bf16(res) if resid else None
+    idx = torch.from_numpy(rows).to(DEV)
+    first = None
+    for cfg in range(clef_i4.gemm_configs()):
+        got = clef_i4.project_prepared(a, qw, residual=res_dev, config=cfg)
+        assert_same_u16(bf16_host(got[idx]), want, f"several tiles resid={resid} config={cfg}")
+        if first is None:
+            first = got
+        else:
+            assert torch.equal(got.view(torch.int16), first.view(torch.int16)), f"config {cfg} vs 0"
+
+
 def test_gemm_extreme_codes_and_saturation():
     """All codes at +-7 (|acc| = 49 K), huge scales (saturation to bf16 max),
     infinite and NaN activation scales (kernels/gemm_integer.loom:411-418)."""
