@@ -448,13 +448,90 @@ typedef unsigned v4u __attribute__((ext_vector_type(4)));
 template <class T>
 constexpr int kEpiWaveLds = 32 * T::WN * 2;
 
+// Scales of the staged epilogue, brought into the wave's LDS block by three
+// 4-byte LDS DMA instructions issued with the tile's last k-step: the wave's
+// WM row scales at byte 0 (rows past M read as zero) and its WN column scales
+// at byte 512. They land with the k-step's own DMA, so the epilogue reads
+// them from LDS instead of waiting on global loads.
+template <class T>
+__device__ __forceinline__ void epi_scales_dma(char* __restrict__ wlds, const float* __restrict__ as,
+                                               const float* __restrict__ ws, int64_t M, int64_t m0, int n0) {
+  static_assert(T::WM == 128 && T::WN == 64, "two row and one column instruction");
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+  const int64_t r0 = m0 + wm * T::WM;
+  const int64_t rows = M - r0 <= 0 ? 0 : (M - r0 < T::WM ? M - r0 : T::WM);
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(as + r0, (uint32_t)(rows * 4));
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(ws + n0 + wn * T::WN, T::WN * 4);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)wlds, 4, lane * 4, 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(wlds + 256), 4, lane * 4, 256, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(wlds + 512), 4, lane * 4, 0, 0, 0);
+}
+
+// Reads the scales placed by epi_scales_dma. `fast` (wave-uniform) holds when,
+// over the wave's rows below M and its columns, every scale is finite and
+// positive, ws * 2^-8 is exact, the largest product stays below bf16 max
+// (as in epi_scales_finish) and ws * 2^-8 * as >= 2^-126. Then a nonzero
+// accumulator never rounds to zero, so the "+ 0" of the G1 epilogue (which
+// only turns -0 into +0) is the identity and is left out. With `fast` the
+// column scales are returned already multiplied by 2^-8.
+template <class T>
+__device__ __forceinline__ EpiScales<T> epi_scales_from_lds(const char* __restrict__ wlds, int K, int64_t M,
+                                                            int64_t m0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / T::WAVES_N;
+  const int h = lane >> 5, lr = lane & 31;
+  const float inf = __builtin_huge_valf();
+  EpiScales<T> e;
+  bool ok = true;
+  float amax = 0.0f, amin = inf, wmax = 0.0f, wmin = inf;
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    e.asr[i] = *reinterpret_cast<const float*>(wlds + (32 * i + lr) * 4);
+    const float a = e.asr[i];
+    if (m0 + wm * T::WM + 32 * i + lr < M) {
+      ok = ok && a > 0.0f && a < inf;
+      amax = __builtin_fmaxf(amax, a);
+      amin = __builtin_fminf(amin, a);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      e.wsr[j][q] = *reinterpret_cast<const float4*>(wlds + 512 + (32 * j + 8 * q + 4 * h) * 4);
+      const float w4[4] = {e.wsr[j][q].x, e.wsr[j][q].y, e.wsr[j][q].z, e.wsr[j][q].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        ok = ok && w4[t] > 0.0f && w4[t] < inf && (w4[t] * 0.00390625f) * 256.0f == w4[t];
+        wmax = __builtin_fmaxf(wmax, w4[t]);
+        wmin = __builtin_fminf(wmin, w4[t]);
+      }
+    }
+  ok = ok && wmax * amax * (98.0f * (float)K) < kBf16Max && (wmin * 0.00390625f) * amin >= 0x1p-126f;
+  e.fast = __all(ok);
+  if (e.fast) {
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        e.wsr[j][q].x *= 0.00390625f;
+        e.wsr[j][q].y *= 0.00390625f;
+        e.wsr[j][q].z *= 0.00390625f;
+        e.wsr[j][q].w *= 0.00390625f;
+      }
+  }
+  return e;
+}
+
 // G1 tile epilogue through a wave-private LDS block: for each 32-row block i
 // the wave writes its bf16 results (8 bytes per lane per 4 columns, 16-byte
 // chunks XOR-swizzled by row), reads them back as 16 bytes of one row per
 // lane and stores whole 128-byte row segments (TM * 4 stores of 16 bytes per
 // lane instead of TM * TN * 4 stores of 8 bytes across 32 rows). LDS
 // operations of one wave execute in order, so block i + 1 may overwrite the
-// rows block i has read without a barrier. Same values as dense_epilogue.
+// rows block i has read without a barrier. Scales come from
+// epi_scales_from_lds. Same values as dense_epilogue.
 template <class T, bool RESID>
 __device__ __forceinline__ void staged_epilogue_store(const v16i (&acc)[T::TM][T::TN], const EpiScales<T>& e,
                                                       int64_t M, int N, int64_t m0, int n0,
@@ -483,9 +560,8 @@ __device__ __forceinline__ void staged_epilogue_store(const v16i (&acc)[T::TM][T
           float y[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            y[t] = (float)acc[i][j][4 * q + t] * (w4[t] * 0.00390625f);
+            y[t] = (float)acc[i][j][4 * q + t] * w4[t];
             y[t] = y[t] * asv;
-            y[t] = y[t] + 0.0f;
           }
           p0 = pack_bf16x2(y[0], y[1]);
           p1 = pack_bf16x2(y[2], y[3]);
@@ -563,9 +639,9 @@ __global__ __launch_bounds__(T::THREADS) void gemm_persistent_kernel(
 // so that `last` (read by the last k-step, then refilled with the next tile's
 // k-step 1) and `first` (filled with the next tile's k-step 0 during the last
 // k-step) are distinct restrict pointers throughout:
-//   DMA next k0 -> first; last k-step from `last`; drain + barrier;
-//   DMA next k1 -> last; last pair; epilogue (scales loaded before the k-step,
-//   stores straight from the accumulators);
+//   DMA this tile's scales -> wlds and next k0 -> first; last k-step from
+//   `last`; drain + barrier; DMA next k1 -> last; last pair; epilogue through
+//   the wave's LDS block `wlds`;
 //   k-step 0 of the next tile from `first`, then wait only for the k1 DMA:
 //   the epilogue's stores, issued after it, keep draining under the MFMAs.
 template <class T, bool RESID>
@@ -580,6 +656,7 @@ __device__ __forceinline__ void gemm_tile_turn(DmaCore<T>& c, v16i (&acc)[T::TM]
   (void)a_cur;
   (void)b_cur;
   constexpr int INST = T::A_INST + T::B_INST, MF = DmaCore<T>::MF, NF = DmaCore<T>::NF;
+  epi_scales_dma<T>(wlds, as, ws, M, m0, n0);
   if constexpr (T::SCHED == kSchedPin) {
     // The next tile's k-step-0 DMA and the reads of pair 0 ride on the MFMA
     // slots of the previous k-step's last substep, as in dma_kstep_next.
@@ -602,10 +679,6 @@ __device__ __forceinline__ void gemm_tile_turn(DmaCore<T>& c, v16i (&acc)[T::TM]
   c.pairs012(acc, last);
   wait_vmcnt<0>();
   __syncthreads();
-  // Scale loads first, then the k1 DMA: waiting for the loads leaves the DMA
-  // in flight (vector memory operations complete in issue order).
-  EpiScales<T> e;
-  epi_scales_issue<T>(e, as, ws, M, m0, n0);
   if constexpr (T::SCHED == kSchedPin) {
     auto extra = [&](int q) {
 #pragma unroll
@@ -618,7 +691,7 @@ __device__ __forceinline__ void gemm_tile_turn(DmaCore<T>& c, v16i (&acc)[T::TM]
     c.template substep<true, 0>(acc, 0, 1, 1, 1);
   }
   c.template substep<false, 0>(acc, 1, 0, 0, 0);
-  epi_scales_finish<T>(e, ksteps * 256);
+  const EpiScales<T> e = epi_scales_from_lds<T>(wlds, ksteps * 256, M, m0);
   // The scheduler must not start the next tile's MFMAs (fresh accumulators)
   // while this tile's accumulators are still being stored.
   __builtin_amdgcn_sched_barrier(0);
@@ -642,9 +715,10 @@ __device__ __forceinline__ void gemm_tile_turn(DmaCore<T>& c, v16i (&acc)[T::TM]
 // Persistent G1 on the DMA core: a workgroup walks tiles b, b + grid, ...
 // (grid a multiple of 8, so all of a workgroup's tiles map to its XCD). The
 // last k-step of a tile loads the next tile's k-step 0 into the free stage
-// while it computes, the epilogue stores straight from the accumulators
-// (no LDS), and the next tile starts on data already in LDS; the epilogue's
-// stores drain under the next tile's first k-step. Needs ksteps >= 2.
+// while it computes, the epilogue goes through a 4 KiB LDS block per wave
+// above the two stages, and the next tile starts on data already in LDS; the
+// epilogue's stores drain under the next tile's first k-step. Needs
+// ksteps >= 2.
 template <class T, bool RESID>
 __global__ __launch_bounds__(T::THREADS) void gemm_dma_persist_kernel(
     const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
@@ -701,7 +775,8 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dma_persist_kernel(
     const Tile nxt = tile(has_next ? tn_next : t);
     gemm_tile_turn<T, RESID>(c, acc, stage(g + kb - 1), stage(g + kb), cur.a_rsrc, cur.b_rsrc, nxt.a_rsrc,
                              nxt.b_rsrc, voff_a, a_q_stride, kb, as, ws, M, N, cur.m0, cur.n0, residual, out,
-                             lds + T::LDS_BYTES + (threadIdx.x >> 6) * kEpiWaveLds<T>, has_next);
+                             lds + T::LDS_BYTES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kEpiWaveLds<T>,
+                             has_next);
     if (!has_next) break;
     g += kb;
     t = tn_next;
