@@ -448,24 +448,28 @@ typedef unsigned v4u __attribute__((ext_vector_type(4)));
 template <class T>
 constexpr int kEpiWaveLds = 32 * T::WN * 2;
 
-// Scales of the staged epilogue, brought into the wave's LDS block by three
-// 4-byte LDS DMA instructions issued with the tile's last k-step: the wave's
-// WM row scales at byte 0 (rows past M read as zero) and its WN column scales
-// at byte 512. They land with the k-step's own DMA, so the epilogue reads
+// Scales of the staged epilogue, brought into the wave's LDS block by 4-byte
+// LDS DMA instructions (64 scales each) issued with the tile's last k-step:
+// the wave's WM row scales at byte 0 (rows past M read as zero) and its WN
+// column scales at byte 512. They land with the k-step's own DMA, so the epilogue reads
 // them from LDS instead of waiting on global loads.
 template <class T>
 __device__ __forceinline__ void epi_scales_dma(char* __restrict__ wlds, const float* __restrict__ as,
                                                const float* __restrict__ ws, int64_t M, int64_t m0, int n0) {
-  static_assert(T::WM == 128 && T::WN == 64, "two row and one column instruction");
+  static_assert(T::WM % 64 == 0 && T::WM <= 128 && T::WN % 64 == 0 && T::WN <= 128, "scale slots");
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
   const int64_t r0 = m0 + wm * T::WM;
   const int64_t rows = M - r0 <= 0 ? 0 : (M - r0 < T::WM ? M - r0 : T::WM);
   const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(as + r0, (uint32_t)(rows * 4));
   const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(ws + n0 + wn * T::WN, T::WN * 4);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)wlds, 4, lane * 4, 0, 0, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(wlds + 256), 4, lane * 4, 256, 0, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(wlds + 512), 4, lane * 4, 0, 0, 0);
+#pragma unroll
+  for (int r = 0; r < T::WM / 64; ++r)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(wlds + 256 * r), 4, lane * 4, 256 * r, 0, 0);
+#pragma unroll
+  for (int c = 0; c < T::WN / 64; ++c)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(wlds + 512 + 256 * c), 4, lane * 4, 256 * c, 0,
+                                             0);
 }
 
 // Reads the scales placed by epi_scales_dma. `fast` (wave-uniform) holds when,
@@ -526,9 +530,10 @@ __device__ __forceinline__ EpiScales<T> epi_scales_from_lds(const char* __restri
 
 // G1 tile epilogue through a wave-private LDS block: for each 32-row block i
 // the wave writes its bf16 results (8 bytes per lane per 4 columns, 16-byte
-// chunks XOR-swizzled by row), reads them back as 16 bytes of one row per
-// lane and stores whole 128-byte row segments (TM * 4 stores of 16 bytes per
-// lane instead of TM * TN * 4 stores of 8 bytes across 32 rows). LDS
+// chunks XOR-swizzled by row within each 128-byte line), reads them back as
+// 16 bytes of one row per lane and stores whole row segments of WN columns
+// (TM * TN * 2 stores of 16 bytes per lane instead of TM * TN * 4 stores of
+// 8 bytes across 32 rows). LDS
 // operations of one wave execute in order, so block i + 1 may overwrite the
 // rows block i has read without a barrier. Scales come from
 // epi_scales_from_lds. Same values as dense_epilogue.
@@ -537,7 +542,8 @@ __device__ __forceinline__ void staged_epilogue_store(const v16i (&acc)[T::TM][T
                                                       int64_t M, int N, int64_t m0, int n0,
                                                       const uint16_t* __restrict__ residual,
                                                       uint16_t* __restrict__ out, char* __restrict__ wlds) {
-  static_assert(T::WN == 64, "one 128-byte row segment per wave");
+  static_assert(T::WN == 64 || T::WN == 128, "one or two 128-byte lines per wave row");
+  constexpr int kRowBytes = T::WN * 2, kLanesPerRow = T::WN / 8, kRowsPerRead = 64 / kLanesPerRow;
   constexpr int kReads = kEpiWaveLds<T> / 1024;  // 16-byte reads per lane per block
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
@@ -570,15 +576,15 @@ __device__ __forceinline__ void staged_epilogue_store(const v16i (&acc)[T::TM][T
           p1 = g1_value(acc[i][j][4 * q + 2], wsv.z, asv) | (g1_value(acc[i][j][4 * q + 3], wsv.w, asv) << 16);
         }
         const int chunk = 4 * j + q;  // 16-byte chunk of the row: columns 8 * chunk .. + 7
-        *reinterpret_cast<v2u*>(wlds + lr * 128 + ((chunk ^ (lr & 7)) << 4) + 8 * h) = v2u{p0, p1};
+        *reinterpret_cast<v2u*>(wlds + lr * kRowBytes + ((chunk ^ (lr & 7)) << 4) + 8 * h) = v2u{p0, p1};
       }
 #pragma unroll
     for (int r = 0; r < kReads; ++r) {
-      const int row = 8 * r + (lane >> 3), chunk = lane & 7;
-      v4u v = *reinterpret_cast<const v4u*>(wlds + row * 128 + ((chunk ^ (lane >> 3)) << 4));
+      const int lrow = lane / kLanesPerRow, row = kRowsPerRead * r + lrow, chunk = lane % kLanesPerRow;
+      v4u v = *reinterpret_cast<const v4u*>(wlds + row * kRowBytes + ((chunk ^ (row & 7)) << 4));
       // lane part in the VGPR offset, the block's rows in the scalar offset
-      const int voff = ((wm * T::WM + (lane >> 3)) * N + n0 + wn * T::WN + 8 * chunk) * 2;
-      const int soff = (32 * i + 8 * r) * N * 2;
+      const int voff = ((wm * T::WM + lrow) * N + n0 + wn * T::WN + 8 * chunk) * 2;
+      const int soff = (32 * i + kRowsPerRead * r) * N * 2;
       if (RESID) {
         const v4i rv = __builtin_amdgcn_raw_buffer_load_b128(res_rsrc, voff, soff, 0);
 #pragma unroll
@@ -1383,7 +1389,7 @@ hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, c
 
 }  // namespace
 
-int gemm_config_count() { return 21; }
+int gemm_config_count() { return 22; }
 
 hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
@@ -1408,10 +1414,10 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
   // Configurations with a 256-wide N tile need n % 256 == 0; the others
   // (N tile 128) take any n % 128 == 0.
   const bool wide_n = config == 2 || config == 4 || config == 7 || (config >= 9 && config <= 12) || config == 14 ||
-                      config == 15 || config == 17 || config == 19 || config == 20;
+                      config == 15 || config == 17 || config >= 19;
   // The persistent loop needs at least two k-steps.
-  if (k < 512 && (config == 12 || config == 13 || config == 19 || config == 20))
-    config = config == 13 ? 6 : config == 20 ? 15 : 9;
+  if (k < 512 && (config == 12 || config == 13 || config >= 19))
+    config = config == 13 ? 6 : config == 20 ? 15 : config == 21 ? 14 : 9;
   if (wide_n && n % 256 != 0) config = 5;
   switch (config) {
     case 0: return launch_dense_any<Tile128x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
@@ -1435,6 +1441,7 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
     case 18: return launch_dma_any<DmaH256x128Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case 19: return launch_dma_persist_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case 20: return launch_dma_persist_any<Dma256x256W8Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 21: return launch_dma_persist_any<Dma256x256Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     default: return hipErrorInvalidValue;
   }
 }
