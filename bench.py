@@ -11,6 +11,9 @@ M=4096 on one MI355X.
                -> SwiGLU -> combine, timed over --steps layer calls.
   mlp_*        INT4-MLP dense block, 4096 x 4096 input, gate|up 24576 x 4096,
                down 4096 x 12288: quantize -> GEMM -> SwiGLU+quantize -> GEMM.
+  int8_gemm_*  the INT8 x INT8 projection at the GEMM's shape.
+  small_m_*    M = 1, 16, 64 on the GEMM's weight (K4096 N12288): GPU time per
+               call (HIP graph replay) and HBM GB/s of the bytes the call moves.
   roofline     the GEMM kernel against the int8 MFMA peak (5.0 POP/s).
   cpu_baseline the CPU oracle (quantize + i32 matmul + epilogue; MoE layer) on
                a bounded sample, timed on this host's cores.
@@ -46,7 +49,7 @@ def parse():
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=600)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--only", choices=["gemm", "moe", "mlp", "i8", "copy", "peaks"], default=None,
+    p.add_argument("--only", choices=["gemm", "moe", "mlp", "i8", "smallm", "copy", "peaks"], default=None,
                    help="run one leg; 'copy' is a plain 512 MiB device copy, the known-size "
                         "kernel that scales HBM byte counters")
     return p.parse_args()
@@ -94,6 +97,51 @@ def gemm_leg(args):
     nbytes = m * k // 2 + 4 * m + n * k // 2 + 4 * n + 2 * m * n
     return {"m": m, "n": n, "k": k, "ms": ms, "tops": ops / ms / 1e9, "prepare_ms": prep_ms,
             "ops": ops, "bytes": nbytes}
+
+
+def graph_timed(fn, calls=50, replays=8):
+    """GPU-side ms per call of fn: `calls` calls captured in one HIP graph,
+    replayed `replays` times. For kernels of a few microseconds, where the
+    host's per-call launch cost would otherwise be what is measured."""
+    import torch
+
+    for _ in range(20):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (calls * replays)
+
+
+def small_m_leg(args):
+    """Decode-sized projections on the headline weight (K4096 N12288): the
+    weight stream is the whole cost, so the figure of merit is HBM GB/s
+    (weight codes and scales, activation, output)."""
+    import torch
+
+    import clef_i4
+
+    k, n = 4096, 12288
+    qw = clef_i4.load_quantized_weight(bf16_randn((n, k), 0.02, 1002 * 16 + 1))
+    res = {}
+    for m in (1, 16, 64):
+        a = clef_i4.prepare(bf16_randn((m, k), 1.0, 1002 * 16 + 0))
+        out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        ms = graph_timed(lambda: clef_i4.project_prepared(a, qw, out=out))
+        nbytes = n * k // 2 + 4 * n + m * (k // 2 + 4) + 2 * m * n
+        res[m] = {"us": ms * 1e3, "gbs": nbytes / ms / 1e6}
+    return res
 
 
 def i8_leg(args):
@@ -240,6 +288,8 @@ def main():
         res["mlp"] = mlp_leg(args)
     if args.only in (None, "i8"):
         res["i8"] = i8_leg(args)
+    if args.only in (None, "smallm"):
+        res["smallm"] = small_m_leg(args)
     if args.only == "peaks":
         import subprocess
         probe = os.path.join(ROOT, "clef-hrx_amd", "lib", "peaks")
@@ -288,6 +338,9 @@ def main():
     if "i8" in res:
         line["int8_gemm_ms"] = round(res["i8"]["ms"], 4)
         line["int8_gemm_tops"] = round(res["i8"]["tops"], 1)
+    if "smallm" in res:
+        line["small_m_k4096_n12288"] = {f"m{m}": {"us": round(v["us"], 2), "hbm_gbs": round(v["gbs"], 1)}
+                                        for m, v in res["smallm"].items()}
     if cpu:
         line["cpu_baseline"] = cpu
         if "moe" in res:

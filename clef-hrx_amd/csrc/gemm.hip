@@ -1387,9 +1387,145 @@ hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, c
                               const int32_t* schedule, int64_t tokens, int topk, int k, int n, int input_routed,
                               uint16_t* out, hipStream_t stream);
 
+// Small-M G1: with few activation rows the weight stream is the whole cost,
+// and N / 128 workgroups walking all of K leave most of the GPU and of HBM
+// idle. Here a workgroup of NW waves (16, or 8 with four row blocks) owns 32
+// output columns and up to 32 * MT rows, and the waves split the k-steps
+// between them. Each wave loads its 32
+// weight rows and MT * 32 activation rows straight into registers (64 bytes
+// per lane per row block per k-step: lane half h takes chunks 4h .. 4h+3 of
+// the row's 128-byte k-step, the lane -> k map of the LDS cores) with the
+// next k-step's loads in flight while the current one computes. The NW
+// partial accumulators meet in LDS by integer atomic adds (exact in any
+// order), and the G1 epilogue runs on the sums.
+template <int MT, int NW, bool RESID>
+__global__ __launch_bounds__(NW * 64) void gemm_skinny_kernel(const uint32_t* __restrict__ a, int a_words,
+                                                          const float* __restrict__ as, const uint32_t* __restrict__ w,
+                                                          const float* __restrict__ ws, int64_t M, int N, int kb,
+                                                          const uint16_t* __restrict__ residual,
+                                                          uint16_t* __restrict__ out) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __shared__ int red[MT][16][64];  // [row block][accumulator register][lane]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 31, h = lane >> 5;
+  const int n0 = blockIdx.x * 32;
+  const int64_t m0 = (int64_t)blockIdx.y * (32 * MT);
+  const int64_t rows = M - m0 < 32 * MT ? M - m0 : 32 * MT;
+  for (int i = threadIdx.x; i < MT * 16 * 64; i += NW * 64) (&red[0][0][0])[i] = 0;
+
+  // Weight row n0 + lr of k-step kt: tiled block (n / 128, kt), row n % 128.
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(w + (int64_t)(n0 / 128) * kb * 4096, (uint32_t)(kb * 16384));
+  const int w_voff = ((n0 % 128) + lr) * 128 + 64 * h;
+  // Activation rows past M read as zero (outside the resource's range).
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a + m0 * a_words, (uint32_t)(rows * a_words * 4));
+  int a_voff[MT];
+#pragma unroll
+  for (int f = 0; f < MT; ++f) a_voff[f] = (32 * f + lr) * a_words * 4 + 64 * h;
+
+  v16i acc[MT];
+#pragma unroll
+  for (int f = 0; f < MT; ++f) acc[f] = v16i{};
+  v4i wr[2][4], ar[2][MT][4];
+  auto load = [&](auto buf, int kt) {
+    constexpr int B = decltype(buf)::value;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) wr[B][c] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff + 16 * c, kt * 16384, 0);
+#pragma unroll
+    for (int f = 0; f < MT; ++f)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        ar[B][f][c] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff[f] + 16 * c, kt * 128, 0);
+  };
+  auto compute = [&](auto buf) {
+    constexpr int B = decltype(buf)::value;
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const v4i& x = wr[B][p];
+        const v4i uw = half ? unpack_pair(x.z, x.w) : unpack_pair(x.x, x.y);
+#pragma unroll
+        for (int f = 0; f < MT; ++f) {
+          const v4i& y = ar[B][f][p];
+          const v4i ua = half ? unpack_pair(y.z, y.w) : unpack_pair(y.x, y.y);
+          acc[f] = mfma32_i8(uw, ua, acc[f]);
+        }
+      }
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  const int k0 = wave * kb / NW, k1 = (wave + 1) * kb / NW;
+  if (k0 < k1) {
+    // The load after the last k-step repeats it (never used), so the body has
+    // no branch around its loads and the waits stay exact.
+    load(B0{}, k0);
+    for (int kt = k0;;) {
+      load(B1{}, kt + 1 < k1 ? kt + 1 : kt);
+      compute(B0{});
+      if (++kt >= k1) break;
+      load(B0{}, kt + 1 < k1 ? kt + 1 : kt);
+      compute(B1{});
+      if (++kt >= k1) break;
+    }
+  }
+  __syncthreads();  // reduction buffer zeroed
+#pragma unroll
+  for (int f = 0; f < MT; ++f)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) atomicAdd(&red[f][r][lane], acc[f][r]);
+  __syncthreads();
+
+  // Epilogue: item g = (row block f, register quad rq, lane) gives row
+  // m0 + 32 f + lane % 32 and columns n0 + 8 rq + 4 (lane / 32) + 0..3.
+  for (int g = threadIdx.x; g < MT * 256; g += NW * 64) {
+    const int f = g >> 8, rq = (g >> 6) & 3, ln = g & 63;
+    const int64_t m = m0 + 32 * f + (ln & 31);
+    if (m >= M) continue;
+    const int col = n0 + 8 * rq + 4 * (ln >> 5);
+    const float asv = as[m];
+    const float4 wsv = *reinterpret_cast<const float4*>(ws + col);
+    uint32_t p0 = g1_value(red[f][4 * rq + 0][ln], wsv.x, asv) | (g1_value(red[f][4 * rq + 1][ln], wsv.y, asv) << 16);
+    uint32_t p1 = g1_value(red[f][4 * rq + 2][ln], wsv.z, asv) | (g1_value(red[f][4 * rq + 3][ln], wsv.w, asv) << 16);
+    uint16_t* dst = out + m * N + col;
+    if (RESID) {
+      const uint2 rv = *reinterpret_cast<const uint2*>(residual + m * N + col);
+      p0 = pack_bf16x2(bf16_lo(rv.x) + bf16_lo(p0), bf16_hi(rv.x) + bf16_hi(p0));
+      p1 = pack_bf16x2(bf16_lo(rv.y) + bf16_lo(p1), bf16_hi(rv.y) + bf16_hi(p1));
+    }
+    *reinterpret_cast<uint2*>(dst) = make_uint2(p0, p1);
+  }
+#endif
+}
+
+template <int MT, bool RESID>
+hipError_t launch_skinny(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                         int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  const int64_t groups = (m + 32 * MT - 1) / (32 * MT);
+  if (groups > 65535) return hipErrorInvalidValue;
+  constexpr int NW = MT == 4 ? 8 : 16;  // four row blocks need 256 VGPRs: two waves per SIMD
+  gemm_skinny_kernel<MT, NW, RESID><<<dim3((unsigned)(n / 32), (unsigned)groups), NW * 64, 0, stream>>>(
+      a, a_words, as, w, ws, m, n, k / 256, residual, out);
+  return hipGetLastError();
+}
+
+template <bool RESID>
+hipError_t launch_skinny_m(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  if (m <= 32) return launch_skinny<1, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (m <= 64) return launch_skinny<2, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return launch_skinny<4, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+}
+
+hipError_t launch_skinny_any(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                             int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  if (residual) return launch_skinny_m<true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return launch_skinny_m<false>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+}
+
 }  // namespace
 
-int gemm_config_count() { return 22; }
+int gemm_config_count() { return 23; }
 
 hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
@@ -1408,15 +1544,24 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
     // each next tile's first k-steps under the current tile's last one
     // (M4096 N12288 K4096: 154 us against 160 us with one workgroup per
     // tile); 128x128 tiles otherwise.
+    // Few rows: the weight stream dominates and 128x128 tiles give too few
+    // workgroups, so the K-split skinny kernel (GPU time, graph replay:
+    // M1 N4096 K4096 5.1 us against 17.4; M64 N12288 K4096 13.0 against
+    // 17.8; M128 N12288 K4096 29.1 against 18.3, where 96 tiles of 128x128
+    // already cover most CUs).
+    const int64_t tiles128 = (m + 127) / 128 * (n / 128);
     const int64_t tiles256 = (m + 255) / 256 * (n / 256);
-    config = (n % 256 == 0 && m >= 1024 && tiles256 >= 192) ? 20 : 6;
+    if (m <= 64 || (m <= 256 && tiles128 < 96))
+      config = 22;
+    else
+      config = (n % 256 == 0 && m >= 1024 && tiles256 >= 192) ? 20 : 6;
   }
   // Configurations with a 256-wide N tile need n % 256 == 0; the others
   // (N tile 128) take any n % 128 == 0.
   const bool wide_n = config == 2 || config == 4 || config == 7 || (config >= 9 && config <= 12) || config == 14 ||
-                      config == 15 || config == 17 || config >= 19;
+                      config == 15 || config == 17 || (config >= 19 && config <= 21);
   // The persistent loop needs at least two k-steps.
-  if (k < 512 && (config == 12 || config == 13 || config >= 19))
+  if (k < 512 && (config == 12 || config == 13 || (config >= 19 && config <= 21)))
     config = config == 13 ? 6 : config == 20 ? 15 : config == 21 ? 14 : 9;
   if (wide_n && n % 256 != 0) config = 5;
   switch (config) {
@@ -1442,6 +1587,7 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
     case 19: return launch_dma_persist_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case 20: return launch_dma_persist_any<Dma256x256W8Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case 21: return launch_dma_persist_any<Dma256x256Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case 22: return launch_skinny_any(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     default: return hipErrorInvalidValue;
   }
 }
