@@ -37,7 +37,7 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE and WRITE_SIZE passes over `bench.py --only gemm`, each scaled by
 # the reading for a plain 512 MiB copy (x2.000 fetch, x1.000 write); the runs
 # and raw readings are in profiles/int4_gemm_m4096_k4096_n12288.txt.
-GEMM_TRAFFIC_BYTES = 269.76e6
+GEMM_TRAFFIC_BYTES = 257.16e6
 
 
 def parse():
