@@ -49,6 +49,9 @@ def parse():
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=600)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--moe-tokens", type=int, default=4096,
+                   help="tokens of the MoE leg (4096 is the benchmark workload; small counts show the "
+                        "decode-sized path)")
     p.add_argument("--only", choices=["gemm", "moe", "mlp", "i8", "smallm", "copy", "peaks"], default=None,
                    help="run one leg; 'copy' is a plain 512 MiB device copy, the known-size "
                         "kernel that scales HBM byte counters")
@@ -196,7 +199,7 @@ def moe_leg(args):
 
     import clef_i4
 
-    t, d, inter = 4096, 2048, 768
+    t, d, inter = args.moe_tokens, 2048, 768
     x = bf16_randn((t, d), 1.0, 1004 * 16 + 0)
     logits = bf16_randn((t, 128), 1.0, 1004 * 16 + 1)
     gate = clef_i4.load_quantized_weight(bf16_randn((128 * inter, d), 0.02, 1004 * 16 + 2))
@@ -329,6 +332,8 @@ def main():
                             "traffic": GEMM_TRAFFIC_BYTES,
                             "algorithmic_bytes": g["bytes"]}
     if "moe" in res:
+        if res["moe"]["tokens"] != 4096:
+            line["moe_tokens"] = res["moe"]["tokens"]
         line["moe_tokens_per_s"] = round(res["moe"]["tokens_per_s"], 1)
         line["moe_layer_ms"] = round(res["moe"]["ms"], 4)
         line["moe_tops"] = round(res["moe"]["tops"], 1)

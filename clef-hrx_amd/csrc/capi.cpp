@@ -301,7 +301,7 @@ int clef_moe_expert_i4(const uint32_t* a, int32_t stride, const float* a_scales,
     return fail(kAlign);
   if (workspace_bytes < clef_moe_expert_workspace_bytes(tokens, topk)) return fail(kWorkspace);
   int32_t* schedule = static_cast<int32_t*>(workspace);
-  if (int rc = hip_status(clef::launch_expert_schedule(groups, tokens, schedule, hs(stream)))) return rc;
+  if (int rc = hip_status(clef::launch_expert_schedule(groups, tokens, topk, schedule, hs(stream)))) return rc;
   return hip_status(clef::launch_expert_i4(a, stride / 8, a_scales, w_tiled, w_scales, groups, schedule,
                                            tokens, topk, k, n, input_routed ? 1 : 0, out, hs(stream)));
 }
@@ -322,7 +322,7 @@ int clef_moe_expert_gate_up_i4(const uint32_t* a, int32_t stride, const float* a
     return fail(kAlign);
   if (workspace_bytes < clef_moe_expert_workspace_bytes(tokens, topk)) return fail(kWorkspace);
   int32_t* schedule = static_cast<int32_t*>(workspace);
-  if (int rc = hip_status(clef::launch_expert_schedule(groups, tokens, schedule, hs(stream)))) return rc;
+  if (int rc = hip_status(clef::launch_expert_schedule(groups, tokens, topk, schedule, hs(stream)))) return rc;
   return hip_status(clef::launch_expert_gate_up(a, stride / 8, a_scales, gate_w, gate_s, up_w, up_s, groups,
                                                 schedule, tokens, topk, k, n, h, hs(stream)));
 }
@@ -426,7 +426,7 @@ int clef_moe_layer(const uint16_t* x, const void* logits, int32_t logits_dtype, 
   if (int rc = hip_status(call)) return rc
   CLEF_STEP(clef::launch_route(logits, logits_dtype, tokens, experts, topk, routes, s));
   CLEF_STEP(clef::launch_group_routes(routes, tokens, topk, groups, order, ws + l.group_ws, s, schedule,
-                                      clef::expert_tile_rows()));
+                                      clef::expert_tile_rows(routed)));
   CLEF_STEP(clef::launch_prepare(x, tokens, hidden, sx, 4, ax, s));
   if (tokens * (int64_t)(sx / 8) * 4 < ((int64_t)1 << 31)) {
     // Gate and up share one pass over the gathered x rows and SwiGLU runs in

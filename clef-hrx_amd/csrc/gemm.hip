@@ -1523,6 +1523,134 @@ hipError_t launch_skinny_any(const uint32_t* a, int a_words, const float* as, co
   return launch_skinny_m<false>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
 }
 
+// Grouped expert GEMM for few routed rows per expert (decode-sized batches),
+// on the schedule's 32-slot tiles: the small-M scheme of gemm_skinny_kernel
+// with gathered activation rows. A workgroup of min(16, k-steps) waves owns one
+// tile and 32 output columns of the expert (GU: 32 gate and the same 32 up columns); the
+// waves split the k-steps, load the expert's weight rows and the slots'
+// activation rows (routed: route; else route / topk; slots past the group's
+// end read zeros) into registers, and the partial sums meet in LDS by integer
+// atomic adds. Epilogue: E1 as expert_dmah_kernel (and for GU, S1 on the bf16
+// gate and up values), stored to the slots' routed rows.
+template <bool GU>
+__global__ __launch_bounds__(1024) void expert_skinny_kernel(
+    const uint32_t* __restrict__ a, int a_words, uint32_t a_bytes, const float* __restrict__ as,
+    const uint32_t* __restrict__ w, const float* __restrict__ ws, const uint32_t* __restrict__ w2,
+    const float* __restrict__ ws2, const float* __restrict__ groups, const int32_t* __restrict__ schedule,
+    int64_t tokens, int topk, int kb, int n, int input_routed, uint16_t* __restrict__ out, int slices) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int NA = GU ? 2 : 1;
+  const int NW = (int)blockDim.x >> 6;
+  __shared__ int red[NA][16][64];  // [gate / up][accumulator register][lane]
+  __shared__ int routes_s[32];
+  const int64_t item = blockIdx.x;
+  if (item >= (int64_t)schedule[0] * slices) return;
+  const int tile = (int)(item / slices);
+  const int c0 = (int)(item - (int64_t)tile * slices) * 32;  // first output column within the expert
+  const int e = schedule[1 + 2 * tile];
+  const int row0 = schedule[2 + 2 * tile];
+  const float* list = groups + (int64_t)e * (tokens + 1);
+  const int count = (int)list[0];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 31, h = lane >> 5;
+  for (int i = threadIdx.x; i < NA * 16 * 64; i += NW * 64) (&red[0][0][0])[i] = 0;
+  if (threadIdx.x < 32) routes_s[threadIdx.x] = row0 + (int)threadIdx.x < count ? (int)list[1 + row0 + threadIdx.x] : -1;
+
+  const int my_route = row0 + lr < count ? (int)list[1 + row0 + lr] : -1;
+  const int64_t xr = input_routed ? (int64_t)my_route : (int64_t)my_route / topk;
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a, a_bytes);
+  const int a_voff = my_route >= 0 ? (int)(xr * a_words * 4) + 64 * h : (int)0x80000000u;
+  const int64_t nrow = (int64_t)e * n + c0;  // first weight row of the slice
+  const int w_voff = (int)(nrow % 128 + lr) * 128 + 64 * h;
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(w + (nrow / 128) * kb * 4096, (uint32_t)(kb * 16384));
+  const __amdgpu_buffer_rsrc_t w2_rsrc = make_rsrc((GU ? w2 : w) + (nrow / 128) * kb * 4096, (uint32_t)(kb * 16384));
+
+  v16i acc[NA];
+#pragma unroll
+  for (int s = 0; s < NA; ++s) acc[s] = v16i{};
+  v4i wr[2][NA][4], ar[2][4];
+  auto load = [&](auto buf, int kt) {
+    constexpr int B = decltype(buf)::value;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      wr[B][0][c] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff + 16 * c, kt * 16384, 0);
+      if constexpr (GU) wr[B][1][c] = __builtin_amdgcn_raw_buffer_load_b128(w2_rsrc, w_voff + 16 * c, kt * 16384, 0);
+      ar[B][c] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff + 16 * c, kt * 128, 0);
+    }
+  };
+  auto compute = [&](auto buf) {
+    constexpr int B = decltype(buf)::value;
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const v4i& y = ar[B][p];
+        const v4i ua = half ? unpack_pair(y.z, y.w) : unpack_pair(y.x, y.y);
+#pragma unroll
+        for (int s = 0; s < NA; ++s) {
+          const v4i& x = wr[B][s][p];
+          acc[s] = mfma32_i8(half ? unpack_pair(x.z, x.w) : unpack_pair(x.x, x.y), ua, acc[s]);
+        }
+      }
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  const int k0 = wave * kb / NW, k1 = (wave + 1) * kb / NW;
+  if (k0 < k1) {
+    load(B0{}, k0);
+    for (int kt = k0;;) {
+      load(B1{}, kt + 1 < k1 ? kt + 1 : kt);
+      compute(B0{});
+      if (++kt >= k1) break;
+      load(B0{}, kt + 1 < k1 ? kt + 1 : kt);
+      compute(B1{});
+      if (++kt >= k1) break;
+    }
+  }
+  __syncthreads();  // reduction buffer zeroed, slot routes written
+#pragma unroll
+  for (int s = 0; s < NA; ++s)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) atomicAdd(&red[s][r][lane], acc[s][r]);
+  __syncthreads();
+
+  // Item g = (register quad rq, lane): slot lane % 32, columns
+  // c0 + 8 rq + 4 (lane / 32) + 0..3.
+  for (int g = threadIdx.x; g < 256; g += NW * 64) {
+    const int rq = g >> 6, ln = g & 63;
+    const int route = routes_s[ln & 31];
+    if (route >= 0) {
+      const int col = c0 + 8 * rq + 4 * (ln >> 5);
+      const float asv = as[input_routed ? (int64_t)route : (int64_t)route / topk];
+      const float4 wg4 = *reinterpret_cast<const float4*>(ws + (int64_t)e * n + col);
+      const float wg[4] = {wg4.x, wg4.y, wg4.z, wg4.w};
+      float y[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) y[t] = (float)(red[0][4 * rq + t][ln] >> 8) * (asv * wg[t]);
+      if constexpr (GU) {
+        const float4 wu4 = *reinterpret_cast<const float4*>(ws2 + (int64_t)e * n + col);
+        const float wu[4] = {wu4.x, wu4.y, wu4.z, wu4.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float g = as_float(pack_bf16x2(0.0f, y[t]));  // bf16(gate)
+          const float u = (float)(red[1][4 * rq + t][ln] >> 8) * (asv * wu[t]);
+          y[t] = silu_bf16(g) * bf16_round(u);
+        }
+      }
+      *reinterpret_cast<uint2*>(out + (int64_t)route * n + col) =
+          make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+    }
+  }
+#endif
+}
+
+template <bool GU>
+hipError_t launch_expert_skinny(const uint32_t* a, int a_words, int64_t a_bytes, const float* as,
+                                const uint32_t* w, const float* ws, const uint32_t* w2, const float* ws2,
+                                const float* groups, const int32_t* schedule, int64_t tokens, int topk, int k,
+                                int n, int input_routed, uint16_t* out, hipStream_t stream);
+
 }  // namespace
 
 int gemm_config_count() { return 23; }
@@ -1592,8 +1720,36 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
   }
 }
 
-int64_t expert_max_tiles(int64_t routes) { return (routes + kExpertBM - 1) / kExpertBM + 128; }
-int expert_tile_rows() { return kExpertBM; }
+// Routed rows up to which the grouped expert GEMMs use 32-slot tiles and
+// expert_skinny_kernel (on average 16 rows per expert at 128 experts).
+constexpr int64_t kExpertSkinnyRoutes = 2048;
+constexpr int kExpertSkinnyBM = 32;
+
+int expert_tile_rows(int64_t routes) { return routes <= kExpertSkinnyRoutes ? kExpertSkinnyBM : kExpertBM; }
+
+// Tiles of the schedule: sum over experts of ceil(count / bm) <= routes / bm
+// rounded up, plus one per expert with any route.
+int64_t expert_max_tiles(int64_t routes) {
+  const int bm = expert_tile_rows(routes);
+  return (routes + bm - 1) / bm + (routes < 128 ? routes : 128);
+}
+
+namespace {
+template <bool GU>
+hipError_t launch_expert_skinny(const uint32_t* a, int a_words, int64_t a_bytes, const float* as,
+                                const uint32_t* w, const float* ws, const uint32_t* w2, const float* ws2,
+                                const float* groups, const int32_t* schedule, int64_t tokens, int topk, int k,
+                                int n, int input_routed, uint16_t* out, hipStream_t stream) {
+  if (a_bytes >= ((int64_t)1 << 31) || n % 32 != 0) return hipErrorInvalidValue;
+  const int slices = n / 32;
+  const int64_t blocks = expert_max_tiles(tokens * topk) * slices;
+  const int waves = k / 256 < 16 ? k / 256 : 16;  // one k-step per wave at most needs no more waves
+  expert_skinny_kernel<GU><<<(unsigned)blocks, 64 * waves, 0, stream>>>(a, a_words, (uint32_t)a_bytes, as, w, ws, w2,
+                                                                   ws2, groups, schedule, tokens, topk, k / 256,
+                                                                   n, input_routed, out, slices);
+  return hipGetLastError();
+}
+}  // namespace
 
 namespace {
 template <class T, bool GU>
@@ -1624,6 +1780,9 @@ hipError_t launch_expert_gate_up(const uint32_t* a, int a_words, const float* as
                                  hipStream_t stream) {
   const int64_t a_bytes = tokens * a_words * 4;
   if (a_bytes >= ((int64_t)1 << 31) || n % 128 != 0) return hipErrorInvalidValue;
+  if (expert_tile_rows(tokens * topk) == kExpertSkinnyBM)
+    return launch_expert_skinny<true>(a, a_words, a_bytes, as, gate_w, gate_s, up_w, up_s, groups, schedule, tokens,
+                                      topk, k, n, 0, h, stream);
   return launch_expert_dmah<ExpertGUTile, true>(a, a_words, a_bytes, as, gate_w, gate_s, up_w, up_s, groups,
                                                 schedule, tokens, topk, k, n, 0, h, stream);
 }
@@ -1632,9 +1791,9 @@ size_t expert_schedule_bytes(int64_t routes) {
   return (size_t)(1 + 2 * expert_max_tiles(routes)) * sizeof(int32_t);
 }
 
-hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int32_t* schedule,
+hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int topk, int32_t* schedule,
                                   hipStream_t stream) {
-  tile_list_kernel<int32_t><<<1, 128, 0, stream>>>(groups, tokens, kExpertBM, schedule);
+  tile_list_kernel<int32_t><<<1, 128, 0, stream>>>(groups, tokens, expert_tile_rows(tokens * topk), schedule);
   return hipGetLastError();
 }
 
@@ -1649,6 +1808,9 @@ hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* as, con
                             hipStream_t stream) {
   const int64_t a_rows = input_routed ? tokens * topk : tokens;
   const int64_t a_bytes = a_rows * a_words * 4;
+  if (expert_tile_rows(tokens * topk) == kExpertSkinnyBM)
+    return launch_expert_skinny<false>(a, a_words, a_bytes, as, w, ws, w, ws, groups, schedule, tokens, topk, k, n,
+                                       input_routed, out, stream);
   if (a_bytes < ((int64_t)1 << 31) && n % 256 == 0)
     return launch_expert_dmah<ExpertHTile, false>(a, a_words, a_bytes, as, w, ws, w, ws, groups, schedule, tokens,
                                                   topk, k, n, input_routed, out, stream);

@@ -46,11 +46,14 @@ hipError_t launch_expert_tasks(const float* groups, int64_t tokens, float* tasks
                                hipStream_t stream);
 
 // Tile schedule of the grouped expert GEMM: int32 [1 + 2 * max_tiles], tiles
-// of expert_tile_rows() slots.
-int expert_tile_rows();
+// of expert_tile_rows(routes) slots for `routes` routed rows (tokens * topk):
+// 32-slot tiles for few routed rows, 128-slot tiles otherwise. The expert
+// GEMM launches pick their kernel by the same rule, so a schedule must be
+// built for the routes count the GEMMs are launched with.
+int expert_tile_rows(int64_t routes);
 int64_t expert_max_tiles(int64_t routes);
 size_t expert_schedule_bytes(int64_t routes);
-hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int32_t* schedule,
+hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int topk, int32_t* schedule,
                                   hipStream_t stream);
 hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* a_scales,
                             const uint32_t* w_tiled, const float* w_scales, const float* groups,
