@@ -409,12 +409,14 @@ def packed_experts(rng, n, k):
     return oracle.pack_weight(w)
 
 
-@pytest.mark.parametrize("tokens", [3, 64, 300])
-def test_expert_gemm_matches_oracle(tokens):
+@pytest.mark.parametrize("tokens,hidden", [(3, 512), (64, 512), (300, 512), (7, 256)])
+def test_expert_gemm_matches_oracle(tokens, hidden):
     """routed_experts_match_sparse_cpu_oracle (src/omni.rs:946-1051) and the
-    OmniExpert paired check (src/benchmarking/omni.rs:328-356), bit-exact."""
+    OmniExpert paired check (src/benchmarking/omni.rs:328-356), bit-exact.
+    Up to 2048 routed rows the 32-slot skinny kernel runs (one wave per
+    k-step: K = 256 gives a single wave), above it the 128-slot kernel."""
     rng = np.random.default_rng(tokens)
-    hidden, inter, topk = 512, 256, 8
+    inter, topk = 256, 8
     routes = random_routes(rng, tokens, skew=2.0)
     groups, _ = oracle.group_routes(routes)
     x = randn_bf16(rng, (tokens, hidden))
@@ -495,9 +497,12 @@ def test_combine_matches_oracle(ordered):
     assert_same_u16(bf16_host(got), want, "combine")
 
 
-@pytest.mark.parametrize("tokens,hidden,inter", [(5, 512, 256), (96, 2048, 768), (300, 1024, 512)])
+@pytest.mark.parametrize("tokens,hidden,inter", [(5, 512, 256), (96, 2048, 768), (300, 1024, 512),
+                                                 (256, 512, 256), (257, 512, 256)])
 def test_moe_layer_matches_oracle(tokens, hidden, inter):
-    """Whole Omni INT4 MoE block (src/omni.rs:762-857) bit-exact vs the oracle."""
+    """Whole Omni INT4 MoE block (src/omni.rs:762-857) bit-exact vs the oracle.
+    256 and 257 tokens (2048 and 2056 routed rows) sit on either side of the
+    switch from 32-slot to 128-slot expert tiles."""
     rng = np.random.default_rng(tokens + hidden)
     x = randn_bf16(rng, (tokens, hidden))
     logits = BF(rng.standard_normal((tokens, 128)).astype(np.float32))
