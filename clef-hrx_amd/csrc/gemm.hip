@@ -1397,8 +1397,10 @@ hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, c
 // the row's 128-byte k-step, the lane -> k map of the LDS cores) with the
 // next k-step's loads in flight while the current one computes. The NW
 // partial accumulators meet in LDS by integer atomic adds (exact in any
-// order), and the G1 epilogue runs on the sums.
-template <int MT, int NW, bool RESID>
+// order), and the G1 epilogue runs on the sums. I8: INT8 operands (k-steps of
+// 128 k, the same 64 bytes per lane; each 16-byte chunk is an MFMA operand as
+// it stands, and the accumulator is the dot product itself).
+template <int MT, int NW, bool RESID, bool I8>
 __global__ __launch_bounds__(NW * 64) void gemm_skinny_kernel(const uint32_t* __restrict__ a, int a_words,
                                                           const float* __restrict__ as, const uint32_t* __restrict__ w,
                                                           const float* __restrict__ ws, int64_t M, int N, int kb,
@@ -1439,6 +1441,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny_kernel(const uint32_t* __
   };
   auto compute = [&](auto buf) {
     constexpr int B = decltype(buf)::value;
+    if constexpr (I8) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int f = 0; f < MT; ++f) acc[f] = mfma32_i8(wr[B][p], ar[B][f][p], acc[f]);
+      return;
+    }
 #pragma unroll
     for (int p = 0; p < 4; ++p)
 #pragma unroll
@@ -1485,8 +1494,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny_kernel(const uint32_t* __
     const int col = n0 + 8 * rq + 4 * (ln >> 5);
     const float asv = as[m];
     const float4 wsv = *reinterpret_cast<const float4*>(ws + col);
-    uint32_t p0 = g1_value(red[f][4 * rq + 0][ln], wsv.x, asv) | (g1_value(red[f][4 * rq + 1][ln], wsv.y, asv) << 16);
-    uint32_t p1 = g1_value(red[f][4 * rq + 2][ln], wsv.z, asv) | (g1_value(red[f][4 * rq + 3][ln], wsv.w, asv) << 16);
+    constexpr int SH = I8 ? 0 : 8;
+    uint32_t p0 = g1_value<SH>(red[f][4 * rq + 0][ln], wsv.x, asv) | (g1_value<SH>(red[f][4 * rq + 1][ln], wsv.y, asv) << 16);
+    uint32_t p1 = g1_value<SH>(red[f][4 * rq + 2][ln], wsv.z, asv) | (g1_value<SH>(red[f][4 * rq + 3][ln], wsv.w, asv) << 16);
     uint16_t* dst = out + m * N + col;
     if (RESID) {
       const uint2 rv = *reinterpret_cast<const uint2*>(residual + m * N + col);
@@ -1498,29 +1508,37 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny_kernel(const uint32_t* __
 #endif
 }
 
-template <int MT, bool RESID>
+template <int MT, bool RESID, bool I8>
 hipError_t launch_skinny(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                          int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
   const int64_t groups = (m + 32 * MT - 1) / (32 * MT);
   if (groups > 65535) return hipErrorInvalidValue;
   constexpr int NW = MT == 4 ? 8 : 16;  // four row blocks need 256 VGPRs: two waves per SIMD
-  gemm_skinny_kernel<MT, NW, RESID><<<dim3((unsigned)(n / 32), (unsigned)groups), NW * 64, 0, stream>>>(
-      a, a_words, as, w, ws, m, n, k / 256, residual, out);
+  gemm_skinny_kernel<MT, NW, RESID, I8><<<dim3((unsigned)(n / 32), (unsigned)groups), NW * 64, 0, stream>>>(
+      a, a_words, as, w, ws, m, n, I8 ? k / 128 : k / 256, residual, out);
   return hipGetLastError();
 }
 
-template <bool RESID>
+template <bool RESID, bool I8>
 hipError_t launch_skinny_m(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                            int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
-  if (m <= 32) return launch_skinny<1, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-  if (m <= 64) return launch_skinny<2, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-  return launch_skinny<4, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (m <= 32) return launch_skinny<1, RESID, I8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (m <= 64) return launch_skinny<2, RESID, I8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return launch_skinny<4, RESID, I8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
 }
 
+template <bool I8 = false>
 hipError_t launch_skinny_any(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                              int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
-  if (residual) return launch_skinny_m<true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-  return launch_skinny_m<false>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (residual) return launch_skinny_m<true, I8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return launch_skinny_m<false, I8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+}
+
+// Few rows, INT4: the skinny kernel where 128x128 tiles would leave most CUs
+// idle (see launch_gemm_i4).
+bool use_skinny(int64_t m, int n) {
+  const int64_t tiles128 = (m + 127) / 128 * (n / 128);
+  return m <= 64 || (m <= 256 && tiles128 < 96);
 }
 
 // Grouped expert GEMM for few routed rows per expert (decode-sized batches),
@@ -1657,6 +1675,9 @@ int gemm_config_count() { return 23; }
 
 hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  // Few rows: the skinny kernel with one 32-row block (graph replay, M1 N12288 K4096: 16.4 us against 24.2;
+  // at M64 the two-block form loses to 128x128 tiles, 34.1 us against 24.7, on the 50 MB INT8 weight).
+  if (m <= 32) return launch_skinny_any<true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
   if (n % 256 == 0 && m >= 1024)
     return launch_dma8_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
   return launch_dma8_any<Dma128x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
@@ -1677,9 +1698,8 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
     // M1 N4096 K4096 5.1 us against 17.4; M64 N12288 K4096 13.0 against
     // 17.8; M128 N12288 K4096 29.1 against 18.3, where 96 tiles of 128x128
     // already cover most CUs).
-    const int64_t tiles128 = (m + 127) / 128 * (n / 128);
     const int64_t tiles256 = (m + 255) / 256 * (n / 256);
-    if (m <= 64 || (m <= 256 && tiles128 < 96))
+    if (use_skinny(m, n))
       config = 22;
     else
       config = (n % 256 == 0 && m >= 1024 && tiles256 >= 192) ? 20 : 6;
