@@ -266,6 +266,46 @@ def test_gemm_extreme_codes_and_saturation():
         assert_same_u16(bf16_host(got), want, f"extreme config={cfg}")
 
 
+def test_gemm_zero_and_tiny_scales():
+    """Scales that make the "+ 0" of the epilogue matter (kernels/gemm_integer.loom:411-418):
+    zero weight scales (a negative accumulator times +0 is -0, which the + 0
+    turns into +0) and scale products near and below the f32 normal range
+    (results that round to zero or to denormals). Every configuration against
+    the oracle, bit for bit; rows past a tile multiple included."""
+    m, n, k = 300, 512, 512
+    rng = np.random.default_rng(77)
+    stride = oracle.activation_stride(k)
+
+    def code_words(rows):
+        # codes in -7..7 as the quantizer makes them, 8 nibbles per word
+        nib = (rng.integers(-7, 8, size=(rows, stride)) & 15).astype(np.uint32)
+        nib[:, k:] = 0
+        return sum(nib[:, j::8] << np.uint32(4 * j) for j in range(8)).astype(np.uint32)
+
+    a_words = code_words(m)
+    a_scales = (10.0 ** rng.uniform(-12, 0, size=m)).astype(np.float32)
+    a_scales[::7] = np.float32(1e-20)
+    a_scales[3] = np.float32(1e-37)
+    w_tiled = oracle.retile(code_words(n), k)
+    w_scales = (10.0 ** rng.uniform(-6, 0, size=n)).astype(np.float32)
+    w_scales[::11] = 0.0
+    w_scales[5::13] = np.float32(1e-30)
+    want = oracle.gemm(a_words, a_scales, w_tiled, w_scales, n, k)
+    # the fixture reaches the cases it is for: negative accumulators in
+    # zero-scale columns (+0 in the reference, -0 without its + 0), and bf16
+    # denormals and underflows from tiny products
+    acc = oracle.gemm_acc(a_words, w_tiled, n, k)
+    zero_cols = w_scales == 0
+    assert (acc[:, zero_cols] < 0).any() and (want[:, zero_cols] == 0).all()
+    assert (((want & 0x7F80) == 0) & ((want & 0x7F) != 0)).any()
+    storage = np.concatenate([a_words.reshape(-1), a_scales.view(np.uint32)])
+    a = clef_i4.Prepared(to_dev_u32(storage), m, k, stride, 4)
+    qw = dev_weight(w_tiled, w_scales, n, k)
+    for cfg in range(clef_i4.gemm_configs()):
+        got = clef_i4.project_prepared(a, qw, config=cfg)
+        assert_same_u16(bf16_host(got), want, f"zero/tiny scales config={cfg}")
+
+
 def assert_same_bf16_nan_aware(got: np.ndarray, want: np.ndarray, what: str):
     """Bit-exact, except that any NaN equals any NaN: a NaN made by 0 * inf
     carries the sign bit of the machine's default NaN (0x7fc00000 on the GPU,
