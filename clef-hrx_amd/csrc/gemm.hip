@@ -9,6 +9,8 @@
 // route = groups[e][1+i], xr = input_routed ? route : route / topk,
 // out[route][c] = bf16(RN(f32(acc) * RN(as[xr] * ws[e*n + c]))), no clamp.
 
+#include <atomic>
+
 #include "gemm_core.hpp"
 #include "silu_table.hpp"
 #include "gemm_dma.hpp"
@@ -21,6 +23,42 @@ namespace clef {
 namespace {
 
 constexpr float kBf16Max = 3.3895313892515355e38f;
+
+// Per-device launch facts of one kernel: whether its dynamic LDS limit has
+// been raised (an attribute HIP keeps per device) and how many of its
+// workgroups a CU holds. Devices 0..31 are cached, safe to share between host
+// threads; any other device is queried on every launch.
+struct LaunchCache {
+  std::atomic<uint32_t> lds_set{0};
+  std::atomic<int> per_cu[32] = {};
+};
+
+hipError_t current_device(int& dev) { return hipGetDevice(&dev); }
+
+hipError_t ensure_dynamic_lds(LaunchCache& c, const void* kern, int bytes) {
+  int dev = 0;
+  if (hipError_t e = current_device(dev)) return e;
+  const uint32_t bit = dev >= 0 && dev < 32 ? 1u << dev : 0u;
+  if (bit && (c.lds_set.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  if (hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes)) return e;
+  c.lds_set.fetch_or(bit, std::memory_order_release);
+  return hipSuccess;
+}
+
+// Workgroups per CU (at least 1) and the CU count of the current device.
+hipError_t resident_per_cu(LaunchCache& c, const void* kern, int threads, int lds_bytes, int& per_cu, int& cus) {
+  int dev = 0;
+  if (hipError_t e = current_device(dev)) return e;
+  if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) return e;
+  const bool cached = dev >= 0 && dev < 32;
+  per_cu = cached ? c.per_cu[dev].load(std::memory_order_relaxed) : 0;
+  if (per_cu > 0) return hipSuccess;
+  int nb = 0;
+  if (hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, threads, lds_bytes)) return e;
+  per_cu = nb > 0 ? nb : 1;
+  if (cached) c.per_cu[dev].store(per_cu, std::memory_order_relaxed);
+  return hipSuccess;
+}
 
 template <int SHIFT = 8>
 __device__ __forceinline__ uint32_t g1_value(int32_t acc, float ws, float as) {
@@ -796,24 +834,11 @@ hipError_t launch_dma_persist(const uint32_t* a, int a_words, const float* as, c
                               int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
   constexpr int kPersistLds = T::LDS_BYTES + T::NW * kEpiWaveLds<T>;
   static_assert(kPersistLds <= 160 * 1024, "LDS per workgroup");
-  static bool configured = false;
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma_persist_kernel<T, RESID>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kPersistLds);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
-  static int per_cu = 0;
-  if (per_cu == 0) {
-    int nb = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &nb, reinterpret_cast<const void*>(&gemm_dma_persist_kernel<T, RESID>), T::THREADS, kPersistLds);
-    if (e != hipSuccess) return e;
-    per_cu = nb > 0 ? nb : 1;
-  }
-  int dev = 0, cus = 0;
-  if (hipError_t e = hipGetDevice(&dev)) return e;
-  if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) return e;
+  static LaunchCache cache;
+  const void* kern = reinterpret_cast<const void*>(&gemm_dma_persist_kernel<T, RESID>);
+  if (hipError_t e = ensure_dynamic_lds(cache, kern, kPersistLds)) return e;
+  int per_cu = 0, cus = 0;
+  if (hipError_t e = resident_per_cu(cache, kern, T::THREADS, kPersistLds, per_cu, cus)) return e;
   const int tiles_n = n / T::BN;
   const int64_t tiles_m = (m + T::BM - 1) / T::BM;
   const int64_t total = tiles_m * tiles_n;
@@ -837,20 +862,12 @@ template <class T, bool RESID>
 hipError_t launch_persistent(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
                              const float* ws, int64_t m, int n, int k, const uint16_t* residual,
                              uint16_t* out, int per_cu, hipStream_t stream) {
-  static bool configured = false;
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_persistent_kernel<T, RESID>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess) return e;
-  }
+  static LaunchCache cache;
+  const void* kern = reinterpret_cast<const void*>(&gemm_persistent_kernel<T, RESID>);
+  if (hipError_t e = ensure_dynamic_lds(cache, kern, T::LDS_BYTES)) return e;
+  int dev = 0, cus = 0;
+  if (hipError_t e = current_device(dev)) return e;
+  if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) return e;
   const int tiles_n = n / T::BN;
   const int64_t tiles_m = (m + T::BM - 1) / T::BM;
   const int64_t total = tiles_m * tiles_n;
@@ -886,12 +903,8 @@ hipError_t launch_dma(const uint32_t* a, int a_words, const float* as, const uin
     kern = reinterpret_cast<const void*>(&gemm_dmah_kernel<T, RESID>);
   else
     kern = reinterpret_cast<const void*>(&gemm_dma_kernel<T, RESID>);
-  static bool configured = false;
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  static LaunchCache cache;
+  if (hipError_t e = ensure_dynamic_lds(cache, kern, T::LDS_BYTES)) return e;
   const int tiles_n = n / T::BN;
   const int64_t tiles_m = (m + T::BM - 1) / T::BM;
   const int64_t blocks = tiles_m * tiles_n;
@@ -915,13 +928,9 @@ hipError_t launch_dma_any(const uint32_t* a, int a_words, const float* as, const
 template <class T, bool RESID>
 hipError_t launch_dma8(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                        int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
-  static bool configured = false;
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_dma8_kernel<T, RESID>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  static LaunchCache cache;
+  const void* kern = reinterpret_cast<const void*>(&gemm_dma8_kernel<T, RESID>);
+  if (hipError_t e = ensure_dynamic_lds(cache, kern, T::LDS_BYTES)) return e;
   const int tiles_n = n / T::BN;
   const int64_t tiles_m = (m + T::BM - 1) / T::BM;
   gemm_dma8_kernel<T, RESID><<<(unsigned)(tiles_m * tiles_n), T::THREADS, T::LDS_BYTES, stream>>>(
@@ -954,13 +963,9 @@ template <class T, bool RESID>
 hipError_t launch_dense(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
                         const float* ws, int64_t m, int n, int k, const uint16_t* residual,
                         uint16_t* out, hipStream_t stream) {
-  static bool configured = false;
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i4_kernel<T, RESID>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  static LaunchCache cache;
+  const void* kern = reinterpret_cast<const void*>(&gemm_i4_kernel<T, RESID>);
+  if (hipError_t e = ensure_dynamic_lds(cache, kern, T::LDS_BYTES)) return e;
   const int tiles_n = n / T::BN;
   const int64_t tiles_m = (m + T::BM - 1) / T::BM;
   const int64_t blocks = tiles_m * tiles_n;
@@ -1777,13 +1782,9 @@ hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, c
                               const float* ws, const uint32_t* w2, const float* ws2, const float* groups,
                               const int32_t* schedule, int64_t tokens, int topk, int k, int n, int input_routed,
                               uint16_t* out, hipStream_t stream) {
-  static bool configured = false;
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&expert_dmah_kernel<T, GU>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, expert_lds_bytes<T, GU>());
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  static LaunchCache cache;
+  const void* kern = reinterpret_cast<const void*>(&expert_dmah_kernel<T, GU>);
+  if (hipError_t e = ensure_dynamic_lds(cache, kern, expert_lds_bytes<T, GU>())) return e;
   const int tiles_n = n / (GU ? T::BN / 2 : T::BN);
   const int64_t blocks = 8 * ((expert_max_tiles(tokens * topk) * tiles_n + 7) / 8);
   expert_dmah_kernel<T, GU><<<(unsigned)blocks, T::THREADS, expert_lds_bytes<T, GU>(), stream>>>(
@@ -1836,13 +1837,9 @@ hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* as, con
                                                   topk, k, n, input_routed, out, stream);
   if (a_bytes < ((int64_t)1 << 31)) {
     using T = ExpertDmaTile;
-    static bool configured = false;
-    if (!configured) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&expert_dma_kernel<T>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
-      if (e != hipSuccess) return e;
-      configured = true;
-    }
+    static LaunchCache cache;
+    const void* kern = reinterpret_cast<const void*>(&expert_dma_kernel<T>);
+    if (hipError_t e = ensure_dynamic_lds(cache, kern, T::LDS_BYTES)) return e;
     const int tiles_n = n / T::BN;
     const int64_t blocks = 8 * ((expert_max_tiles(tokens * topk) * tiles_n + 7) / 8);
     expert_dma_kernel<T><<<(unsigned)blocks, T::THREADS, T::LDS_BYTES, stream>>>(
@@ -1852,13 +1849,9 @@ hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* as, con
   }
   // Activation buffers of 2 GiB or more: 64-bit row addressing.
   using T = ExpertTile;
-  static bool configured = false;
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&expert_i4_kernel<T>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  static LaunchCache cache;
+  const void* kern = reinterpret_cast<const void*>(&expert_i4_kernel<T>);
+  if (hipError_t e = ensure_dynamic_lds(cache, kern, T::LDS_BYTES)) return e;
   const int tiles_n = n / T::BN;
   const int64_t blocks = expert_max_tiles(tokens * topk) * tiles_n;
   expert_i4_kernel<T><<<(unsigned)blocks, 256, T::LDS_BYTES, stream>>>(
