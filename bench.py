@@ -14,6 +14,9 @@ M=4096 on one MI355X.
   int8_gemm_*  the INT8 x INT8 projection at the GEMM's shape.
   small_m_*    M = 1, 16, 64 on the GEMM's weight (K4096 N12288): GPU time per
                call (HIP graph replay) and HBM GB/s of the bytes the call moves.
+  linear_m512_k2048_n2048  the single INT4 linear M512 K2048 N2048: GPU time
+               per call (graph replay), TOPS and HBM GB/s.
+  attn_proj_*  INT4 attention projections at M=16384 (Q, K, V, O + residual).
   roofline     the GEMM kernel against the int8 MFMA peak (5.0 POP/s).
   cpu_baseline the CPU oracle (quantize + i32 matmul + epilogue; MoE layer) on
                a bounded sample, timed on this host's cores.
@@ -52,7 +55,7 @@ def parse():
     p.add_argument("--moe-tokens", type=int, default=4096,
                    help="tokens of the MoE leg (4096 is the benchmark workload; small counts show the "
                         "decode-sized path)")
-    p.add_argument("--only", choices=["gemm", "moe", "mlp", "i8", "smallm", "copy", "peaks"], default=None,
+    p.add_argument("--only", choices=["gemm", "moe", "mlp", "attn", "i8", "smallm", "copy", "peaks"], default=None,
                    help="run one leg; 'copy' is a plain 512 MiB device copy, the known-size "
                         "kernel that scales HBM byte counters")
     return p.parse_args()
@@ -145,6 +148,56 @@ def small_m_leg(args):
         nbytes = n * k // 2 + 4 * n + m * (k // 2 + 4) + 2 * m * n
         res[m] = {"us": ms * 1e3, "gbs": nbytes / ms / 1e6}
     return res
+
+
+def linear_c1_leg(args):
+    """Single INT4 linear M512 K2048 N2048 (the reference's CPU-path shape):
+    latency-bound, so GPU time per call by graph replay, with TOPS and the HBM
+    rate of the bytes the call moves."""
+    import torch
+
+    import clef_i4
+
+    m, k, n = 512, 2048, 2048
+    qw = clef_i4.load_quantized_weight(bf16_randn((n, k), 0.02, 1001 * 16 + 1))
+    a = clef_i4.prepare(bf16_randn((m, k), 1.0, 1001 * 16 + 0))
+    out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    ms = graph_timed(lambda: clef_i4.project_prepared(a, qw, out=out))
+    nbytes = n * k // 2 + 4 * n + m * (k // 2 + 4) + 2 * m * n
+    return {"us": ms * 1e3, "tops": 2.0 * m * n * k / ms / 1e9, "gbs": nbytes / ms / 1e6}
+
+
+def attention_leg(args):
+    """INT4 attention projections at M=16384: Q 4096->4096, K and V 4096->1024
+    on one shared quantized activation, and O 4096->4096 with the residual
+    (fed the same activation here: its real input, the attention output, has
+    the same shape)."""
+    import torch
+
+    import clef_i4
+
+    m, d, kv = 16384, 4096, 1024
+    x = bf16_randn((m, d), 1.0, 1003 * 16 + 0)
+    wq = clef_i4.load_quantized_weight(bf16_randn((d, d), 0.02, 1003 * 16 + 1))
+    wk = clef_i4.load_quantized_weight(bf16_randn((kv, d), 0.02, 1003 * 16 + 2))
+    wv = clef_i4.load_quantized_weight(bf16_randn((kv, d), 0.02, 1003 * 16 + 3))
+    wo = clef_i4.load_quantized_weight(bf16_randn((d, d), 0.02, 1003 * 16 + 4))
+    res = bf16_randn((m, d), 1.0, 1003 * 16 + 5)
+    ax = clef_i4.prepare(x)
+    q = torch.empty((m, d), dtype=torch.bfloat16, device="cuda")
+    kk = torch.empty((m, kv), dtype=torch.bfloat16, device="cuda")
+    v = torch.empty((m, kv), dtype=torch.bfloat16, device="cuda")
+    o = torch.empty((m, d), dtype=torch.bfloat16, device="cuda")
+
+    def step():
+        clef_i4.project_prepared(ax, wq, out=q)
+        clef_i4.project_prepared(ax, wk, out=kk)
+        clef_i4.project_prepared(ax, wv, out=v)
+        clef_i4.project_prepared(ax, wo, residual=res, out=o)
+
+    ms = timed(step, max(1, args.steps // 4), max(1, args.warmup // 4))
+    ops = 2.0 * m * d * (d + kv + kv + d)
+    return {"ms": ms, "tops": ops / ms / 1e9}
 
 
 def i8_leg(args):
@@ -293,6 +346,9 @@ def main():
         res["i8"] = i8_leg(args)
     if args.only in (None, "smallm"):
         res["smallm"] = small_m_leg(args)
+        res["c1"] = linear_c1_leg(args)
+    if args.only in (None, "attn"):
+        res["attn"] = attention_leg(args)
     if args.only == "peaks":
         import subprocess
         probe = os.path.join(ROOT, "clef-hrx_amd", "lib", "peaks")
@@ -343,6 +399,12 @@ def main():
     if "i8" in res:
         line["int8_gemm_ms"] = round(res["i8"]["ms"], 4)
         line["int8_gemm_tops"] = round(res["i8"]["tops"], 1)
+    if "c1" in res:
+        line["linear_m512_k2048_n2048"] = {"us": round(res["c1"]["us"], 2), "tops": round(res["c1"]["tops"], 1),
+                                           "hbm_gbs": round(res["c1"]["gbs"], 1)}
+    if "attn" in res:
+        line["attn_proj_m16384_ms"] = round(res["attn"]["ms"], 4)
+        line["attn_proj_tops"] = round(res["attn"]["tops"], 1)
     if "smallm" in res:
         line["small_m_k4096_n12288"] = {f"m{m}": {"us": round(v["us"], 2), "hbm_gbs": round(v["gbs"], 1)}
                                         for m, v in res["smallm"].items()}

@@ -1543,7 +1543,7 @@ hipError_t launch_skinny_any(const uint32_t* a, int a_words, const float* as, co
 // idle (see launch_gemm_i4).
 bool use_skinny(int64_t m, int n) {
   const int64_t tiles128 = (m + 127) / 128 * (n / 128);
-  return m <= 64 || (m <= 256 && tiles128 < 96);
+  return m <= 64 || (m <= 512 && tiles128 < 96);
 }
 
 // Grouped expert GEMM for few routed rows per expert (decode-sized batches),
@@ -1701,8 +1701,8 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
     // Few rows: the weight stream dominates and 128x128 tiles give too few
     // workgroups, so the K-split skinny kernel (GPU time, graph replay:
     // M1 N4096 K4096 5.1 us against 17.4; M64 N12288 K4096 13.0 against
-    // 17.8; M128 N12288 K4096 29.1 against 18.3, where 96 tiles of 128x128
-    // already cover most CUs).
+    // 17.8; M512 N2048 K2048 7.5 against 11.3; M128 N12288 K4096 29.1
+    // against 18.3, where 96 tiles of 128x128 already cover most CUs).
     const int64_t tiles256 = (m + 255) / 256 * (n / 256);
     if (use_skinny(m, n))
       config = 22;
