@@ -17,6 +17,8 @@ M=4096 on one MI355X.
   linear_m512_k2048_n2048  the single INT4 linear M512 K2048 N2048: GPU time
                per call (graph replay), TOPS and HBM GB/s.
   attn_proj_*  INT4 attention projections at M=16384 (Q, K, V, O + residual).
+  moe_skewed_t65536  the MoE layer at 65536 tokens with skewed routing (a few
+               experts take most rows, eight none).
   roofline     the GEMM kernel against the int8 MFMA peak (5.0 POP/s).
   cpu_baseline the CPU oracle (quantize + i32 matmul + epilogue; MoE layer) on
                a bounded sample, timed on this host's cores.
@@ -55,7 +57,8 @@ def parse():
     p.add_argument("--moe-tokens", type=int, default=4096,
                    help="tokens of the MoE leg (4096 is the benchmark workload; small counts show the "
                         "decode-sized path)")
-    p.add_argument("--only", choices=["gemm", "moe", "mlp", "attn", "i8", "smallm", "copy", "peaks"], default=None,
+    p.add_argument("--only", choices=["gemm", "moe", "moe65536", "mlp", "attn", "i8", "smallm", "copy", "peaks"],
+                   default=None,
                    help="run one leg; 'copy' is a plain 512 MiB device copy, the known-size "
                         "kernel that scales HBM byte counters")
     return p.parse_args()
@@ -148,6 +151,34 @@ def small_m_leg(args):
         nbytes = n * k // 2 + 4 * n + m * (k // 2 + 4) + 2 * m * n
         res[m] = {"us": ms * 1e3, "gbs": nbytes / ms / 1e6}
     return res
+
+
+def moe_skewed_leg(args):
+    """Omni INT4 MoE layer at 65536 tokens with skewed routing: router logits
+    N(0,1) + bias_e, bias_e = -1.1 * 0.57 * ln(1 + rank(e)) for a seeded rank
+    permutation (seed 55), the eight lowest-ranked experts at -30 (never
+    chosen)."""
+    import numpy as np
+    import torch
+
+    import clef_i4
+
+    t, d, inter = 65536, 2048, 768
+    rank = np.random.default_rng(55).permutation(128)
+    bias = -1.1 * 0.57 * np.log1p(rank)
+    bias[rank >= 120] = -30.0
+    g = torch.Generator(device="cuda").manual_seed(1005 * 16 + 1)
+    z = torch.randn((t, 128), generator=g, device="cuda", dtype=torch.float32)
+    logits = (z + torch.from_numpy(bias.astype(np.float32)).cuda()).to(torch.bfloat16)
+    x = bf16_randn((t, d), 1.0, 1005 * 16 + 0)
+    gate = clef_i4.load_quantized_weight(bf16_randn((128 * inter, d), 0.02, 1005 * 16 + 2))
+    up = clef_i4.load_quantized_weight(bf16_randn((128 * inter, d), 0.02, 1005 * 16 + 3))
+    down = clef_i4.load_quantized_weight(bf16_randn((128 * d, inter), 0.02, 1005 * 16 + 4))
+    layer = clef_i4.MoeLayer(gate, up, down)
+    out = torch.empty((t, d), dtype=torch.bfloat16, device="cuda")
+    ms = timed(lambda: layer(x, logits, out=out), max(1, args.steps // 20), max(1, args.warmup // 60))
+    ops = 8.0 * t * 2 * (2 * inter * d + d * inter)
+    return {"tokens": t, "ms": ms, "tokens_per_s": t / ms * 1e3, "tops": ops / ms / 1e9}
 
 
 def linear_c1_leg(args):
@@ -349,6 +380,8 @@ def main():
         res["c1"] = linear_c1_leg(args)
     if args.only in (None, "attn"):
         res["attn"] = attention_leg(args)
+    if args.only in (None, "moe65536"):
+        res["moe65536"] = moe_skewed_leg(args)
     if args.only == "peaks":
         import subprocess
         probe = os.path.join(ROOT, "clef-hrx_amd", "lib", "peaks")
@@ -402,6 +435,10 @@ def main():
     if "c1" in res:
         line["linear_m512_k2048_n2048"] = {"us": round(res["c1"]["us"], 2), "tops": round(res["c1"]["tops"], 1),
                                            "hbm_gbs": round(res["c1"]["gbs"], 1)}
+    if "moe65536" in res:
+        line["moe_skewed_t65536"] = {"ms": round(res["moe65536"]["ms"], 3),
+                                     "tokens_per_s": round(res["moe65536"]["tokens_per_s"], 1),
+                                     "tops": round(res["moe65536"]["tops"], 1)}
     if "attn" in res:
         line["attn_proj_m16384_ms"] = round(res["attn"]["ms"], 4)
         line["attn_proj_tops"] = round(res["attn"]["tops"], 1)
