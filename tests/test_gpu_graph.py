@@ -17,24 +17,30 @@ def randn(shape, std, seed):
     return (torch.randn(shape, generator=g, device="cuda") * std).to(torch.bfloat16)
 
 
-def test_graph_replays_match_eager():
-    t, d, inter = 256, 512, 256
+@pytest.mark.parametrize("t,pm,pn", [(256, 256, 1024), (512, 2048, 6144)])
+def test_graph_replays_match_eager(t, pm, pn):
+    """256 tokens and a 256 x 1024 projection take the few-rows kernels (32-slot
+    expert tiles, the K-split GEMM); 512 tokens and a 2048 x 6144 projection
+    take the 128-slot expert kernels and the persistent GEMM."""
+    d, inter = 512, 256
     gate = clef_i4.load_quantized_weight(randn((128 * inter, d), 0.02, 1))
     up = clef_i4.load_quantized_weight(randn((128 * inter, d), 0.02, 2))
     down = clef_i4.load_quantized_weight(randn((128 * d, inter), 0.02, 3))
-    qw = clef_i4.load_quantized_weight(randn((1024, d), 0.02, 4))
+    qw = clef_i4.load_quantized_weight(randn((pn, d), 0.02, 4))
     layer = clef_i4.MoeLayer(gate, up, down)
-    inputs = [(randn((t, d), 1.0, 10 + i), randn((t, 128), 1.0, 20 + i)) for i in range(4)]
+    inputs = [(randn((t, d), 1.0, 10 + i), randn((t, 128), 1.0, 20 + i), randn((pm, d), 1.0, 30 + i))
+              for i in range(4)]
 
     # static buffers the graph reads and writes
     x = inputs[0][0].clone()
     logits = inputs[0][1].clone()
+    px = inputs[0][2].clone()
     moe_out = torch.empty((t, d), dtype=torch.bfloat16, device="cuda")
-    a = clef_i4.prepare(x)
-    proj_out = torch.empty((t, 1024), dtype=torch.bfloat16, device="cuda")
+    a = clef_i4.prepare(px)
+    proj_out = torch.empty((pm, pn), dtype=torch.bfloat16, device="cuda")
 
     def step():
-        clef_i4.prepare(x, out=a.storage)
+        clef_i4.prepare(px, out=a.storage)
         clef_i4.project_prepared(a, qw, out=proj_out)
         layer(x, logits, out=moe_out)
 
@@ -49,12 +55,13 @@ def test_graph_replays_match_eager():
     with torch.cuda.graph(graph):
         step()
 
-    for i, (xi, li) in enumerate(inputs * 2):
+    for i, (xi, li, pi) in enumerate(inputs * 2):
         want_moe = layer(xi, li)
-        want_proj = clef_i4.project_prepared(clef_i4.prepare(xi), qw)
+        want_proj = clef_i4.project_prepared(clef_i4.prepare(pi), qw)
         torch.cuda.synchronize()
         x.copy_(xi)
         logits.copy_(li)
+        px.copy_(pi)
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(moe_out.view(torch.int16), want_moe.view(torch.int16)), f"replay {i}: MoE layer"
