@@ -93,6 +93,25 @@ __device__ __forceinline__ uint32_t silu_lut_offset(uint32_t w, bool& inside) {
   return ((t >> 15) & 0x1FFFu) | ((w >> 18) & ~0x1FFFu);  // w >> 18 < 2^14: bit 13 is the sign
 }
 
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+// silu_lut_offset of two bf16 values at once, with packed 16-bit operations:
+// `pair` holds the bf16 bits of two values (low and high half); the result
+// holds their two byte offsets in the same halves. In 16 bits,
+// t = h - (kSiluLutExp0 << 7) has bits 12..14 zero exactly when h's exponent
+// field is in the table's range, (t << 1) & 0x1FFF = (exponent - kSiluLutExp0)
+// << 8 | mantissa << 1 and h >> 2 puts the sign at bit 13, as in
+// silu_lut_offset. Bits 12..14 of either half of t are ORed into `outside`.
+__device__ __forceinline__ uint32_t silu_lut_offset2(uint32_t pair, uint32_t& outside) {
+  const u16x2 h = __builtin_bit_cast(u16x2, pair);
+  const u16x2 t = h - (u16x2)(uint16_t)(kSiluLutExp0 << 7);
+  const uint32_t tb = __builtin_bit_cast(uint32_t, t);
+  outside |= tb & 0x70007000u;
+  const uint32_t lo = __builtin_bit_cast(uint32_t, (u16x2)(t << (uint16_t)1));
+  const uint32_t sg = __builtin_bit_cast(uint32_t, (u16x2)(h >> (uint16_t)2));
+  return (lo & 0x1FFF1FFFu) | (sg & 0xE000E000u);
+}
+
 // One radix-4 stage of the reference rotation on a quad (a, b, c, d) taken at
 // stride s: s01=a+b, s23=c+d, d01=a-b, d23=c-d; a'=s01+d23, b'=s01-d23,
 // c'=d01+s23, d'=s23-d01. Separate f32 adds, no contraction.

@@ -358,10 +358,6 @@ __global__ __launch_bounds__(T::THREADS, 2) void gemm_dmah_kernel(
 #endif
 }
 
-// G1 epilogue of the persistent kernel: same values as dense_epilogue, stored
-// straight from the accumulators with exactly TM * TN * 4 buffer stores per
-// wave (rows past M fall outside the output range and are dropped), so the
-// next tile's k-step 0 can wait on its own DMA only.
 // Scales and fast-path flag of a G1 tile epilogue, loaded ahead of the
 // epilogue (so no global load waits there).
 template <class T>
@@ -1317,58 +1313,74 @@ __global__ __launch_bounds__(T::THREADS, 2) void expert_dmah_kernel(
   float asr8[T::TM];
 #pragma unroll
   for (int i = 0; i < T::TM; ++i) asr8[i] = asr[i] * 0x1p-8f;
-  auto scaled = [&](int i, int jj, int r, float w) -> float {
-    const int a = acc[i][jj][r];
-    return fast ? (float)a * (asr8[i] * w) : (float)(a >> 8) * (asr[i] * w);
-  };
+  // The epilogue body for one value of `fast` (wave-uniform, so one branch
+  // instead of a select per value).
+  auto values = [&](auto fast_tag) {
+    constexpr bool FAST = decltype(fast_tag)::value;
+    auto scaled = [&](int i, int jj, int r, float w) -> float {
+      const int a = acc[i][jj][r];
+      return FAST ? (float)a * (asr8[i] * w) : (float)(a >> 8) * (asr[i] * w);
+    };
 #pragma unroll
-  for (int j = 0; j < JN; ++j)
+    for (int j = 0; j < JN; ++j)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int col = wn * (GU ? T::WN / 2 : T::WN) + 32 * j + 8 * q + 4 * h;  // within the tile
-      const float4 wsv = *reinterpret_cast<const float4*>(ws_lds + col * 4);
-      float4 wsu = wsv;
-      if constexpr (GU) wsu = *reinterpret_cast<const float4*>(ws_lds + WS_SLOT + col * 4);
-      const float wg[4] = {wsv.x, wsv.y, wsv.z, wsv.w}, wu[4] = {wsu.x, wsu.y, wsu.z, wsu.w};
-      float y[T::TM][4];
-#pragma unroll
-      for (int i = 0; i < T::TM; ++i)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) y[i][t] = scaled(i, j, 4 * q + t, wg[t]);
-      if constexpr (GU) {
-        // SiLU from the LDS table for all 4 * TM values at once (their reads
-        // overlap), then one wave-uniform branch for the rare values outside
-        // the table, computed directly.
-        float act[T::TM][4];
-        bool inside[T::TM][4];
-        bool slow = false;
+      for (int q = 0; q < 4; ++q) {
+        const int col = wn * (GU ? T::WN / 2 : T::WN) + 32 * j + 8 * q + 4 * h;  // within the tile
+        const float4 wsv = *reinterpret_cast<const float4*>(ws_lds + col * 4);
+        float4 wsu = wsv;
+        if constexpr (GU) wsu = *reinterpret_cast<const float4*>(ws_lds + WS_SLOT + col * 4);
+        const float wg[4] = {wsv.x, wsv.y, wsv.z, wsv.w}, wu[4] = {wsu.x, wsu.y, wsu.z, wsu.w};
+        float y[T::TM][4];
 #pragma unroll
         for (int i = 0; i < T::TM; ++i)
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const uint32_t wb = pack_bf16x2(0.0f, y[i][t]);  // bf16(y) in the high half, low half zero
-            y[i][t] = as_float(wb);
-            const uint32_t off = silu_lut_offset(wb, inside[i][t]);
-            slow |= !inside[i][t];
-            act[i][t] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(lds + LUT_OFF + off));
-          }
-        if (__any(slow)) {
+          for (int t = 0; t < 4; ++t) y[i][t] = scaled(i, j, 4 * q + t, wg[t]);
+        if constexpr (GU) {
+          // bf16(g) two per register, SiLU from the LDS table for all 4 * TM
+          // values at once (their reads overlap), then one wave-uniform branch
+          // for the rare values outside the table, computed directly.
+          uint32_t gp[T::TM][2];
+          float act[T::TM][4];
+          uint32_t outside = 0;
 #pragma unroll
           for (int i = 0; i < T::TM; ++i)
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
-              if (!inside[i][t]) act[i][t] = silu_bf16(y[i][t]);
+            for (int p = 0; p < 2; ++p) {
+              gp[i][p] = pack_bf16x2(y[i][2 * p], y[i][2 * p + 1]);
+              const uint32_t off = silu_lut_offset2(gp[i][p], outside);
+              act[i][2 * p] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(lds + LUT_OFF + (off & 0xFFFFu)));
+              act[i][2 * p + 1] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(lds + LUT_OFF + (off >> 16)));
+            }
+          if (__any(outside != 0)) {
+#pragma unroll
+            for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                const uint32_t gb = (t & 1) ? gp[i][t >> 1] >> 16 : gp[i][t >> 1] & 0xFFFFu;
+                if (((gb - ((uint32_t)kSiluLutExp0 << 7)) & 0x7000u) != 0) act[i][t] = silu_bf16(bf16_to_f32(gb));
+              }
+          }
+          // h = bf16(act * bf16(u)), u rounded two per register; the packing
+          // below rounds h to bf16
+#pragma unroll
+          for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+              const uint32_t up = pack_bf16x2(scaled(i, j + JN, 4 * q + 2 * p, wu[2 * p]),
+                                              scaled(i, j + JN, 4 * q + 2 * p + 1, wu[2 * p + 1]));
+              y[i][2 * p] = act[i][2 * p] * bf16_lo(up);
+              y[i][2 * p + 1] = act[i][2 * p + 1] * bf16_hi(up);
+            }
         }
-        // h = bf16(act * bf16(u)); the packing below rounds to bf16
 #pragma unroll
         for (int i = 0; i < T::TM; ++i)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) y[i][t] = act[i][t] * bf16_round(scaled(i, j + JN, 4 * q + t, wu[t]));
+          stage(wm * T::WM + 32 * i + lr, col, pack_bf16x2(y[i][0], y[i][1]), pack_bf16x2(y[i][2], y[i][3]));
       }
-#pragma unroll
-      for (int i = 0; i < T::TM; ++i)
-        stage(wm * T::WM + 32 * i + lr, col, pack_bf16x2(y[i][0], y[i][1]), pack_bf16x2(y[i][2], y[i][3]));
-    }
+  };
+  if (GU && fast)
+    values(std::true_type{});
+  else
+    values(std::false_type{});
   __syncthreads();
   constexpr int LPR = COLS / 8;              // lanes per row (16 bytes each)
   constexpr int RPP = T::THREADS / LPR;      // rows per pass

@@ -404,9 +404,11 @@ def random_routes(rng, tokens, topk=8, skew=0.0):
     return oracle.route(logits, topk)
 
 
-@pytest.mark.parametrize("tokens", [1, 2, 17, 255, 256, 257, 1000, 4096])
+@pytest.mark.parametrize("tokens", [1, 2, 17, 255, 256, 257, 511, 512, 513, 1000, 4096, 6000])
 def test_group_routes_matches_oracle(tokens):
-    """grouped_routes_match_cpu (src/omni.rs:908-942): stable lists, counts, order."""
+    """grouped_routes_match_cpu (src/omni.rs:908-942): stable lists, counts, order.
+    Up to 512 tokens at top-8 one workgroup groups them, above that three
+    kernels do; both sides of the switch are covered."""
     rng = np.random.default_rng(tokens)
     routes = random_routes(rng, tokens, skew=1.0 if tokens > 100 else 0.0)
     want_g, want_o = oracle.group_routes(routes)
@@ -440,6 +442,32 @@ def test_group_routes_empty_and_full_experts():
         c = int(want_g[e, 0])
         assert np.array_equal(g[e, :1 + c], want_g[e, :1 + c]), f"e={e}"
     assert np.array_equal(o.cpu().numpy(), want_o)
+
+
+@pytest.mark.parametrize("tokens", [300, 512, 513, 5000])
+def test_group_routes_duplicate_and_invalid_ids(tokens):
+    """Route rows that name an expert twice (the last rank is listed), ids
+    outside 0..127 (-1, 128, 130: no expert) and fractional ids (7.5 names
+    expert 7, 0.25 expert 0), as the oracle truncates them; on both sides of
+    the one-workgroup switch at 512 tokens. (An id in (-1, 0) would name
+    expert 0 yet sort below it, so two experts of the row would claim the
+    same order slot, and which write lands is not specified.)"""
+    rng = np.random.default_rng(tokens + 77)
+    routes = random_routes(rng, tokens)
+    special = [-1.0, 128.0, 130.0, 7.5, 0.25]
+    for t in range(0, tokens, 3):
+        r1, r2 = rng.choice(8, 2, replace=False)
+        routes[t, r2] = routes[t, r1]  # duplicate
+        if t % 2 == 0:
+            routes[t, rng.integers(8)] = special[(t // 6) % len(special)]
+    want_g, want_o = oracle.group_routes(routes)
+    g, o = clef_i4.omni_group_routes(to_dev_f32(routes))
+    g = g.cpu().numpy()
+    for e in range(128):
+        c = int(want_g[e, 0])
+        assert g[e, 0] == want_g[e, 0], f"count e={e}"
+        assert np.array_equal(g[e, 1:1 + c], want_g[e, 1:1 + c]), f"list e={e}"
+    assert np.array_equal(o.cpu().numpy(), want_o), "order"
 
 
 # ---------------------------------------------------------------- E1, S1, C1
