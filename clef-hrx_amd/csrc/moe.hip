@@ -405,6 +405,10 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict_
 }
 
 // One thread per (token, 8 columns).
+// KT > 0: topk == KT; the ranks, their probabilities and all KT value chunks
+// are loaded before the ordered accumulation, so a thread waits for memory
+// twice instead of once per rank. KT == 0: any topk, rank by rank.
+template <int KT>
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ values,
                                                       const float* __restrict__ routes,
                                                       const float* __restrict__ order, int64_t tokens,
@@ -418,6 +422,52 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   float acc[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+  if constexpr (KT > 0) {
+    int rank[KT];
+    if (order) {
+#pragma unroll
+      for (int j = 0; j < KT; ++j) rank[j] = (int)order[t * KT + j];
+    } else {
+      float ids[KT];
+#pragma unroll
+      for (int r = 0; r < KT; ++r) ids[r] = rt[r];
+      float prev = -1.0f;
+#pragma unroll
+      for (int j = 0; j < KT; ++j) {
+        float best = 1000000.0f;
+        int rk = 0;
+#pragma unroll
+        for (int r = 0; r < KT; ++r)
+          if (ids[r] > prev && ids[r] < best) {
+            best = ids[r];
+            rk = r;
+          }
+        prev = best;
+        rank[j] = rk;
+      }
+    }
+    float p[KT];
+    uint4 v[KT];
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+      p[j] = rt[KT + rank[j]];
+      v[j] = *reinterpret_cast<const uint4*>(values + ((t * KT + rank[j]) * width + c));
+    }
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+      const uint32_t vw[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[2 * q] = bf16_round(acc[2 * q] + bf16_round(bf16_lo(vw[q]) * p[j]));
+        acc[2 * q + 1] = bf16_round(acc[2 * q + 1] + bf16_round(bf16_hi(vw[q]) * p[j]));
+      }
+    }
+    uint32_t ow[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ow[q] = f32_to_bf16(acc[2 * q]) | (f32_to_bf16(acc[2 * q + 1]) << 16);
+    *reinterpret_cast<uint4*>(out + t * width + c) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    return;
+  }
   float prev = -1.0f;
   for (int j = 0; j < topk; ++j) {
     int rank;
@@ -545,7 +595,10 @@ hipError_t launch_combine(const uint16_t* values, const float* routes, const flo
   const int64_t threads = tokens * (width / 8);
   const int64_t blocks = (threads + 255) / 256;
   if (blocks == 0) return hipSuccess;
-  combine_kernel<<<(unsigned)blocks, 256, 0, stream>>>(values, routes, order, tokens, width, topk, out);
+  if (topk == 8)
+    combine_kernel<8><<<(unsigned)blocks, 256, 0, stream>>>(values, routes, order, tokens, width, topk, out);
+  else
+    combine_kernel<0><<<(unsigned)blocks, 256, 0, stream>>>(values, routes, order, tokens, width, topk, out);
   return hipGetLastError();
 }
 

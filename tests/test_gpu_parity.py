@@ -552,14 +552,16 @@ def test_swiglu_every_bf16_gate():
 
 
 @pytest.mark.parametrize("ordered", [True, False])
-def test_combine_matches_oracle(ordered):
-    """OmniCombine paired check (src/benchmarking/omni.rs:387-431)."""
-    rng = np.random.default_rng(int(ordered))
-    tokens, width, topk = 77, 2048, 8
-    routes = random_routes(rng, tokens)
-    _, order = oracle.group_routes(routes)
+@pytest.mark.parametrize("topk", [8, 4])
+def test_combine_matches_oracle(ordered, topk):
+    """OmniCombine paired check (src/benchmarking/omni.rs:387-431); top-8 runs
+    the kernel that loads every rank first, other topk the rank-by-rank one."""
+    rng = np.random.default_rng(int(ordered) + 2 * topk)
+    tokens, width = 77, 2048
+    routes = random_routes(rng, tokens, topk=topk)
+    _, order = oracle.group_routes(routes, topk=topk)
     values = randn_bf16(rng, (tokens * topk, width), std=2.0)
-    want = oracle.combine(values, routes, order if ordered else None)
+    want = oracle.combine(values, routes, order if ordered else None, topk=topk)
     got = clef_i4.omni_combine(to_dev_bf16(values), to_dev_f32(routes),
                                to_dev_f32(order) if ordered else None)
     assert_same_u16(bf16_host(got), want, "combine")
