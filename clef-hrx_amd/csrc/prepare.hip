@@ -183,12 +183,14 @@ struct NormSource {
 };
 
 __device__ __forceinline__ uint32_t group_max16(uint32_t m) {
-  // Reduce over the 16 lanes of a group (lanes differ in the low 4 bits).
-#pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) {
-    uint32_t o = (uint32_t)__shfl_xor((int)m, off, 64);
-    m = m > o ? m : o;
-  }
+  // Reduce over the 16 lanes of a group (lanes differ in the low 4 bits): a
+  // DPP row. quad_perm [1,0,3,2] and [2,3,0,1], then row_ror 4 and 8, leave
+  // the row's maximum in every lane (every lane of the wave is active here).
+  auto step = [](uint32_t v, uint32_t o) { return v > o ? v : o; };
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x124, 0xF, 0xF, false));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x128, 0xF, 0xF, false));
   return m;
 }
 
