@@ -144,6 +144,9 @@ __device__ __forceinline__ bool last_slot(const float* rt, int topk, int r, int 
   return true;
 }
 
+// KT > 0: topk == KT, the token's KT route ids loaded together before the
+// atomics; KT == 0: any topk.
+template <int KT>
 __device__ void build_masks(const float* __restrict__ routes, int64_t tokens, int topk,
                             unsigned long long* masks /* [128] */) {
   const int lane = threadIdx.x;
@@ -153,18 +156,28 @@ __device__ void build_masks(const float* __restrict__ routes, int64_t tokens, in
   const int64_t t = (int64_t)blockIdx.x * kGroupBlock + lane;
   if (t < tokens) {
     const float* rt = routes + t * 2 * topk;
-    for (int r = 0; r < topk; ++r) {
-      const int e = route_expert(rt[r]);
-      if (e >= 0) atomicOr(&masks[e], 1ull << lane);
+    if constexpr (KT > 0) {
+      int ex[KT];
+#pragma unroll
+      for (int r = 0; r < KT; ++r) ex[r] = route_expert(rt[r]);
+#pragma unroll
+      for (int r = 0; r < KT; ++r)
+        if (ex[r] >= 0) atomicOr(&masks[ex[r]], 1ull << lane);
+    } else {
+      for (int r = 0; r < topk; ++r) {
+        const int e = route_expert(rt[r]);
+        if (e >= 0) atomicOr(&masks[e], 1ull << lane);
+      }
     }
   }
   __syncthreads();
 }
 
+template <int KT>
 __global__ __launch_bounds__(64) void group_count_kernel(const float* __restrict__ routes, int64_t tokens,
                                                          int topk, int* __restrict__ block_counts) {
   __shared__ unsigned long long masks[128];
-  build_masks(routes, tokens, topk, masks);
+  build_masks<KT>(routes, tokens, topk, masks);
   const int lane = threadIdx.x;
   int* dst = block_counts + (int64_t)blockIdx.x * 128;
   dst[lane] = __popcll(masks[lane]);
@@ -184,16 +197,30 @@ __global__ __launch_bounds__(1024) void group_scan_kernel(int* __restrict__ bloc
   const int64_t per = (blocks + 7) / 8;
   const int64_t b0 = j * per < blocks ? j * per : blocks;
   const int64_t b1 = b0 + per < blocks ? b0 + per : blocks;
+  // The run's counts are read 8 at a time (independent loads in flight
+  // together), summed, then rewritten as exclusive prefixes.
   int sum = 0;
-  for (int64_t b = b0; b < b1; ++b) sum += block_counts[b * 128 + e];
+  for (int64_t b = b0; b < b1; b += 8) {
+    int c[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) c[u] = b + u < b1 ? block_counts[(b + u) * 128 + e] : 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) sum += c[u];
+  }
   part[j][e] = sum;
   __syncthreads();
   int run = 0;
   for (int q = 0; q < j; ++q) run += part[q][e];
-  for (int64_t b = b0; b < b1; ++b) {
-    const int c = block_counts[b * 128 + e];
-    block_counts[b * 128 + e] = run;
-    run += c;
+  for (int64_t b = b0; b < b1; b += 8) {
+    int c[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) c[u] = b + u < b1 ? block_counts[(b + u) * 128 + e] : 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (b + u < b1) {
+        block_counts[(b + u) * 128 + e] = run;
+        run += c[u];
+      }
   }
   if (j == 7) groups[(int64_t)e * (tokens + 1)] = (float)run;
   if (schedule == nullptr) return;
@@ -228,7 +255,7 @@ __global__ __launch_bounds__(64) void group_scatter_kernel(const float* __restri
                                                            int topk, const int* __restrict__ block_offsets,
                                                            float* __restrict__ groups, float* __restrict__ order) {
   __shared__ unsigned long long masks[128];
-  build_masks(routes, tokens, topk, masks);
+  build_masks<KT>(routes, tokens, topk, masks);
   const int lane = threadIdx.x;
   const int64_t t = (int64_t)blockIdx.x * kGroupBlock + lane;
   if (t >= tokens) return;
@@ -597,7 +624,10 @@ hipError_t launch_group_routes(const float* routes, int64_t tokens, int topk, fl
   }
   const int64_t blocks = (tokens + kGroupBlock - 1) / kGroupBlock;
   int* counts = static_cast<int*>(workspace);
-  group_count_kernel<<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts);
+  if (topk == 8)
+    group_count_kernel<8><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts);
+  else
+    group_count_kernel<0><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts);
   group_scan_kernel<<<1, 1024, 0, stream>>>(counts, blocks, tokens, groups, schedule, schedule_bm);
   if (topk == 8)
     group_scatter_kernel<8><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts, groups, order);
