@@ -33,8 +33,8 @@ struct PlainSource {
   struct Raw {
     u4 a, b;
   };
-  __device__ __forceinline__ Raw fetch(int64_t row, int width, int col) const {
-    const u4* p = reinterpret_cast<const u4*>(x + row * width + col);
+  __device__ __forceinline__ Raw fetch(int64_t rowoff, int col) const {
+    const u4* p = reinterpret_cast<const u4*>(x + rowoff + col);
     return Raw{p[0], p[1]};
   }
   __device__ __forceinline__ void convert(const Raw& r, float* v) const {
@@ -45,8 +45,8 @@ struct PlainSource {
       v[2 * i + 1] = bf16_hi(w[i]);
     }
   }
-  __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
-    convert(fetch(row, width, col), v);
+  __device__ __forceinline__ void load16(int64_t rowoff, int col, float* v) const {
+    convert(fetch(rowoff, col), v);
   }
 };
 
@@ -59,9 +59,9 @@ struct SwigluSource {
   struct Raw {
     u4 ga, gb, ua, ub;
   };
-  __device__ __forceinline__ Raw fetch(int64_t row, int width, int col) const {
-    const u4* pg = reinterpret_cast<const u4*>(gate + row * width + col);
-    const u4* pu = reinterpret_cast<const u4*>(up + row * width + col);
+  __device__ __forceinline__ Raw fetch(int64_t rowoff, int col) const {
+    const u4* pg = reinterpret_cast<const u4*>(gate + rowoff + col);
+    const u4* pu = reinterpret_cast<const u4*>(up + rowoff + col);
     return Raw{pg[0], pg[1], pu[0], pu[1]};
   }
   __device__ __forceinline__ void convert(const Raw& r, float* v) const {
@@ -80,8 +80,8 @@ struct SwigluSource {
       v[2 * i + 1] = bf16_round(act[2 * i + 1] * bf16_hi(uw[i]));
     }
   }
-  __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
-    convert(fetch(row, width, col), v);
+  __device__ __forceinline__ void load16(int64_t rowoff, int col, float* v) const {
+    convert(fetch(rowoff, col), v);
   }
 };
 
@@ -96,10 +96,10 @@ struct AttentionGateSource {
   struct Raw {
     u4 xa, xb, ga, gb;
   };
-  __device__ __forceinline__ Raw fetch(int64_t row, int width, int col) const {
-    const u4* px = reinterpret_cast<const u4*>(x + row * width + col);
+  __device__ __forceinline__ Raw fetch(int64_t rowoff, int col) const {
+    const u4* px = reinterpret_cast<const u4*>(x + rowoff + col);
     const int gcol = (col >> 8) * 512 + 256 + (col & 255);  // 16 values stay inside one 256-column half
-    const u4* pg = reinterpret_cast<const u4*>(q_gate + row * 2 * width + gcol);
+    const u4* pg = reinterpret_cast<const u4*>(q_gate + 2 * rowoff + gcol);  // rows of 2 * width
     return Raw{px[0], px[1], pg[0], pg[1]};
   }
   __device__ __forceinline__ static float gated(float x, float g) {
@@ -115,8 +115,8 @@ struct AttentionGateSource {
       v[2 * i + 1] = gated(bf16_hi(a[i]), bf16_hi(g[i]));
     }
   }
-  __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
-    convert(fetch(row, width, col), v);
+  __device__ __forceinline__ void load16(int64_t rowoff, int col, float* v) const {
+    convert(fetch(rowoff, col), v);
   }
 };
 
@@ -133,12 +133,10 @@ struct NormSource {
   const uint16_t* weight;
   uint16_t* normalized;  // nullable
   using Raw = PlainSource::Raw;
-  __device__ __forceinline__ Raw fetch(int64_t row, int width, int col) const {
-    return PlainSource{x}.fetch(row, width, col);
-  }
+  __device__ __forceinline__ Raw fetch(int64_t rowoff, int col) const { return PlainSource{x}.fetch(rowoff, col); }
   __device__ __forceinline__ void convert(const Raw& r, float* v) const { PlainSource{x}.convert(r, v); }
-  __device__ __forceinline__ void load16(int64_t row, int width, int col, float* v) const {
-    convert(fetch(row, width, col), v);
+  __device__ __forceinline__ void load16(int64_t rowoff, int col, float* v) const {
+    convert(fetch(rowoff, col), v);
   }
   template <int P>
   __device__ __forceinline__ void normalize(float (&v)[P][16], int64_t row, int width, int grp0, int L,
@@ -244,7 +242,7 @@ __global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int
   for (int p = 0; p < P; ++p) {
     const int grp = grp0 + 16 * p;
     if (active && grp < G) {
-      src.load16(row, width, grp * 256 + 16 * L, v[p]);
+      src.load16(row * width, grp * 256 + 16 * L, v[p]);
     } else {
 #pragma unroll
       for (int i = 0; i < 16; ++i) v[p][i] = 0.0f;
@@ -361,14 +359,17 @@ __global__ __launch_bounds__(256) void prepare_loop_kernel(Src src, int64_t rows
   constexpr int per = 32 / BITS;
   constexpr float qmax = BITS == 8 ? 127.0f : 7.0f;
 
+  // The row and its input and output offsets advance by one grid stride per
+  // block (additions, not the quarter-rate 64-bit multiplies per iteration).
+  const int col = grp * 256 + 16 * L;
+  const int64_t step = (int64_t)gridDim.x * rows_per_block;
+  const int64_t in_step = step * width, out_step = step * out_words;
   int64_t blk = blockIdx.x;
+  int64_t row = blk * rows_per_block + row_local;
+  int64_t in_off = row * width, out_off = row * out_words;
   typename Src::Raw raw{};
-  {
-    const int64_t row = blk * rows_per_block + row_local;
-    if (lane_on && row < rows) raw = src.fetch(row, width, grp * 256 + 16 * L);
-  }
-  for (; blk < nblk; blk += gridDim.x) {
-    const int64_t row = blk * rows_per_block + row_local;
+  if (lane_on && row < rows) raw = src.fetch(in_off, col);
+  for (; blk < nblk; blk += gridDim.x, row += step, in_off += in_step, out_off += out_step) {
     const bool on = lane_on && row < rows;
     float v[16];
     if (on) {
@@ -377,10 +378,7 @@ __global__ __launch_bounds__(256) void prepare_loop_kernel(Src src, int64_t rows
 #pragma unroll
       for (int i = 0; i < 16; ++i) v[i] = 0.0f;
     }
-    {
-      const int64_t nrow = (blk + gridDim.x) * rows_per_block + row_local;
-      if (lane_on && nrow < rows) raw = src.fetch(nrow, width, grp * 256 + 16 * L);
-    }
+    if (lane_on && row + step < rows) raw = src.fetch(in_off + in_step, col);
     radix4x2(v);  // strides 1 and 4
     float4* wrow = reinterpret_cast<float4*>(buf + L * kPitch);
 #pragma unroll
@@ -401,20 +399,31 @@ __global__ __launch_bounds__(256) void prepare_loop_kernel(Src src, int64_t rows
     mbits = group_max16(mbits);
     if (L == 0) gmax[lg * kGroupLds] = mbits;
     __syncthreads();
-    uint32_t m = 0;
-    for (int g = 0; g < G; ++g) {
-      uint32_t o = gmax[((lane_on ? row_local : 0) * G + g) * kGroupLds];
-      m = m > o ? m : o;
+    // Row r's scale and 1/16-scale by thread r of wave 0 (the other waves
+    // skip the divisions), kept in floats 17 and 18 of group r's first LDS
+    // row (padding the transposes never touch) and read after the next
+    // barrier.
+    if (threadIdx.x < rows_per_block) {
+      const int r = threadIdx.x;
+      uint32_t m = 0;
+      for (int g = 0; g < G; ++g) {
+        const uint32_t o = gmax[(r * G + g) * kGroupLds];
+        m = m > o ? m : o;
+      }
+      const float mf = m >= 0x7f800000u ? __builtin_huge_valf() : as_float(m);
+      const float normal = mf * 0.0625f;
+      const float safe = __builtin_fmaxf(normal, 1e-30f);
+      const float sc = safe / qmax;
+      lds[r * kGroupLds + 17] = sc;
+      lds[r * kGroupLds + 18] = 0.0625f / sc;
     }
-    const float mf = m >= 0x7f800000u ? __builtin_huge_valf() : as_float(m);
-    const float normal = mf * 0.0625f;
-    const float safe = __builtin_fmaxf(normal, 1e-30f);
-    const float scale = safe / qmax;
-    const bool valid = scale < __builtin_huge_valf();
-    const float inv = 0.0625f / scale;
 #pragma unroll
     for (int k = 0; k < 16; ++k) buf[k * kPitch + L] = v[k];
     __syncthreads();
+    const int srow = lane_on ? row_local : 0;
+    const float scale = lds[srow * kGroupLds + 17];
+    const float inv = lds[srow * kGroupLds + 18];
+    const bool valid = scale < __builtin_huge_valf();
     float nat[16];
     const float4* rrow = reinterpret_cast<const float4*>(buf + L * kPitch);
 #pragma unroll
@@ -427,7 +436,7 @@ __global__ __launch_bounds__(256) void prepare_loop_kernel(Src src, int64_t rows
     }
     __syncthreads();
     if (on) {
-      uint32_t* dst = out + row * out_words + (grp * 256 + 16 * L) / per;
+      uint32_t* dst = out + out_off + col / per;
       if (BITS == 4) {
         *reinterpret_cast<uint2*>(dst) = make_uint2(pack_codes<4>(nat, inv, valid), pack_codes<4>(nat + 8, inv, valid));
       } else {
