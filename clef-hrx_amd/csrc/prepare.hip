@@ -29,6 +29,7 @@ constexpr int kGroupLds = 16 * kPitch; // LDS floats per 256-column group
 
 struct PlainSource {
   static constexpr bool kRowNorm = false;
+  static constexpr bool kLdsTable = false;
   const uint16_t* x;
   struct Raw {
     u4 a, b;
@@ -54,6 +55,8 @@ struct PlainSource {
 // rotation sees f32(bf16(swiglu)) exactly as if h had been materialized.
 struct SwigluSource {
   static constexpr bool kRowNorm = false;
+  // prepare_kernel copies the SiLU table into LDS for convert_with.
+  static constexpr bool kLdsTable = true;
   const uint16_t* gate;
   const uint16_t* up;
   struct Raw {
@@ -64,7 +67,8 @@ struct SwigluSource {
     const u4* pu = reinterpret_cast<const u4*>(up + rowoff + col);
     return Raw{pg[0], pg[1], pu[0], pu[1]};
   }
-  __device__ __forceinline__ void convert(const Raw& r, float* v) const {
+  __device__ __forceinline__ void convert(const Raw& r, float* v) const { convert_with(r, v, g_silu_lut); }
+  __device__ __forceinline__ void convert_with(const Raw& r, float* v, const uint16_t* table) const {
     const uint32_t gw[8] = {r.ga.x, r.ga.y, r.ga.z, r.ga.w, r.gb.x, r.gb.y, r.gb.z, r.gb.w};
     const uint32_t uw[8] = {r.ua.x, r.ua.y, r.ua.z, r.ua.w, r.ub.x, r.ub.y, r.ub.z, r.ub.w};
     float g[16], act[16];
@@ -73,7 +77,7 @@ struct SwigluSource {
       g[2 * i] = bf16_lo(gw[i]);
       g[2 * i + 1] = bf16_hi(gw[i]);
     }
-    silu_lut<16>(g, act);  // = silu_bf16(g), from the table where it covers g
+    silu_lut<16>(g, act, table);  // = silu_bf16(g), from the table where it covers g
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       v[2 * i] = bf16_round(act[2 * i] * bf16_lo(uw[i]));
@@ -91,6 +95,7 @@ struct SwigluSource {
 // value is bf16(x * bf16(1 / (1 + exp(-g)))).
 struct AttentionGateSource {
   static constexpr bool kRowNorm = false;
+  static constexpr bool kLdsTable = false;
   const uint16_t* x;
   const uint16_t* q_gate;
   struct Raw {
@@ -129,6 +134,7 @@ struct AttentionGateSource {
 // optionally stored to `normalized`. Used by the one-row-per-workgroup kernel.
 struct NormSource {
   static constexpr bool kRowNorm = true;
+  static constexpr bool kLdsTable = false;
   const uint16_t* x;
   const uint16_t* weight;
   uint16_t* normalized;  // nullable
@@ -238,14 +244,42 @@ __global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int
   float* buf = lds + lg * kGroupLds;
 
   float v[P][16];
+  if constexpr (Src::kLdsTable) {
+    // The SiLU table (16 KiB) goes into the transpose buffer, which is idle
+    // until the values are converted: LDS reads instead of one global gather
+    // per value. Its loads go out with the inputs'.
+    static_assert(kSiluLutSize * 2 <= 16 * kGroupLds * 4 && kSiluLutSize * 2 == 256 * 4 * 16, "table copy");
+    u4 t[4];
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int grp = grp0 + 16 * p;
-    if (active && grp < G) {
-      src.load16(row * width, grp * 256 + 16 * L, v[p]);
-    } else {
+    for (int i = 0; i < 4; ++i) t[i] = reinterpret_cast<const u4*>(g_silu_lut)[tid + 256 * i];
+    typename Src::Raw raw[P];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) v[p][i] = 0.0f;
+    for (int p = 0; p < P; ++p)
+      if (active && grp0 + 16 * p < G) raw[p] = src.fetch(row * width, (grp0 + 16 * p) * 256 + 16 * L);
+    uint16_t* table = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) reinterpret_cast<u4*>(table)[tid + 256 * i] = t[i];
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      if (active && grp0 + 16 * p < G) {
+        src.convert_with(raw[p], v[p], table);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[p][i] = 0.0f;
+      }
+    }
+    __syncthreads();  // the table's LDS becomes the transpose buffer
+  } else {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int grp = grp0 + 16 * p;
+      if (active && grp < G) {
+        src.load16(row * width, grp * 256 + 16 * L, v[p]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[p][i] = 0.0f;
+      }
     }
   }
   if constexpr (Src::kRowNorm) {

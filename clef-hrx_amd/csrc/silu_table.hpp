@@ -9,21 +9,22 @@
 
 namespace clef {
 
-__device__ const uint16_t g_silu_lut[kSiluLutSize] __attribute__((unused)) = {
+__device__ const uint16_t g_silu_lut[kSiluLutSize] __attribute__((unused, aligned(16))) = {
 #include "silu_table.inc"
 };
 
 // bf16(silu(g)) for N bf16 values g (exact bf16 values in f32): table reads
 // for all, then one wave-uniform branch for values outside the table.
+// `table` is g_silu_lut or a copy of it (in LDS).
 template <int N>
-__device__ __forceinline__ void silu_lut(const float (&g)[N], float (&act)[N]) {
+__device__ __forceinline__ void silu_lut(const float (&g)[N], float (&act)[N], const uint16_t* table = g_silu_lut) {
   bool inside[N];
   bool slow = false;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const uint32_t off = silu_lut_offset(as_uint(g[i]), inside[i]);
     slow |= !inside[i];
-    act[i] = bf16_to_f32(g_silu_lut[off >> 1]);
+    act[i] = bf16_to_f32(table[off >> 1]);
   }
   if (__any(slow)) {
 #pragma unroll
