@@ -424,10 +424,16 @@ int clef_moe_layer(const uint16_t* x, const void* logits, int32_t logits_dtype, 
 
 #define CLEF_STEP(call) \
   if (int rc = hip_status(call)) return rc
-  CLEF_STEP(clef::launch_route(logits, logits_dtype, tokens, experts, topk, routes, s));
-  CLEF_STEP(clef::launch_group_routes(routes, tokens, topk, groups, order, ws + l.group_ws, s, schedule,
-                                      clef::expert_tile_rows(routed)));
-  CLEF_STEP(clef::launch_prepare(x, tokens, hidden, sx, 4, ax, s));
+  if (clef::route_prepare_fusable(hidden)) {  // router and the quantizer of x side by side
+    CLEF_STEP(clef::launch_route_prepare(logits, logits_dtype, tokens, experts, topk, routes, x, hidden, sx, ax, s));
+    CLEF_STEP(clef::launch_group_routes(routes, tokens, topk, groups, order, ws + l.group_ws, s, schedule,
+                                        clef::expert_tile_rows(routed)));
+  } else {
+    CLEF_STEP(clef::launch_route(logits, logits_dtype, tokens, experts, topk, routes, s));
+    CLEF_STEP(clef::launch_group_routes(routes, tokens, topk, groups, order, ws + l.group_ws, s, schedule,
+                                        clef::expert_tile_rows(routed)));
+    CLEF_STEP(clef::launch_prepare(x, tokens, hidden, sx, 4, ax, s));
+  }
   if (tokens * (int64_t)(sx / 8) * 4 < ((int64_t)1 << 31)) {
     // Gate and up share one pass over the gathered x rows and SwiGLU runs in
     // their epilogue; h is then quantized per routed row. Bit-equal to the

@@ -11,6 +11,13 @@ namespace clef {
 
 hipError_t launch_prepare(const uint16_t* x, int64_t rows, int width, int stride, int bits,
                           uint32_t* out, hipStream_t stream);
+// The router and the INT4 quantizer of `x` ([tokens][width], stride as
+// launch_prepare) in one launch; only for widths the grid-stride quantizer
+// takes (route_prepare_fusable).
+bool route_prepare_fusable(int width);
+hipError_t launch_route_prepare(const void* logits, int dtype, int64_t tokens, int experts, int topk,
+                                float* routes, const uint16_t* x, int width, int stride, uint32_t* out,
+                                hipStream_t stream);
 hipError_t launch_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t rows, int width,
                                  int stride, int bits, uint32_t* out, hipStream_t stream);
 hipError_t launch_prepare_attention_gate(const uint16_t* x, const uint16_t* q_gate, int64_t rows, int width,

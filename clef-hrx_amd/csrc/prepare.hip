@@ -19,6 +19,7 @@
 #include "common.hpp"
 #include "silu_table.hpp"
 #include "kernels.hpp"
+#include "route.hpp"
 
 namespace clef {
 
@@ -373,9 +374,10 @@ __global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int
 // walks row blocks (16 / G rows each) with a grid stride and fetches the next
 // block's inputs before rotating and packing the current one, so HBM latency
 // overlaps the work instead of being paid once per workgroup.
+// The body runs as workgroup `block` of `nblocks` walking the row blocks.
 template <int BITS, class Src>
-__global__ __launch_bounds__(256) void prepare_loop_kernel(Src src, int64_t rows, int width, int out_words,
-                                                           uint32_t* __restrict__ out) {
+__device__ __forceinline__ void prepare_loop_body(Src src, int64_t rows, int width, int out_words,
+                                                  uint32_t* __restrict__ out, int64_t block, int64_t nblocks) {
   // 20 KiB: eight workgroups fill a CU's LDS. Each group's maximum goes to
   // the padding float of its first LDS row, which the transposes never touch.
   __shared__ __align__(16) float lds[16 * kGroupLds];
@@ -396,14 +398,14 @@ __global__ __launch_bounds__(256) void prepare_loop_kernel(Src src, int64_t rows
   // The row and its input and output offsets advance by one grid stride per
   // block (additions, not the quarter-rate 64-bit multiplies per iteration).
   const int col = grp * 256 + 16 * L;
-  const int64_t step = (int64_t)gridDim.x * rows_per_block;
+  const int64_t step = nblocks * rows_per_block;
   const int64_t in_step = step * width, out_step = step * out_words;
-  int64_t blk = blockIdx.x;
+  int64_t blk = block;
   int64_t row = blk * rows_per_block + row_local;
   int64_t in_off = row * width, out_off = row * out_words;
   typename Src::Raw raw{};
   if (lane_on && row < rows) raw = src.fetch(in_off, col);
-  for (; blk < nblk; blk += gridDim.x, row += step, in_off += in_step, out_off += out_step) {
+  for (; blk < nblk; blk += nblocks, row += step, in_off += in_step, out_off += out_step) {
     const bool on = lane_on && row < rows;
     float v[16];
     if (on) {
@@ -481,6 +483,29 @@ __global__ __launch_bounds__(256) void prepare_loop_kernel(Src src, int64_t rows
       if (grp == 0 && L == 0) reinterpret_cast<float*>(out + rows * out_words)[row] = scale;
     }
   }
+}
+
+template <int BITS, class Src>
+__global__ __launch_bounds__(256) void prepare_loop_kernel(Src src, int64_t rows, int width, int out_words,
+                                                           uint32_t* __restrict__ out) {
+  prepare_loop_body<BITS, Src>(src, rows, width, out_words, out, blockIdx.x, gridDim.x);
+}
+
+// The router and the INT4 quantizer of the MoE input in one launch: the first
+// route_blocks workgroups route four tokens each, the others run the
+// grid-stride quantizer. Neither needs the other's output, so they share the
+// GPU instead of running one after the other.
+__global__ __launch_bounds__(256) void route_prepare_kernel(const void* __restrict__ logits, int dtype,
+                                                            int64_t tokens, int experts, int topk,
+                                                            float* __restrict__ routes, int64_t route_blocks,
+                                                            PlainSource src, int width, int out_words,
+                                                            uint32_t* __restrict__ out) {
+  if ((int64_t)blockIdx.x < route_blocks) {
+    route_impl::route_body(logits, dtype, tokens, experts, topk, routes, blockIdx.x);
+    return;
+  }
+  prepare_loop_body<4, PlainSource>(src, tokens, width, out_words, out, blockIdx.x - route_blocks,
+                                    gridDim.x - route_blocks);
 }
 
 template <int BITS, class Src>
@@ -578,6 +603,21 @@ __global__ __launch_bounds__(256) void tile_permute_kernel(const uint16_t* __res
 hipError_t launch_prepare(const uint16_t* x, int64_t rows, int width, int stride, int bits,
                           uint32_t* out, hipStream_t stream) {
   return launch_prepare_src(PlainSource{x}, rows, width, stride, bits, out, stream);
+}
+
+bool route_prepare_fusable(int width) { return width % 256 == 0 && width / 256 <= 16; }
+
+hipError_t launch_route_prepare(const void* logits, int dtype, int64_t tokens, int experts, int topk,
+                                float* routes, const uint16_t* x, int width, int stride, uint32_t* out,
+                                hipStream_t stream) {
+  if (!route_prepare_fusable(width)) return hipErrorInvalidValue;
+  const int per_block = 16 / (width / 256);
+  const int64_t blocks = (tokens + per_block - 1) / per_block;
+  const int64_t prep = blocks < 2048 ? blocks : 2048;
+  const int64_t route_blocks = (tokens + 3) / 4;
+  route_prepare_kernel<<<(unsigned)(route_blocks + prep), 256, 0, stream>>>(
+      logits, dtype, tokens, experts, topk, routes, route_blocks, PlainSource{x}, width, stride / 8, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t rows, int width,
