@@ -92,6 +92,38 @@ __global__ __launch_bounds__(64) void group_count_kernel(const float* __restrict
   dst[64 + lane] = __popcll(masks[64 + lane]);
 }
 
+// The expert GEMM's tile list from the experts' counts: tiles of bm slots,
+// schedule = [total] then (expert, first slot) per tile, experts ascending.
+// `holder` threads (one per expert e) pass e's count; every thread of the
+// workgroup calls this. The tile counts' exclusive prefix is one wave's scan,
+// two experts per lane, between two barriers.
+__device__ void write_tile_schedule(int count, bool holder, int e, int bm, int* tiles_lds /* [128] */,
+                                    int32_t* __restrict__ schedule) {
+  if (holder) tiles_lds[e] = (count + bm - 1) / bm;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int l = threadIdx.x;
+    const int t0 = tiles_lds[2 * l], t1 = tiles_lds[2 * l + 1];
+    int incl = t0 + t1;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (l >= off) incl += o;
+    }
+    tiles_lds[2 * l] = incl - t0 - t1;  // first tile of each expert
+    tiles_lds[2 * l + 1] = incl - t1;
+    if (l == 63) schedule[0] = incl;
+  }
+  __syncthreads();
+  if (holder) {
+    const int start = tiles_lds[e], tiles = (count + bm - 1) / bm;
+    for (int t = 0; t < tiles; ++t) {
+      schedule[1 + 2 * (start + t)] = e;
+      schedule[2 + 2 * (start + t)] = t * bm;
+    }
+  }
+}
+
 // One workgroup of 1024 threads: 8 threads per expert, each summing a
 // contiguous run of blocks, then an 8-way scan. With `schedule` non-NULL it
 // also writes the expert GEMM's tile list: [count] then (expert, first slot)
@@ -132,28 +164,7 @@ __global__ __launch_bounds__(1024) void group_scan_kernel(int* __restrict__ bloc
   }
   if (j == 7) groups[(int64_t)e * (tokens + 1)] = (float)run;
   if (schedule == nullptr) return;
-  // run of thread j == 7 is expert e's count
-  int tiles = 0;
-  if (j == 7) {
-    tiles = (run + bm - 1) / bm;
-    tiles_scan[e] = tiles;
-  }
-  __syncthreads();
-  for (int off = 1; off < 128; off <<= 1) {
-    int v = 0;
-    if (j == 7 && e >= off) v = tiles_scan[e - off];
-    __syncthreads();
-    if (j == 7) tiles_scan[e] += v;
-    __syncthreads();
-  }
-  if (j == 7) {
-    const int start = tiles_scan[e] - tiles;
-    for (int t = 0; t < tiles; ++t) {
-      schedule[1 + 2 * (start + t)] = e;
-      schedule[2 + 2 * (start + t)] = t * bm;
-    }
-    if (e == 127) schedule[0] = tiles_scan[127];
-  }
+  write_tile_schedule(run, j == 7, e, bm, tiles_scan, schedule);  // run of thread j == 7 is e's count
 }
 
 // KT > 0: topk == KT, the token's route ids held in registers; KT == 0: any
@@ -287,29 +298,7 @@ __global__ __launch_bounds__(1024) void group_single_kernel(const float* __restr
       run += c;
     }
     if (j == 7) groups[(int64_t)e * (tokens + 1)] = (float)run;
-    if (schedule != nullptr) {  // the expert GEMM's tile list, as group_scan_kernel
-      int tiles = 0;
-      if (j == 7) {
-        tiles = (run + bm - 1) / bm;
-        tiles_scan[e] = tiles;
-      }
-      __syncthreads();
-      for (int off = 1; off < 128; off <<= 1) {
-        int v = 0;
-        if (j == 7 && e >= off) v = tiles_scan[e - off];
-        __syncthreads();
-        if (j == 7) tiles_scan[e] += v;
-        __syncthreads();
-      }
-      if (j == 7) {
-        const int start = tiles_scan[e] - tiles;
-        for (int t = 0; t < tiles; ++t) {
-          schedule[1 + 2 * (start + t)] = e;
-          schedule[2 + 2 * (start + t)] = t * bm;
-        }
-        if (e == 127) schedule[0] = tiles_scan[127];
-      }
-    }
+    if (schedule != nullptr) write_tile_schedule(run, j == 7, e, bm, tiles_scan, schedule);
   }
   __syncthreads();
   // scatter
