@@ -29,6 +29,7 @@ _SZ = ctypes.c_size_t
 SIGNATURES = {
     "clef_last_error": (ctypes.c_char_p, []),
     "clef_abi_version": (ctypes.c_int, []),
+    "clef_build_id": (ctypes.c_char_p, []),
     "clef_i4_activation_stride": (_I32, [_I32, _I32]),
     "clef_i4_prepared_words": (_I64, [_I64, _I32, _I32]),
     "clef_i4_prepare": (ctypes.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P]),
@@ -79,11 +80,15 @@ class ClefError(RuntimeError):
 
 
 def lib() -> ctypes.CDLL:
+    """The loaded library. Raises ImportError when it is missing or, where the
+    sources sit beside it, built from other sources than the tree's."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise ImportError(f"{LIB_PATH} is not built; run `make -C clef-hrx_amd` "
-                              "(or __graft_entry__.build())")
+        import build_id
+
+        problem = build_id.stale()
+        if problem:
+            raise ImportError(f"{problem}; run `make -C clef-hrx_amd` (or __graft_entry__.build())")
         handle = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(handle, name)

@@ -11,10 +11,8 @@
 
 #include <atomic>
 
-#include "gemm_core.hpp"
 #include "silu_table.hpp"
 #include "gemm_dma.hpp"
-#include "gemm_persist.hpp"
 #include "gemm_dmah.hpp"
 #include "kernels.hpp"
 
@@ -68,69 +66,6 @@ __device__ __forceinline__ uint32_t g1_value(int32_t acc, float ws, float as) {
   float sat = __builtin_fmaxf(__builtin_fminf(y, kBf16Max), -kBf16Max);
   float checked = __builtin_fabsf(y) < __builtin_huge_valf() ? sat : y;
   return f32_to_bf16(checked);
-}
-
-__device__ __forceinline__ uint32_t add_residual(uint32_t out, uint32_t res) {
-  return f32_to_bf16(bf16_to_f32(res) + bf16_to_f32(out));
-}
-
-template <class T, bool RESID>
-__global__ __launch_bounds__(256) void gemm_i4_kernel(
-    const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
-    const uint32_t* __restrict__ w, const float* __restrict__ ws, int64_t M, int N, int kb,
-    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_n) {
-  extern __shared__ __align__(16) char lds[];
-  const int tid = threadIdx.x;
-  const int64_t bid = blockIdx.x;
-  const int tn = (int)(bid % tiles_n);
-  const int64_t m0 = (bid / tiles_n) * T::BM;
-  const int n0 = tn * T::BN;
-
-  const uint32_t* a_ptr[T::AL];
-  const uint32_t* b_ptr[T::BL];
-#pragma unroll
-  for (int j = 0; j < T::AL; ++j) {
-    const int idx = tid + 256 * j;
-    int64_t row = m0 + (idx >> 3);
-    row = row < M ? row : M - 1;
-    a_ptr[j] = a + row * a_words + (idx & 7) * 4;
-  }
-#pragma unroll
-  for (int j = 0; j < T::BL; ++j) {
-    const int idx = tid + 256 * j;
-    const int64_t nb = n0 / 128 + (idx >> 10);
-    b_ptr[j] = w + nb * kb * 4096 + (idx & 1023) * 4;
-  }
-  v4i acc[T::TM][T::TN];
-  gemm_mainloop<T>(a_ptr, b_ptr, kb, lds, acc);
-
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
-  const int g = lane >> 4, lr = lane & 15;
-#pragma unroll
-  for (int i = 0; i < T::TM; ++i) {
-    const int64_t m = m0 + wm * T::WM + 16 * i + lr;
-    if (m >= M) continue;
-    const float asv = as[m];
-#pragma unroll
-    for (int j = 0; j < T::TN; ++j) {
-      const int n = n0 + wn * T::WN + 16 * j + 4 * g;
-      const float4 wsv = *reinterpret_cast<const float4*>(ws + n);
-      uint32_t v0 = g1_value(acc[i][j].x, wsv.x, asv);
-      uint32_t v1 = g1_value(acc[i][j].y, wsv.y, asv);
-      uint32_t v2 = g1_value(acc[i][j].z, wsv.z, asv);
-      uint32_t v3 = g1_value(acc[i][j].w, wsv.w, asv);
-      uint2* dst = reinterpret_cast<uint2*>(out + m * N + n);
-      if (RESID) {
-        const uint2 r = *reinterpret_cast<const uint2*>(residual + m * N + n);
-        v0 = add_residual(v0, r.x & 0xffffu);
-        v1 = add_residual(v1, r.x >> 16);
-        v2 = add_residual(v2, r.y & 0xffffu);
-        v3 = add_residual(v3, r.y >> 16);
-      }
-      *dst = make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
-    }
-  }
 }
 
 // G1 epilogue for the 32x32 MFMA layout (lane: row m = l % 32; register r:
@@ -328,151 +263,13 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dma8_kernel(
 #endif
 }
 
-// Same contraction on the half-k-step core: 4 waves, 72 KiB of LDS, two
-// workgroups per CU.
-template <class T, bool RESID>
-__global__ __launch_bounds__(T::THREADS, 2) void gemm_dmah_kernel(
-    const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
-    const uint32_t* __restrict__ w, const float* __restrict__ ws, int64_t M, int N, int kb,
-    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  extern __shared__ __align__(16) char lds[];
-  int64_t tm;
-  int tn;
-  tile_of_block(blockIdx.x, (int64_t)gridDim.x, tiles_m, tiles_n, tm, tn);
-  const int64_t m0 = tm * T::BM;
-  const int n0 = tn * T::BN;
-  const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
-  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a + m0 * a_words, (uint32_t)(rows_here * a_words * 4));
-  const __amdgpu_buffer_rsrc_t b_rsrc =
-      make_rsrc(w + (int64_t)(n0 / 128) * kb * 4096, (uint32_t)((T::BN / 128) * kb * 16384));
-  v16i acc[T::TM][T::TN];
-  int voff_a[T::A_INST];
-  {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int ql = 0; ql < T::A_INST; ++ql) voff_a[ql] = (lane >> 2) * a_words * 4 + dmah_chunk16(lane);
-  }
-  dmah_mainloop<T>(a_rsrc, voff_a, a_words * 4, b_rsrc, b_rsrc, kb, lds, acc);
-  dense_epilogue<T, RESID>(acc, as, ws, M, N, kb * 256, m0, n0, residual, out, lds);
-#endif
-}
-
-// Scales and fast-path flag of a G1 tile epilogue, loaded ahead of the
-// epilogue (so no global load waits there).
+// Scales and fast-path flag of a G1 tile epilogue (epi_scales_from_lds).
 template <class T>
 struct EpiScales {
   float asr[T::TM];
   float4 wsr[T::TN][4];
   bool fast;
 };
-
-// The loads only; epi_scales_finish computes the flag. Issued ahead of a DMA,
-// the loads can then be waited for without waiting for the DMA.
-template <class T>
-__device__ __forceinline__ void epi_scales_issue(EpiScales<T>& e, const float* __restrict__ as,
-                                                 const float* __restrict__ ws, int64_t M, int64_t m0, int n0) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
-  const int h = lane >> 5, lr = lane & 31;
-#pragma unroll
-  for (int i = 0; i < T::TM; ++i) {
-    const int64_t m = m0 + wm * T::WM + 32 * i + lr;
-    e.asr[i] = m < M ? as[m] : 0.0f;
-  }
-#pragma unroll
-  for (int j = 0; j < T::TN; ++j)
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      e.wsr[j][q] = *reinterpret_cast<const float4*>(ws + n0 + wn * T::WN + 32 * j + 8 * q + 4 * h);
-}
-
-template <class T>
-__device__ __forceinline__ void epi_scales_finish(EpiScales<T>& e, int K) {
-  const float inf = __builtin_huge_valf();
-  float mas = 0.0f;
-#pragma unroll
-  for (int i = 0; i < T::TM; ++i) {
-    const float a = __builtin_fabsf(e.asr[i]);
-    mas = __builtin_fmaxf(mas, a < inf ? a : 0.0f);
-  }
-  float mws = 0.0f;
-  bool exact = true;
-#pragma unroll
-  for (int j = 0; j < T::TN; ++j)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float w4[4] = {e.wsr[j][q].x, e.wsr[j][q].y, e.wsr[j][q].z, e.wsr[j][q].w};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        exact = exact && (w4[t] * 0.00390625f) * 256.0f == w4[t];
-        const float a = __builtin_fabsf(w4[t]);
-        mws = __builtin_fmaxf(mws, a < inf ? a : 0.0f);
-      }
-    }
-  e.fast = __all(exact && mws * mas * (98.0f * (float)K) < kBf16Max);
-}
-
-template <class T>
-__device__ __forceinline__ EpiScales<T> epi_scales_load(const float* __restrict__ as, const float* __restrict__ ws,
-                                                        int64_t M, int K, int64_t m0, int n0) {
-  EpiScales<T> e;
-  epi_scales_issue<T>(e, as, ws, M, m0, n0);
-  epi_scales_finish<T>(e, K);
-  return e;
-}
-
-// G1 tile epilogue stored straight from the accumulators: TM * TN * 4 buffer
-// stores per wave (plus as many residual loads), rows past M fall outside the
-// output range and are dropped. Same values as dense_epilogue.
-template <class T, bool RESID>
-__device__ __forceinline__ void direct_epilogue_store(const v16i (&acc)[T::TM][T::TN], const EpiScales<T>& e,
-                                                      int64_t M, int N, int64_t m0, int n0,
-                                                      const uint16_t* __restrict__ residual,
-                                                      uint16_t* __restrict__ out) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
-  const int h = lane >> 5, lr = lane & 31;
-  const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
-  const __amdgpu_buffer_rsrc_t out_rsrc = make_rsrc(out + m0 * N, (uint32_t)(rows_here * N * 2));
-  const __amdgpu_buffer_rsrc_t res_rsrc =
-      make_rsrc(RESID ? residual + m0 * N : out, RESID ? (uint32_t)(rows_here * N * 2) : 0u);
-#pragma unroll
-  for (int i = 0; i < T::TM; ++i) {
-    const float asv = e.asr[i];
-    const int row = wm * T::WM + 32 * i + lr;
-#pragma unroll
-    for (int j = 0; j < T::TN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int col = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
-        const int off = (row * N + col) * 2;
-        const float4 wsv = e.wsr[j][q];
-        uint32_t p0, p1;
-        if (e.fast) {
-          const float w4[4] = {wsv.x, wsv.y, wsv.z, wsv.w};
-          float y[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            y[t] = (float)acc[i][j][4 * q + t] * (w4[t] * 0.00390625f);
-            y[t] = y[t] * asv;
-            y[t] = y[t] + 0.0f;
-          }
-          p0 = pack_bf16x2(y[0], y[1]);
-          p1 = pack_bf16x2(y[2], y[3]);
-        } else {
-          p0 = g1_value(acc[i][j][4 * q + 0], wsv.x, asv) | (g1_value(acc[i][j][4 * q + 1], wsv.y, asv) << 16);
-          p1 = g1_value(acc[i][j][4 * q + 2], wsv.z, asv) | (g1_value(acc[i][j][4 * q + 3], wsv.w, asv) << 16);
-        }
-        if (RESID) {
-          const v2i r = __builtin_amdgcn_raw_buffer_load_b64(res_rsrc, off, 0, 0);
-          p0 = pack_bf16x2(bf16_lo((uint32_t)r.x) + bf16_lo(p0), bf16_hi((uint32_t)r.x) + bf16_hi(p0));
-          p1 = pack_bf16x2(bf16_lo((uint32_t)r.y) + bf16_lo(p1), bf16_hi((uint32_t)r.y) + bf16_hi(p1));
-        }
-        __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)p0, (int)p1}, out_rsrc, off, 0, 0);
-      }
-  }
-}
 
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
@@ -630,49 +427,6 @@ __device__ __forceinline__ void staged_epilogue_store(const v16i (&acc)[T::TM][T
       __builtin_amdgcn_raw_buffer_store_b128(v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]}, out_rsrc, voff, soff, 0);
     }
   }
-}
-
-template <class T, bool RESID>
-__device__ __forceinline__ void direct_epilogue(const v16i (&acc)[T::TM][T::TN], const float* __restrict__ as,
-                                                const float* __restrict__ ws, int64_t M, int N, int K,
-                                                int64_t m0, int n0, const uint16_t* __restrict__ residual,
-                                                uint16_t* __restrict__ out) {
-  const EpiScales<T> e = epi_scales_load<T>(as, ws, M, K, m0, n0);
-  direct_epilogue_store<T, RESID>(acc, e, M, N, m0, n0, residual, out);
-}
-
-template <class T, bool RESID>
-__global__ __launch_bounds__(T::THREADS) void gemm_persistent_kernel(
-    const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
-    const uint32_t* __restrict__ w, const float* __restrict__ ws, int64_t M, int N, int kb,
-    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
-#if defined(__HIP_DEVICE_COMPILE__)  // buffer-resource builtins exist only in the device pass
-  extern __shared__ __align__(16) char lds[];
-  const int total = tiles_m * tiles_n;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  auto get = [&](int t) {
-    TileRsrc ta;
-    int64_t tm;
-    int tn;
-    tile_of_block(t, total, tiles_m, tiles_n, tm, tn);
-    const int64_t m0 = tm * T::BM;
-    const int n0 = tn * T::BN;
-    const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
-    ta.a_rsrc = make_rsrc(a + m0 * a_words, (uint32_t)(rows_here * a_words * 4));
-    ta.b_rsrc = make_rsrc(w + (int64_t)(n0 / 128) * kb * 4096, (uint32_t)((T::BN / 128) * kb * 16384));
-    return ta;
-  };
-  auto epi = [&](int t, const v16i (&acc)[T::TM][T::TN]) {
-    int64_t tm;
-    int tn;
-    tile_of_block(t, total, tiles_m, tiles_n, tm, tn);
-    direct_epilogue<T, RESID>(acc, as, ws, M, N, kb * 256, tm * T::BM, tn * T::BN, residual, out);
-  };
-  const int voff = (lane >> 3) * a_words * 4 + dma_chunk16(wave, lane);
-  persistent_loop<T, T::TM * T::TN * 4, TileRsrc>(blockIdx.x, gridDim.x, total, kb, voff, a_words * 4, lds, get,
-                                                  epi);
-#endif
 }
 
 // Last k-step of one tile and first k-step of the next, in one inlined body
@@ -855,61 +609,16 @@ hipError_t launch_dma_persist_any(const uint32_t* a, int a_words, const float* a
 }
 
 template <class T, bool RESID>
-hipError_t launch_persistent(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
-                             const float* ws, int64_t m, int n, int k, const uint16_t* residual,
-                             uint16_t* out, int per_cu, hipStream_t stream) {
-  static LaunchCache cache;
-  const void* kern = reinterpret_cast<const void*>(&gemm_persistent_kernel<T, RESID>);
-  if (hipError_t e = ensure_dynamic_lds(cache, kern, T::LDS_BYTES)) return e;
-  int dev = 0, cus = 0;
-  if (hipError_t e = current_device(dev)) return e;
-  if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) return e;
-  const int tiles_n = n / T::BN;
-  const int64_t tiles_m = (m + T::BM - 1) / T::BM;
-  const int64_t total = tiles_m * tiles_n;
-  int64_t grid = (int64_t)cus * per_cu;
-  grid = grid / 8 * 8;
-  if (grid > total) grid = total;
-  gemm_persistent_kernel<T, RESID><<<(unsigned)grid, T::THREADS, T::LDS_BYTES, stream>>>(
-      a, a_words, as, w, ws, m, n, k / 256, residual, out, (int)tiles_m, tiles_n);
-  return hipGetLastError();
-}
-
-template <class T>
-hipError_t launch_persistent_any(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
-                                 const float* ws, int64_t m, int n, int k, const uint16_t* residual,
-                                 uint16_t* out, int per_cu, hipStream_t stream) {
-  if (residual)
-    return launch_persistent<T, true>(a, a_words, as, w, ws, m, n, k, residual, out, per_cu, stream);
-  return launch_persistent<T, false>(a, a_words, as, w, ws, m, n, k, residual, out, per_cu, stream);
-}
-
-template <class T>
-struct IsHalfStage : std::false_type {};
-template <int A, int B, int C, int D, int E, bool F>
-struct IsHalfStage<DmaHTile<A, B, C, D, E, F>> : std::true_type {};
-
-template <class T, bool RESID>
 hipError_t launch_dma(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
                       const float* ws, int64_t m, int n, int k, const uint16_t* residual,
                       uint16_t* out, hipStream_t stream) {
-  constexpr bool H = IsHalfStage<T>::value;
-  const void* kern;
-  if constexpr (H)
-    kern = reinterpret_cast<const void*>(&gemm_dmah_kernel<T, RESID>);
-  else
-    kern = reinterpret_cast<const void*>(&gemm_dma_kernel<T, RESID>);
+  const void* kern = reinterpret_cast<const void*>(&gemm_dma_kernel<T, RESID>);
   static LaunchCache cache;
   if (hipError_t e = ensure_dynamic_lds(cache, kern, T::LDS_BYTES)) return e;
   const int tiles_n = n / T::BN;
   const int64_t tiles_m = (m + T::BM - 1) / T::BM;
-  const int64_t blocks = tiles_m * tiles_n;
-  if constexpr (H)
-    gemm_dmah_kernel<T, RESID><<<(unsigned)blocks, T::THREADS, T::LDS_BYTES, stream>>>(
-        a, a_words, as, w, ws, m, n, k / 256, residual, out, (int)tiles_m, tiles_n);
-  else
-    gemm_dma_kernel<T, RESID><<<(unsigned)blocks, T::THREADS, T::LDS_BYTES, stream>>>(
-        a, a_words, as, w, ws, m, n, k / 256, residual, out, (int)tiles_m, tiles_n);
+  gemm_dma_kernel<T, RESID><<<(unsigned)(tiles_m * tiles_n), T::THREADS, T::LDS_BYTES, stream>>>(
+      a, a_words, as, w, ws, m, n, k / 256, residual, out, (int)tiles_m, tiles_n);
   return hipGetLastError();
 }
 
@@ -941,52 +650,17 @@ hipError_t launch_dma8_any(const uint32_t* a, int a_words, const float* as, cons
   return launch_dma8<T, false>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
 }
 
-using Dma256x256 = DmaTile<128, 128, 2, 2>;
-using Dma256x128 = DmaTile<128, 64, 2, 2>;
+// G1 tiles: 128x128 on four 64x64 waves (compiler-hinted MFMA/unpack
+// interleave), and 256x256 on eight 128x64 waves with the pinned schedule
+// (one workgroup per tile, or persistent). INT8 uses the eight-wave tile with
+// the compiler's own schedule.
 using Dma128x128 = DmaTile<64, 64, 2, 2>;
-using Dma256x256NoHint = DmaTile<128, 128, 2, 2, kSchedFree>;
-using Dma128x128NoHint = DmaTile<64, 64, 2, 2, kSchedFree>;
 using Dma256x256W8 = DmaTile<128, 64, 2, 4, kSchedFree>;
-using Dma256x256W8b = DmaTile<64, 128, 4, 2, kSchedFree>;
-using Dma256x256W8Hint = DmaTile<128, 64, 2, 4, kSchedHint>;
-using Dma256x256Pin = DmaTile<128, 128, 2, 2, kSchedPin>;
 using Dma256x256W8Pin = DmaTile<128, 64, 2, 4, kSchedPin>;
-using DmaH256x128 = DmaHTile<128, 64, 2, 2, kSchedFree>;
-using DmaH128x256 = DmaHTile<128, 64, 1, 4, kSchedFree>;
-using DmaH256x128Pin = DmaHTile<128, 64, 2, 2, kSchedPin>;
-
-template <class T, bool RESID>
-hipError_t launch_dense(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
-                        const float* ws, int64_t m, int n, int k, const uint16_t* residual,
-                        uint16_t* out, hipStream_t stream) {
-  static LaunchCache cache;
-  const void* kern = reinterpret_cast<const void*>(&gemm_i4_kernel<T, RESID>);
-  if (hipError_t e = ensure_dynamic_lds(cache, kern, T::LDS_BYTES)) return e;
-  const int tiles_n = n / T::BN;
-  const int64_t tiles_m = (m + T::BM - 1) / T::BM;
-  const int64_t blocks = tiles_m * tiles_n;
-  gemm_i4_kernel<T, RESID><<<(unsigned)blocks, 256, T::LDS_BYTES, stream>>>(
-      a, a_words, as, w, ws, m, n, k / 256, residual, out, tiles_n);
-  return hipGetLastError();
-}
-
-template <class T>
-hipError_t launch_dense_any(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
-                            const float* ws, int64_t m, int n, int k, const uint16_t* residual,
-                            uint16_t* out, hipStream_t stream) {
-  if (residual) return launch_dense<T, true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-  return launch_dense<T, false>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-}
-
-using Tile128x128 = GemmTile<128, 128, 64, 64>;
-using Tile256x128 = GemmTile<256, 128, 128, 64>;
-using Tile128x256 = GemmTile<128, 256, 64, 128>;
-using Tile64x128 = GemmTile<64, 128, 32, 64>;
 
 // ---------------------------------------------------------------- experts
 
 constexpr int kExpertBM = 128;
-using ExpertTile = GemmTile<kExpertBM, 128, 64, 64>;
 
 // Per-expert tile list: schedule[0] = tiles, then (expert, first slot) pairs
 // for experts ascending and tiles of kExpertBM slots each. With bm = 16 and
@@ -1015,144 +689,6 @@ __global__ __launch_bounds__(128) void tile_list_kernel(const float* __restrict_
   if (e == 127) list[0] = (OutT)scan[127];
 }
 
-template <class T>
-__global__ __launch_bounds__(256) void expert_i4_kernel(
-    const uint32_t* __restrict__ a, int a_words, const float* __restrict__ as,
-    const uint32_t* __restrict__ w, const float* __restrict__ ws, const float* __restrict__ groups,
-    const int32_t* __restrict__ schedule, int64_t tokens, int topk, int kb, int n, int input_routed,
-    uint16_t* __restrict__ out, int tiles_n) {
-  extern __shared__ __align__(16) char lds[];
-  const int tile = blockIdx.x / tiles_n;
-  if (tile >= schedule[0]) return;
-  const int tn = blockIdx.x - tile * tiles_n;
-  const int e = schedule[1 + 2 * tile];
-  const int row0 = schedule[2 + 2 * tile];
-  const float* list = groups + (int64_t)e * (tokens + 1);
-  const int count = (int)list[0];
-  const int n0 = tn * T::BN;
-  const int tid = threadIdx.x;
-
-  const uint32_t* a_ptr[T::AL];
-  const uint32_t* b_ptr[T::BL];
-#pragma unroll
-  for (int j = 0; j < T::AL; ++j) {
-    const int idx = tid + 256 * j;
-    int slot = row0 + (idx >> 3);
-    slot = slot < count ? slot : row0;
-    const int64_t route = (int64_t)list[1 + slot];
-    const int64_t xr = input_routed ? route : route / topk;
-    a_ptr[j] = a + xr * a_words + (idx & 7) * 4;
-  }
-#pragma unroll
-  for (int j = 0; j < T::BL; ++j) {
-    const int idx = tid + 256 * j;
-    const int64_t nb = ((int64_t)e * n + n0) / 128 + (idx >> 10);
-    b_ptr[j] = w + nb * kb * 4096 + (idx & 1023) * 4;
-  }
-  v4i acc[T::TM][T::TN];
-  gemm_mainloop<T>(a_ptr, b_ptr, kb, lds, acc);
-
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
-  const int g = lane >> 4, lr = lane & 15;
-#pragma unroll
-  for (int i = 0; i < T::TM; ++i) {
-    const int slot = row0 + wm * T::WM + 16 * i + lr;
-    if (slot >= count) continue;
-    const int64_t route = (int64_t)list[1 + slot];
-    const int64_t xr = input_routed ? route : route / topk;
-    const float asv = as[xr];
-#pragma unroll
-    for (int j = 0; j < T::TN; ++j) {
-      const int c = n0 + wn * T::WN + 16 * j + 4 * g;
-      const float4 wsv = *reinterpret_cast<const float4*>(ws + (int64_t)e * n + c);
-      const uint32_t v0 = f32_to_bf16((float)(acc[i][j].x >> 8) * (asv * wsv.x));
-      const uint32_t v1 = f32_to_bf16((float)(acc[i][j].y >> 8) * (asv * wsv.y));
-      const uint32_t v2 = f32_to_bf16((float)(acc[i][j].z >> 8) * (asv * wsv.z));
-      const uint32_t v3 = f32_to_bf16((float)(acc[i][j].w >> 8) * (asv * wsv.w));
-      *reinterpret_cast<uint2*>(out + route * n + c) = make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
-    }
-  }
-}
-
-// E1 on the DMA core: rows gathered through the expert's route list.
-// Slots past the expert's count get an out-of-range offset (2^31 >= the
-// buffer size, checked by the launcher) and read zeros; they are not stored.
-template <class T>
-__global__ __launch_bounds__(T::THREADS) void expert_dma_kernel(
-    const uint32_t* __restrict__ a, int a_words, uint32_t a_bytes, const float* __restrict__ as,
-    const uint32_t* __restrict__ w, const float* __restrict__ ws, const float* __restrict__ groups,
-    const int32_t* __restrict__ schedule, int64_t tokens, int topk, int kb, int n, int input_routed,
-    uint16_t* __restrict__ out, int tiles_n) {
-#if defined(__HIP_DEVICE_COMPILE__)  // buffer-resource builtins exist only in the device pass
-  extern __shared__ __align__(16) char lds[];
-  // Work items are (tile, column block) pairs in expert-major order. Block b
-  // runs on XCD b % 8 (round-robin dispatch); XCD x takes the contiguous item
-  // range [x * C, (x + 1) * C), so the row tiles of one expert and weight
-  // panel run together on one XCD and share the panel in its L2. The grid is
-  // a multiple of 8 and covers 8 * C items.
-  const int64_t items = (int64_t)schedule[0] * tiles_n;
-  const int64_t chunk = (items + 7) / 8;
-  const int64_t local = blockIdx.x / 8;
-  if (local >= chunk) return;
-  const int64_t item = (blockIdx.x % 8) * chunk + local;
-  if (item >= items) return;
-  const int tile = (int)(item / tiles_n);
-  const int tn = (int)(item - (int64_t)tile * tiles_n);
-  const int e = schedule[1 + 2 * tile];
-  const int row0 = schedule[2 + 2 * tile];
-  const float* list = groups + (int64_t)e * (tokens + 1);
-  const int count = (int)list[0];
-  const int n0 = tn * T::BN;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-
-  int voff_a[T::A_INST];
-#pragma unroll
-  for (int ql = 0; ql < T::A_INST; ++ql) {
-    const int slot = row0 + 8 * (wave + T::NW * ql) + (lane >> 3);
-    if (slot < count) {
-      const int64_t route = (int64_t)list[1 + slot];
-      const int64_t xr = input_routed ? route : route / topk;
-      voff_a[ql] = (int)(xr * a_words * 4) + dma_chunk16(wave, lane);
-    } else {
-      voff_a[ql] = (int)0x80000000u;
-    }
-  }
-  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a, a_bytes);
-  const __amdgpu_buffer_rsrc_t b_rsrc =
-      make_rsrc(w + (((int64_t)e * n + n0) / 128) * kb * 4096, (uint32_t)((T::BN / 128) * kb * 16384));
-  v16i acc[T::TM][T::TN];
-  dma_mainloop<T>(a_rsrc, voff_a, 0, b_rsrc, kb, lds, acc);
-
-  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
-  const int h = lane >> 5, lr = lane & 31;
-#pragma unroll
-  for (int i = 0; i < T::TM; ++i) {
-    const int slot = row0 + wm * T::WM + 32 * i + lr;
-    if (slot >= count) continue;
-    const int64_t route = (int64_t)list[1 + slot];
-    const int64_t xr = input_routed ? route : route / topk;
-    const float asv = as[xr];
-#pragma unroll
-    for (int j = 0; j < T::TN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int c = n0 + wn * T::WN + 32 * j + 8 * q + 4 * h;
-        const float4 wsv = *reinterpret_cast<const float4*>(ws + (int64_t)e * n + c);
-        const float y0 = (float)(acc[i][j][4 * q + 0] >> 8) * (asv * wsv.x);
-        const float y1 = (float)(acc[i][j][4 * q + 1] >> 8) * (asv * wsv.y);
-        const float y2 = (float)(acc[i][j][4 * q + 2] >> 8) * (asv * wsv.z);
-        const float y3 = (float)(acc[i][j][4 * q + 3] >> 8) * (asv * wsv.w);
-        *reinterpret_cast<uint2*>(out + route * n + c) = make_uint2(pack_bf16x2(y0, y1), pack_bf16x2(y2, y3));
-      }
-  }
-#endif
-}
-
-using ExpertDmaTile = DmaTile<64, 64, 2, 2>;
-static_assert(ExpertDmaTile::BM == kExpertBM, "expert schedule tile height");
-
 // Grouped expert GEMM on the half-k-step core: 128 expert slots x 256 weight
 // rows per workgroup, four 64 x 128 waves, two workgroups per CU.
 //  GU = false: E1 over 256 output columns of one weight set.
@@ -1160,8 +696,15 @@ static_assert(ExpertDmaTile::BM == kExpertBM, "expert schedule tile height");
 //    rows and the same 128 up rows; each lane holds gate and up of the same
 //    output column, applies E1 to both (bf16), then S1, and writes h.
 // A wave whose 64 slots are all past the expert's count runs the DMA and
-// barrier schedule only. Work items, XCD chunking and the gathered A rows
-// are as in expert_dma_kernel.
+// barrier schedule only.
+// Work items are (schedule tile, column block) pairs in expert-major order.
+// Block b runs on XCD b % 8 (round-robin dispatch); XCD x takes the
+// contiguous item range [x * C, (x + 1) * C), so the row tiles of one expert
+// and weight panel run together on one XCD and share the panel in its L2.
+// The grid is a multiple of 8 and covers 8 * C items. A rows are gathered:
+// each DMA lane's offset is its slot's row (route / topk, or route for routed
+// input); slots past the expert's count get an out-of-range offset (2^31 >=
+// the buffer size, checked by the launcher) and read zeros.
 
 using ExpertHTile = DmaHTile<64, 128, 2, 2, kSchedFree, false>;
 using ExpertGUTile = DmaHTile<64, 128, 2, 2, kSchedFree, true>;
@@ -1688,7 +1231,7 @@ hipError_t launch_expert_skinny(const uint32_t* a, int a_words, int64_t a_bytes,
 
 }  // namespace
 
-int gemm_config_count() { return 23; }
+int gemm_config_count() { return kGemmConfigs; }
 
 hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
@@ -1717,42 +1260,20 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
     // against 18.3, where 96 tiles of 128x128 already cover most CUs).
     const int64_t tiles256 = (m + 255) / 256 * (n / 256);
     if (use_skinny(m, n))
-      config = 22;
+      config = kGemmSkinny;
     else
-      config = (n % 256 == 0 && m >= 1024 && tiles256 >= 192) ? 20 : 6;
+      config = (n % 256 == 0 && m >= 1024 && tiles256 >= 192) ? kGemmPersist256 : kGemmTile128;
   }
-  // Configurations with a 256-wide N tile need n % 256 == 0; the others
-  // (N tile 128) take any n % 128 == 0.
-  const bool wide_n = config == 2 || config == 4 || config == 7 || (config >= 9 && config <= 12) || config == 14 ||
-                      config == 15 || config == 17 || (config >= 19 && config <= 21);
-  // The persistent loop needs at least two k-steps.
-  if (k < 512 && (config == 12 || config == 13 || (config >= 19 && config <= 21)))
-    config = config == 13 ? 6 : config == 20 ? 15 : config == 21 ? 14 : 9;
-  if (wide_n && n % 256 != 0) config = 5;
+  // The 256x256 tiles need n % 256 == 0 (128x128 and skinny take any
+  // n % 128 == 0); the persistent loop needs at least two k-steps.
+  if ((config == kGemmTile256 || config == kGemmPersist256) && n % 256 != 0) config = kGemmTile128;
+  if (config == kGemmPersist256 && k < 512) config = kGemmTile256;
   switch (config) {
-    case 0: return launch_dense_any<Tile128x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 1: return launch_dense_any<Tile256x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 2: return launch_dense_any<Tile128x256>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 3: return launch_dense_any<Tile64x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 4: return launch_dma_any<Dma256x256>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 5: return launch_dma_any<Dma256x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 6: return launch_dma_any<Dma128x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 7: return launch_dma_any<Dma256x256NoHint>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 8: return launch_dma_any<Dma128x128NoHint>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 9: return launch_dma_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 10: return launch_dma_any<Dma256x256W8b>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 11: return launch_dma_any<Dma256x256W8Hint>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 12: return launch_persistent_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, 1, stream);
-    case 13: return launch_persistent_any<Dma128x128>(a, a_words, as, w, ws, m, n, k, residual, out, 2, stream);
-    case 14: return launch_dma_any<Dma256x256Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 15: return launch_dma_any<Dma256x256W8Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 16: return launch_dma_any<DmaH256x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 17: return launch_dma_any<DmaH128x256>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 18: return launch_dma_any<DmaH256x128Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 19: return launch_dma_persist_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 20: return launch_dma_persist_any<Dma256x256W8Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 21: return launch_dma_persist_any<Dma256x256Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-    case 22: return launch_skinny_any(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case kGemmTile128: return launch_dma_any<Dma128x128>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case kGemmTile256: return launch_dma_any<Dma256x256W8Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case kGemmPersist256:
+      return launch_dma_persist_any<Dma256x256W8Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case kGemmSkinny: return launch_skinny_any(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1844,31 +1365,10 @@ hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* as, con
   if (expert_tile_rows(tokens * topk) == kExpertSkinnyBM)
     return launch_expert_skinny<false>(a, a_words, a_bytes, as, w, ws, w, ws, groups, schedule, tokens, topk, k, n,
                                        input_routed, out, stream);
-  if (a_bytes < ((int64_t)1 << 31) && n % 256 == 0)
-    return launch_expert_dmah<ExpertHTile, false>(a, a_words, a_bytes, as, w, ws, w, ws, groups, schedule, tokens,
-                                                  topk, k, n, input_routed, out, stream);
-  if (a_bytes < ((int64_t)1 << 31)) {
-    using T = ExpertDmaTile;
-    static LaunchCache cache;
-    const void* kern = reinterpret_cast<const void*>(&expert_dma_kernel<T>);
-    if (hipError_t e = ensure_dynamic_lds(cache, kern, T::LDS_BYTES)) return e;
-    const int tiles_n = n / T::BN;
-    const int64_t blocks = 8 * ((expert_max_tiles(tokens * topk) * tiles_n + 7) / 8);
-    expert_dma_kernel<T><<<(unsigned)blocks, T::THREADS, T::LDS_BYTES, stream>>>(
-        a, a_words, (uint32_t)a_bytes, as, w, ws, groups, schedule, tokens, topk, k / 256, n, input_routed,
-        out, tiles_n);
-    return hipGetLastError();
-  }
-  // Activation buffers of 2 GiB or more: 64-bit row addressing.
-  using T = ExpertTile;
-  static LaunchCache cache;
-  const void* kern = reinterpret_cast<const void*>(&expert_i4_kernel<T>);
-  if (hipError_t e = ensure_dynamic_lds(cache, kern, T::LDS_BYTES)) return e;
-  const int tiles_n = n / T::BN;
-  const int64_t blocks = expert_max_tiles(tokens * topk) * tiles_n;
-  expert_i4_kernel<T><<<(unsigned)blocks, 256, T::LDS_BYTES, stream>>>(
-      a, a_words, as, w, ws, groups, schedule, tokens, topk, k / 256, n, input_routed, out, tiles_n);
-  return hipGetLastError();
+  // The callers reject activation operands of 2 GiB or more and n % 256 != 0.
+  if (a_bytes >= ((int64_t)1 << 31) || n % 256 != 0) return hipErrorInvalidValue;
+  return launch_expert_dmah<ExpertHTile, false>(a, a_words, a_bytes, as, w, ws, w, ws, groups, schedule, tokens,
+                                                topk, k, n, input_routed, out, stream);
 }
 
 }  // namespace clef

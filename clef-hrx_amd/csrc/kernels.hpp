@@ -37,6 +37,10 @@ hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const
                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream);
 // Records msg as clef_last_error() of this thread; returns CLEF_EINVAL.
 int set_last_error(const char* msg);
+// G1 tile configurations (clef_i4_gemm_config): 128x128 tiles, 256x256
+// tiles with one workgroup per tile, 256x256 tiles walked by a persistent
+// grid, and the K-split small-M kernel.
+enum GemmConfig { kGemmTile128 = 0, kGemmTile256 = 1, kGemmPersist256 = 2, kGemmSkinny = 3, kGemmConfigs = 4 };
 int gemm_config_count();
 
 hipError_t launch_router_gate(const uint16_t* x, const uint16_t* w, int64_t tokens, int hidden, int experts,

@@ -53,6 +53,13 @@ const char* clef_last_error(void);
 /* ABI version of this header (major * 100 + minor). */
 int clef_abi_version(void);
 
+/* Identity of the sources the library was built from: the first 16 hex
+ * digits of the SHA-256 of clef-hrx_amd/csrc/* (sorted), this header and the
+ * library's Makefile. Has no counterpart in the reference (whose kernels are
+ * compiled at run time); lets a caller detect a library that is stale against
+ * its source tree. */
+const char* clef_build_id(void);
+
 /* ------------------------------------------------------------------ Q1/Q2 */
 
 /* Activation/weight stride rule: width + (width % 1024 == 0 ? 512/bits : 0).
@@ -174,7 +181,10 @@ int clef_i8_gemm(const uint32_t* a, int32_t k_stride, const float* a_scales, con
                  uint16_t* out, clef_stream_t stream);
 
 /* Same, with an explicit tile configuration (0..clef_i4_gemm_configs()-1;
- * -1 = automatic). For tuning and tests. */
+ * -1 = automatic): 0 = 128x128 tiles, 1 = 256x256 tiles (one workgroup per
+ * tile), 2 = 256x256 tiles on a persistent grid, 3 = the K-split small-M
+ * kernel. Configurations 1 and 2 fall back to 0 when n % 256 != 0, and 2 to 1
+ * when k < 512. For tuning and tests. */
 int clef_i4_gemm_config(const uint32_t* a, int32_t k_stride, const float* a_scales,
                         const uint32_t* w_tiled, const float* w_scales, int64_t m, int32_t n,
                         int32_t k, const uint16_t* residual, uint16_t* out, int32_t config,
@@ -209,9 +219,10 @@ size_t clef_moe_group_workspace_bytes(int64_t tokens);
  * omni_group_routes_ordered (src/omni.rs:192-245) and
  * kernels/omni_group_routes.loom, omni_group_routes_ordered.loom. The
  * reference caps tokens at 2048 per chunk (src/omni.rs:11); this library
- * accepts up to 1048576 tokens in one call (every stage is row-local).
- * Preconditions: 1 <= tokens <= 1048576, 1 <= topk <= 128 ->
- * "unsupported Omni route grouping shape". */
+ * accepts up to 1048576 tokens in one call (every stage is row-local), while
+ * the f32-encoded route ordinals t*topk+r stay exact (below 2^24).
+ * Preconditions: 1 <= tokens <= 1048576, 1 <= topk <= 128, tokens * topk <=
+ * 16777216 -> "unsupported Omni route grouping shape". */
 int clef_moe_group_routes(const float* routes, int64_t tokens, int32_t topk, float* groups,
                           float* order, void* workspace, size_t workspace_bytes,
                           clef_stream_t stream);
@@ -234,9 +245,12 @@ size_t clef_moe_expert_workspace_bytes(int64_t tokens, int32_t topk);
  * Replaces Engine::omni_expert_impl / omni_expert_inputs
  * (src/omni.rs:289-534) and kernels/omni_expert_i4.loom,
  * omni_expert_i4_k128_down.loom, omni_expert_i4_compact.loom.
- * Preconditions: k % 256 == 0 && n % 256 == 0 && k, n >= 256 && stride >= k
- * && stride % 8 == 0 -> "unsupported Omni expert tile shape"; tokens >= 1,
- * 1 <= topk <= 128 -> "invalid grouped expert routes". */
+ * Preconditions: 1 <= tokens <= 1048576, 1 <= topk <= 128 -> "invalid
+ * grouped expert routes"; tokens * topk <= 16777216 -> "unsupported Omni
+ * route grouping shape"; k % 256 == 0 && n % 256 == 0 && k, n >= 256 &&
+ * stride >= k && stride % 32 == 0 -> "unsupported Omni expert tile shape";
+ * the packed codes of `a` (rows * stride / 2 bytes) below 2 GiB -> "expert
+ * activation operand of 2 GiB or more ...". */
 int clef_moe_expert_i4(const uint32_t* a, int32_t stride, const float* a_scales,
                        const uint32_t* w_tiled, const float* w_scales, const float* groups,
                        int64_t tokens, int32_t topk, int32_t k, int32_t n, int32_t input_routed,
@@ -251,10 +265,12 @@ int clef_moe_expert_i4(const uint32_t* a, int32_t stride, const float* a_scales,
  * followed by clef_swiglu. Replaces Engine::omni_gate_up (src/omni.rs:300-372)
  * and benches/kernels/omni_gate_up_i4.loom. Workspace: as clef_moe_expert_i4.
  * Preconditions: 1 <= tokens <= 1048576, 1 <= topk <= 128 -> "fused gate/up
- * requires regular grouped routes"; k % 256 == 0, n % 128 == 0 (the tiled
- * weight layout's 128-row panels; the reference accepts n % 64 == 0),
- * stride >= k, stride % 32 == 0 and tokens * stride / 2 < 2 GiB ->
- * "incompatible fused expert weights". */
+ * requires regular grouped routes"; tokens * topk <= 16777216 ->
+ * "unsupported Omni route grouping shape"; k % 256 == 0, n % 128 == 0 (the
+ * tiled weight layout's 128-row panels; the reference accepts n % 64 == 0),
+ * stride >= k, stride % 32 == 0 -> "incompatible fused expert weights";
+ * tokens * stride / 2 < 2 GiB -> "expert activation operand of 2 GiB or
+ * more ...". */
 int clef_moe_expert_gate_up_i4(const uint32_t* a, int32_t stride, const float* a_scales,
                                const uint32_t* gate_w, const float* gate_s, const uint32_t* up_w,
                                const float* up_s, const float* groups, int64_t tokens, int32_t topk,
@@ -288,7 +304,10 @@ size_t clef_moe_layer_workspace_bytes(int64_t tokens, int32_t hidden, int32_t in
  * MoE half of omni::forward_layers_cached (src/omni.rs:760-857) without the
  * bf16 router-gate projection (logits are an input) and without the residual
  * add. Preconditions: experts == 128 -> "Omni MoE requires 128 experts";
- * hidden, inter % 256 == 0; then those of the stages. */
+ * hidden, inter % 256 == 0; then those of the stages, including the 2 GiB
+ * bound on the packed x (tokens rows) and packed h (tokens * topk rows): the
+ * reference runs at most 2048 tokens per call (src/omni.rs:11), and callers
+ * with more tokens than the bound allows split them into chunks. */
 int clef_moe_layer(const uint16_t* x, const void* logits, int32_t logits_dtype, int64_t tokens,
                    int32_t hidden, int32_t inter, int32_t experts, int32_t topk,
                    const uint32_t* gate_w, const float* gate_s, const uint32_t* up_w,

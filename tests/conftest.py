@@ -13,11 +13,19 @@ for p in (ROOT, PKG):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
-    # Build only what is missing; a built tree is used as is.
-    if not os.path.exists(os.path.join(PKG, "lib", "libclef_i4.so")):
-        subprocess.run(["make", "-s", "-C", PKG], check=True)
-    if not os.path.exists(os.path.join(ROOT, "oracle", "_build", "libclef_oracle.so")):
-        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
+    # The library must match the sources: its embedded build identity is
+    # compared with the tree's hash and a missing or stale library is rebuilt
+    # from scratch (timestamps do not survive every copy of the tree). The
+    # oracle's incremental make is a no-op when it is up to date.
+    import build_id
+
+    problem = build_id.stale()
+    if problem:
+        print(f"conftest: {problem}; rebuilding", flush=True)
+        subprocess.run(["make", "-s", "-B", "-j", "16", "-C", PKG], check=True)
+        problem = build_id.stale()
+        assert problem is None, problem
+    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
 
 
 def pytest_collection_modifyitems(config, items):

@@ -100,6 +100,76 @@ def test_group_rejects():
     assert rc == -1 and msg == "workspace too small"
 
 
+def test_build_identity_matches_sources():
+    """The library's embedded build identity is the hash of the sources it was
+    built from; the loader refuses a stale library."""
+    import build_id
+
+    assert build_id.stale() is None
+    assert clef_i4.lib().clef_build_id().decode() == build_id.source_id() == build_id.library_id()
+
+
+# Route ordinals t * topk + r are f32 in the reference's tables: exact below
+# 2^24 only, so every entry point that reads or writes them caps tokens * topk.
+@pytest.mark.parametrize("tokens,topk", [(1048576, 32), (1048576, 17), (262144, 65), (524289, 32)])
+def test_route_ordinals_capped_below_2_pow_24(tokens, topk):
+    msg = "unsupported Omni route grouping shape"
+    rc, got = call("clef_moe_group_routes", FAKE, tokens, topk, FAKE, None, FAKE, 1 << 40, None)
+    assert rc == -1 and got == msg
+    rc, got = call("clef_moe_expert_i4", FAKE, 256, FAKE, FAKE, FAKE, FAKE, tokens, topk, 256, 256, 0, FAKE, FAKE,
+                   1 << 40, None)
+    assert rc == -1 and got == msg
+    rc, got = call("clef_moe_expert_gate_up_i4", FAKE, 256, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, tokens, topk, 256,
+                   256, FAKE, FAKE, 1 << 40, None)
+    assert rc == -1 and got == msg
+    rc, got = call("clef_moe_layer", FAKE, FAKE, 0, tokens, 256, 256, 128, topk, FAKE, FAKE, FAKE, FAKE, FAKE,
+                   FAKE, None, FAKE, FAKE, 1 << 40, None)
+    assert rc == -1 and got == msg
+
+
+def test_route_ordinal_cap_admits_2_pow_24():
+    """tokens * topk == 2^24 passes the grouping checks (fails later, on the
+    workspace)."""
+    rc, got = call("clef_moe_group_routes", FAKE, 1048576, 16, FAKE, None, FAKE, 16, None)
+    assert rc == -1 and got == "workspace too small"
+
+
+@pytest.mark.parametrize("tokens,topk,stride,routed", [(1048576, 8, 16384, 0), (65536, 16, 16384, 1),
+                                                       (1048576, 2, 4096, 0)])
+def test_expert_operand_below_2gib(tokens, topk, stride, routed):
+    """Gathered activation rows are addressed by 32-bit buffer offsets: the
+    packed operand (rows * stride / 2 bytes) must stay below 2 GiB."""
+    rows = tokens * topk if routed else tokens
+    big = rows * stride // 2 >= 1 << 31
+    rc, got = call("clef_moe_expert_i4", FAKE, stride, FAKE, FAKE, FAKE, FAKE, tokens, topk, 256, 256, routed, FAKE,
+                   FAKE, 16, None)
+    assert rc == -1 and got == ("expert activation operand of 2 GiB or more (split the tokens into chunks, as the "
+                                "reference does)" if big else "workspace too small")
+    if not routed:
+        rc, got = call("clef_moe_expert_gate_up_i4", FAKE, stride, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, tokens, topk,
+                       256, 256, FAKE, FAKE, 16, None)
+        assert rc == -1 and got.startswith("expert activation operand" if big else "workspace too small")
+
+
+def test_moe_layer_rejects_operands_of_2gib():
+    # x packed: 131072 rows of (32768 + 128) / 2 bytes > 2 GiB
+    rc, got = call("clef_moe_layer", FAKE, FAKE, 0, 131072, 32768, 256, 128, 8, FAKE, FAKE, FAKE, FAKE, FAKE,
+                   FAKE, None, FAKE, FAKE, 1 << 40, None)
+    assert rc == -1 and got.startswith("expert activation operand of 2 GiB")
+    # h packed: 131072 * 8 routed rows of (8192 + 128) / 2 bytes > 2 GiB
+    rc, got = call("clef_moe_layer", FAKE, FAKE, 0, 131072, 256, 8192, 128, 8, FAKE, FAKE, FAKE, FAKE, FAKE,
+                   FAKE, None, FAKE, FAKE, 1 << 40, None)
+    assert rc == -1 and got.startswith("expert activation operand of 2 GiB")
+
+
+def test_expert_stride_multiple_of_32():
+    """include/clef_i4.h: stride % 32 == 0 for the grouped expert GEMM."""
+    for stride, ok in [(272, False), (288, True)]:
+        rc, got = call("clef_moe_expert_i4", FAKE, stride, FAKE, FAKE, FAKE, FAKE, 4, 8, 256, 256, 0, FAKE, FAKE,
+                       16, None)
+        assert rc == -1 and got == ("workspace too small" if ok else "unsupported Omni expert tile shape")
+
+
 @pytest.mark.parametrize("k,n,stride", [(300, 256, 320), (256, 128, 256), (256, 256, 200)])
 def test_expert_rejects(k, n, stride):
     rc, msg = call("clef_moe_expert_i4", FAKE, stride, FAKE, FAKE, FAKE, FAKE, 4, 8, k, n, 0, FAKE, FAKE,

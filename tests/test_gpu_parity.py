@@ -125,6 +125,35 @@ def test_prepare_swiglu_matches_oracle(width):
     assert_same_u32(u32_host(got.storage), want, f"prepare_swiglu width={width}")
 
 
+@pytest.mark.parametrize("width,bits,row_counts", __import__("ref_inputs").fused_swiglu_cases())
+def test_prepare_swiglu_reference_inputs(width, bits, row_counts):
+    """fused_swiglu_packing_matches_reference (src/quantized.rs:1189-1266) on
+    its own inputs: gate rows 0, NaN at column 259, +inf at 515, bf16::MAX,
+    the bf16 denormal 0x0001, +-80 and the formula (every out-of-table SiLU
+    case of the fused kernel), the up formula, the row-offset slices (gate
+    from row 1, up from row 2) and stride width + 512 / bits. The fused
+    producer equals the oracle, equals clef_swiglu followed by clef_i4_prepare
+    on the device, and is the same on a second run, codes and scales bit for
+    bit."""
+    import ref_inputs
+
+    stride = width + 512 // bits
+    words = width // (32 // bits)
+    for rows in row_counts:
+        print(f"prepare_swiglu width={width} bits={bits} rows={rows}", flush=True)
+        gate, up = ref_inputs.swiglu_gate_up(width, rows)
+        want_c, want_s, _ = oracle.prepare_swiglu(gate, up, stride, bits)
+        g_dev, u_dev = to_dev_bf16(gate), to_dev_bf16(up)
+        fused = clef_i4.prepare_swiglu(g_dev, u_dev, bits=bits, stride=stride)
+        again = clef_i4.prepare_swiglu(g_dev, u_dev, bits=bits, stride=stride)
+        split = clef_i4.prepare(clef_i4.swiglu(g_dev, u_dev), bits=bits, stride=stride)
+        for what, got in (("fused", fused), ("fused again", again), ("swiglu then prepare", split)):
+            codes = u32_host(got.codes).reshape(rows, -1)[:, :words]
+            assert_same_u32(codes, want_c[:, :words], f"{what} codes width={width} bits={bits} rows={rows}")
+            assert_same_u32(got.scales.cpu().numpy().view(np.uint32), want_s.view(np.uint32),
+                            f"{what} scales width={width} bits={bits} rows={rows}")
+
+
 @pytest.mark.parametrize("rows,cols", [(128, 256), (256, 2048), (384, 768)])
 def test_retile_matches_block_formula(rows, cols):
     """retiled_codes_match_block_formula (src/quantized.rs:1371-1407)."""
@@ -588,3 +617,42 @@ def test_moe_layer_matches_oracle(tokens, hidden, inter):
     assert_same_u16(bf16_host(got), want, f"moe layer tokens={tokens}")
     again = layer(to_dev_bf16(x), to_dev_bf16(logits))
     assert_same_u16(bf16_host(again), want, "moe layer replay")
+
+
+def test_moe_layer_closed_form():
+    """The MoE block on constant rows (every code +-7, silu(g) = g for the
+    gates >= 17 these inputs give) against the closed form of
+    test_oracle.moe_closed_form, and against the oracle, bit for bit; the
+    device routes are the routes the closed form is evaluated on."""
+    from test_oracle import closed_form_case, moe_closed_form
+
+    t, d, inter, topk = 300, 512, 256, 8  # 2400 routed rows: the 128-slot expert tiles
+    c, x, logits, (gate, up, down), (wg, wu, wd) = closed_form_case(11, t, d, inter, topk)
+    dev = [clef_i4.load_quantized_weight(to_dev_bf16(w)) for w in (gate, up, down)]
+    layer = clef_i4.MoeLayer(*dev)
+    routes = torch.empty((t, 2 * topk), dtype=torch.float32, device=DEV)
+    got = bf16_host(layer(to_dev_bf16(x), to_dev_bf16(logits), routes_out=routes))
+    want, gates = moe_closed_form(c, routes.cpu().numpy(), wg, wu, wd, d, inter, topk)
+    assert np.all(gates >= 17.0)
+    assert np.array_equal(F(got), want)
+    small = bf16_host(layer(to_dev_bf16(x[:40]), to_dev_bf16(logits[:40])))  # 320 rows: 32-slot tiles
+    assert np.array_equal(small, got[:40])
+
+
+def test_c1_linear_full_output():
+    """The single INT4 linear of the reference's CPU path at its exact shape,
+    M512 K2048 N2048 (x ~ N(0, 1), w ~ N(0, 0.02), seed 1001): the whole
+    [512][2048] output of the default path (quantize + projection) and of
+    every tile configuration equals the oracle, bit for bit."""
+    m, k, n = 512, 2048, 2048
+    rng = np.random.default_rng(1001)
+    x, w, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
+    want = oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k)
+    qw = clef_i4.load_quantized_weight(to_dev_bf16(w))
+    assert_same_u32(u32_host(qw.codes), w_tiled, "c1 packed weight")
+    got = clef_i4.project_quantized(to_dev_bf16(x), qw)
+    assert_same_u16(bf16_host(got), want, "c1 default path")
+    a = dev_prepared(x, stride)
+    for cfg in range(clef_i4.gemm_configs()):
+        got = clef_i4.project_prepared(a, qw, config=cfg)
+        assert_same_u16(bf16_host(got), want, f"c1 config={cfg}")

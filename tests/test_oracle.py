@@ -583,3 +583,166 @@ def test_prepare_attention_gate_closed_forms(width):
         want = oracle.prepare(expect, stride)
         assert np.array_equal(got[0][:, : width // 8], want[0][:, : width // 8]), gate
         assert np.array_equal(got[1].view(np.uint32), want[1].view(np.uint32)), gate
+
+
+# ---------------------------------------------------------------- fused SwiGLU quantizer
+
+@pytest.mark.parametrize("width,bits,row_counts", __import__("ref_inputs").fused_swiglu_cases())
+def test_prepare_swiglu_is_swiglu_then_prepare(width, bits, row_counts):
+    """fused_swiglu_packing_matches_reference (src/quantized.rs:1189-1266): on
+    the reference test's gate rows (0, NaN at 259, +inf at 515, bf16::MAX, the
+    bf16 denormal, +-80, the formula) and up rows, with its row-offset slices
+    and stride width + 512 / bits, the fused producer equals S1 materialized as
+    bf16 and then Q1, codes and scales bit for bit. orc_swiglu and orc_prepare
+    are pinned on their own (every bf16 gate against float64; the reference
+    test oracle of Q1)."""
+    import ref_inputs
+
+    stride = width + 512 // bits
+    words = width // (32 // bits)
+    for rows in row_counts:
+        gate, up = ref_inputs.swiglu_gate_up(width, rows)
+        fc, fs, _ = oracle.prepare_swiglu(gate, up, stride, bits)
+        uc, us, _ = oracle.prepare(oracle.swiglu(gate, up), stride, bits)
+        assert np.array_equal(fc[:, :words], uc[:, :words]), (width, bits, rows)
+        assert np.array_equal(fs.view(np.uint32), us.view(np.uint32)), (width, bits, rows)
+
+
+def test_swiglu_on_reference_gate_classes():
+    """S1 on the special gate rows of the fused test, against what the
+    arithmetic fixes: silu(0) = 0, NaN stays NaN, silu(+inf) = +inf,
+    silu(bf16::MAX) = bf16::MAX (exp underflows), silu(+-80) = 80 and a
+    negative value of magnitude 80 * e^-80, silu(denormal 0x0001) = bf16(g / 2)
+    = 0 (ties to even)."""
+    import ref_inputs
+
+    gate, up = ref_inputs.swiglu_gate_up(768, 7)
+    h = F(oracle.swiglu(gate, up)).astype(np.float64)
+    u = F(up).astype(np.float64)
+    # slice row r is buffer row r + 1: classes 1, 2, 3, 4, 5, 6 (formula), 0
+    assert np.isnan(h[0, 259])
+    assert np.isinf(h[1, 515]) and np.sign(h[1, 515]) == np.sign(u[1, 515]) or u[1, 515] == 0
+    big = F(np.array([ref_inputs.BF16_MAX], np.uint16)).astype(np.float64)[0]
+    want_max = F(BF((big * u[2]).astype(np.float32))).astype(np.float64)  # bf16(MAX * u), may overflow
+    fin = np.isfinite(want_max)
+    assert np.array_equal(h[2][fin], want_max[fin])
+    assert np.all(np.isinf(h[2][~fin]))
+    assert np.all(h[3] == 0.0)
+    even = np.arange(768) % 2 == 0
+    assert np.array_equal(h[4][~even], F(BF((80.0 * u[4][~even]).astype(np.float32))))
+    # silu(-80) = -80 e^-80 / (1 + e^-80): two bf16 roundings of half a step
+    want_neg = -80.0 * math.exp(-80.0) * u[4][even]
+    assert np.all(np.abs(h[4][even] - want_neg) <= np.abs(want_neg) * 2.0 ** -7)
+    assert np.all(h[6] == 0.0)
+
+
+# ---------------------------------------------------------------- MoE block
+
+def _moe_inputs(rng, t, d, inter):
+    x = BF(rng.standard_normal((t, d)).astype(np.float32))
+    logits = BF(rng.standard_normal((t, 128)).astype(np.float32))
+    gate = oracle.pack_weight(BF((rng.standard_normal((128 * inter, d)) * 0.02).astype(np.float32)))
+    up = oracle.pack_weight(BF((rng.standard_normal((128 * inter, d)) * 0.02).astype(np.float32)))
+    down = oracle.pack_weight(BF((rng.standard_normal((128 * d, inter)) * 0.02).astype(np.float32)))
+    return x, logits, gate, up, down
+
+
+@pytest.mark.parametrize("t,d,inter,topk", [(1, 512, 256, 8), (37, 512, 256, 8), (40, 1024, 256, 8),
+                                            (23, 256, 512, 4)])
+def test_moe_layer_is_stage_composition(t, d, inter, topk):
+    """The MoE block of forward_layers_cached (src/omni.rs:762-857) with the
+    fast defaults: R1 -> ordered R2 -> Q1(x) shared by gate and up -> E1 gate,
+    E1 up -> S1 -> Q1 of each routed h row -> E1 down on routed input ->
+    ordered C1. orc_moe_layer equals this recipe built from the separately
+    pinned stage functions, bit for bit."""
+    rng = np.random.default_rng(t * 1000 + d + inter + topk)
+    x, logits, gate, up, down = _moe_inputs(rng, t, d, inter)
+    want, routes_want = oracle.moe_layer(x, logits, gate, up, down, topk)
+    routes = oracle.route(logits, topk)
+    assert np.array_equal(routes, routes_want)
+    groups, order = oracle.group_routes(routes, topk)
+    sx, sh = oracle.activation_stride(d), oracle.activation_stride(inter)
+    ax, axs, _ = oracle.prepare(x, sx)
+    g = oracle.expert_i4(ax, axs, gate[0], gate[1], groups, t, topk, d, inter, False)
+    u = oracle.expert_i4(ax, axs, up[0], up[1], groups, t, topk, d, inter, False)
+    h = oracle.swiglu(g, u)
+    ah, ahs, _ = oracle.prepare(h, sh)
+    values = oracle.expert_i4(ah, ahs, down[0], down[1], groups, t, topk, inter, d, True)
+    got = oracle.combine(values, routes, order, topk)
+    assert np.array_equal(got, want)
+
+
+def _bf16_rne(v: np.ndarray) -> np.ndarray:
+    """float32 -> bf16-rounded float32 (finite values), written out here so
+    the closed form below uses none of the oracle's arithmetic."""
+    u = np.ascontiguousarray(v, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)
+
+
+def moe_closed_form(c, routes, wg, wu, wd, d, inter, topk):
+    """MoE output when every row of x and every weight row of an expert is
+    constant. A constant row v rotates to 16 v in every position (each radix-4
+    stage doubles it), so its row maximum is 16|v|, its scale RN(|v| / 7) and
+    every code 7 sign(v). Then every E1 dot over K is 49 K sign(a) sign(w),
+    gate and up are constant along their rows, and with gate >= 17
+    bf16(silu(g)) = g exactly (1 + e^-17 rounds to 1 in f32), so h = bf16(g u)
+    is constant too and Q1 of h follows the same rule. Returns float32
+    [T][d] (constant along each row) and the gate values (for the >= 17
+    check)."""
+    f = np.float32
+    t_n = len(c)
+    out = np.zeros(t_n, np.float32)
+    gates = []
+    for t in range(t_n):
+        a_s = f(abs(c[t])) / f(7.0)
+        sel = sorted((int(routes[t, r]), f(routes[t, topk + r])) for r in range(topk))
+        acc = f(0.0)
+        for e, p in sel:
+            def e1(w_const, k, a_scale, a_sign):
+                w_s = f(abs(w_const)) / f(7.0)
+                dot = f(49 * k * a_sign * np.sign(w_const))
+                return _bf16_rne(np.array([dot * (a_scale * w_s)], np.float32))[0]
+            g = e1(wg[e], d, a_s, np.sign(c[t]))
+            u = e1(wu[e], d, a_s, np.sign(c[t]))
+            gates.append(g)
+            h = _bf16_rne(np.array([g * u], np.float32))[0]  # bf16(bf16(silu(g)) u) with silu(g) = g
+            h_s = f(abs(h)) / f(7.0)
+            v = e1(wd[e], inter, h_s, np.sign(h))
+            y = _bf16_rne(np.array([v * p], np.float32))[0]
+            acc = _bf16_rne(np.array([acc + y], np.float32))[0]
+        out[t] = acc
+    return np.repeat(out[:, None], d, axis=1), np.array(gates)
+
+
+def closed_form_case(seed, t, d, inter, topk=8):
+    """Inputs of moe_closed_form: x row t = c_t > 0, expert e's gate rows
+    (e % 8 + 3) / 32, up rows +-((e % 5) + 1) / 16, down rows
+    +-((e % 3) + 1) / 64, logits N(0, 1)."""
+    rng = np.random.default_rng(seed)
+    c = F(BF((0.5 + 1.5 * rng.random(t)).astype(np.float32)))
+    x = BF(np.repeat(c[:, None], d, axis=1).astype(np.float32))
+    logits = BF(rng.standard_normal((t, 128)).astype(np.float32))
+    e = np.arange(128)
+    wg = ((e % 8 + 3) / 32.0).astype(np.float32)
+    wu = (np.where(e % 2 == 0, 1.0, -1.0) * ((e % 5) + 1) / 16.0).astype(np.float32)
+    wd = (np.where(e % 3 == 0, -1.0, 1.0) * ((e % 3) + 1) / 64.0).astype(np.float32)
+    gate = BF(np.repeat(np.repeat(wg, inter)[:, None], d, axis=1))
+    up = BF(np.repeat(np.repeat(wu, inter)[:, None], d, axis=1))
+    down = BF(np.repeat(np.repeat(wd, d)[:, None], inter, axis=1))
+    return c, x, logits, (gate, up, down), (wg, wu, wd)
+
+
+def test_moe_layer_closed_form():
+    """orc_moe_layer against the closed form of moe_closed_form (the routes,
+    pinned by the stable-sort test, are its only input from the oracle)."""
+    t, d, inter, topk = 24, 512, 256, 8
+    c, x, logits, (gate, up, down), (wg, wu, wd) = closed_form_case(7, t, d, inter, topk)
+    packed = [oracle.pack_weight(w) for w in (gate, up, down)]
+    # every code of every packed row is +-7: 0x77777777 or 0x99999999 words
+    for codes, _ in packed:
+        assert np.all((codes == 0x77777777) | (codes == 0x99999999))
+    got, routes = oracle.moe_layer(x, logits, *packed, topk=topk)
+    want, gates = moe_closed_form(c, routes, wg, wu, wd, d, inter, topk)
+    assert np.all(gates >= 17.0)
+    assert np.array_equal(F(got), want)
