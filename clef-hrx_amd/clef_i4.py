@@ -66,6 +66,8 @@ SIGNATURES = {
     "clef_moe_layer_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
     "clef_moe_layer": (ctypes.c_int, [_P, _P, _I32, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P,
                                       _P, _P, _P, _SZ, _P]),
+    "clef_moe_layer_static": (ctypes.c_int, [_P, _P, _I32, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P,
+                                             _P, _P, _P]),
 }
 
 _lib = None

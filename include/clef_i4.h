@@ -54,8 +54,8 @@ const char* clef_last_error(void);
 int clef_abi_version(void);
 
 /* Identity of the sources the library was built from: the first 16 hex
- * digits of the SHA-256 of clef-hrx_amd/csrc/* (sorted), this header and the
- * library's Makefile. Has no counterpart in the reference (whose kernels are
+ * digits of the SHA-256 of the files of clef-hrx_amd/csrc (sorted by name),
+ * this header and the library's Makefile. Has no counterpart in the reference (whose kernels are
  * compiled at run time); lets a caller detect a library that is stale against
  * its source tree. */
 const char* clef_build_id(void);
@@ -314,6 +314,32 @@ int clef_moe_layer(const uint16_t* x, const void* logits, int32_t logits_dtype, 
                    const float* up_s, const uint32_t* down_w, const float* down_s,
                    float* routes_out, uint16_t* out, void* workspace, size_t workspace_bytes,
                    clef_stream_t stream);
+
+/* Bytes of the static scratch of clef_moe_layer_static: 32 MiB per device. */
+#define CLEF_MOE_STATIC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* clef_moe_layer without a workspace argument: allocates nothing (no
+ * hipMalloc, hipFree or allocating library call) and takes its intermediates
+ * from a static device array of CLEF_MOE_STATIC_SCRATCH_BYTES, one per device,
+ * which the library holds from the first call on a device until the process
+ * ends. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same preconditions and results as
+ * clef_moe_layer, plus clef_moe_layer_workspace_bytes(tokens, hidden, inter,
+ * topk) <= CLEF_MOE_STATIC_SCRATCH_BYTES (about 650 tokens at hidden 2048,
+ * inter 768, top-8) -> "MoE layer needs N bytes of scratch; ...". Nothing
+ * in the scratch needs to start at zero (every intermediate is written before
+ * it is read). Every call on one device shares that device's scratch, and it
+ * keeps the last call's contents: calls that overlap on one device (on
+ * different streams, or from different host threads) race and must be
+ * ordered by the caller. The first call on a device looks up the scratch's
+ * device address with that device current, so call it with the device of
+ * `stream` current. */
+int clef_moe_layer_static(const uint16_t* x, const void* logits, int32_t logits_dtype, int64_t tokens,
+                          int32_t hidden, int32_t inter, int32_t experts, int32_t topk,
+                          const uint32_t* gate_w, const float* gate_s, const uint32_t* up_w,
+                          const float* up_s, const uint32_t* down_w, const float* down_s,
+                          float* routes_out, uint16_t* out, clef_stream_t stream);
 
 /* Router gate projection: logits[t][e] = bf16(sum_k x[t][k] * gate_w[e][k])
  * with f32 accumulation (bf16 MFMA), x bf16 [tokens][hidden], gate_w bf16

@@ -316,3 +316,17 @@ def test_i8_gemm_rejects(m, n, k, ks):
 def test_router_logits_rejects(tokens, hidden, experts):
     rc, msg = call("clef_moe_router_logits", FAKE, FAKE, tokens, hidden, experts, FAKE, None)
     assert rc == -1 and msg == "linear shape/dtype mismatch"
+
+
+def test_moe_layer_static_rejects_beyond_scratch():
+    """clef_moe_layer_static allocates nothing: shapes whose intermediates
+    exceed its 32 MiB static scratch are rejected before any device work."""
+    need = clef_i4.lib().clef_moe_layer_workspace_bytes(4096, 2048, 768, 8)
+    assert need > 32 << 20
+    rc, msg = call("clef_moe_layer_static", FAKE, FAKE, 0, 4096, 2048, 768, 128, 8, FAKE, FAKE, FAKE, FAKE, FAKE,
+                   FAKE, None, FAKE, None)
+    assert rc == -1 and msg.startswith(f"MoE layer needs {need} bytes of scratch; the static scratch holds "
+                                       f"{32 << 20}")
+    rc, msg = call("clef_moe_layer_static", FAKE, FAKE, 0, 16, 2048, 768, 64, 8, FAKE, FAKE, FAKE, FAKE, FAKE,
+                   FAKE, None, FAKE, None)
+    assert rc == -1 and msg == "Omni MoE requires 128 experts"
