@@ -43,6 +43,10 @@ HBM_PEAK_GBS = 8000.0
 # the reading for a plain 512 MiB copy (x2.000 fetch, x1.000 write); the runs
 # and raw readings are in profiles/int4_gemm_m4096_k4096_n12288.txt.
 GEMM_TRAFFIC_BYTES = 257.16e6
+# HBM bytes moved per MoE layer call at 4096 tokens (the same two counter
+# passes over `bench.py --only moe`, summed over the layer's kernels); None
+# until measured for the current kernels.
+MOE_TRAFFIC_BYTES = None
 
 
 def parse():
@@ -176,7 +180,7 @@ def moe_skewed_leg(args):
     down = clef_i4.load_quantized_weight(bf16_randn((128 * d, inter), 0.02, 1005 * 16 + 4))
     layer = clef_i4.MoeLayer(gate, up, down)
     out = torch.empty((t, d), dtype=torch.bfloat16, device="cuda")
-    ms = timed(lambda: layer(x, logits, out=out), max(1, args.steps // 20), max(1, args.warmup // 60))
+    ms = timed(lambda: layer(x, logits, out=out), args.steps, max(1, args.warmup // 20))
     ops = 8.0 * t * 2 * (2 * inter * d + d * inter)
     return {"tokens": t, "ms": ms, "tokens_per_s": t / ms * 1e3, "tops": ops / ms / 1e9}
 
@@ -226,7 +230,7 @@ def attention_leg(args):
         clef_i4.project_prepared(ax, wv, out=v)
         clef_i4.project_prepared(ax, wo, residual=res, out=o)
 
-    ms = timed(step, max(1, args.steps // 4), max(1, args.warmup // 4))
+    ms = timed(step, args.steps, max(1, args.warmup // 4))
     ops = 2.0 * m * d * (d + kv + kv + d)
     return {"ms": ms, "tops": ops / ms / 1e9}
 
@@ -243,7 +247,7 @@ def i8_leg(args):
     qw = clef_i4.load_quantized_weight(w, bits=8)
     a = clef_i4.prepare(x, bits=8)
     out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-    ms = timed(lambda: clef_i4.project_prepared(a, qw, out=out), max(1, args.steps // 4), args.warmup // 4)
+    ms = timed(lambda: clef_i4.project_prepared(a, qw, out=out), args.steps, max(1, args.warmup // 4))
     return {"ms": ms, "tops": 2.0 * m * n * k / ms / 1e9}
 
 
@@ -273,7 +277,7 @@ def mlp_leg(args):
                                                             h.storage.data_ptr(), stream))
         clef_i4.project_prepared(h, wd, out=y)
 
-    ms = timed(block, max(1, args.steps // 2), args.warmup)
+    ms = timed(block, args.steps, max(1, args.warmup // 2))
     ops = 2.0 * m * (2 * f) * d + 2.0 * m * d * f
     return {"ms": ms, "tops": ops / ms / 1e9}
 
@@ -293,7 +297,11 @@ def moe_leg(args):
     out = torch.empty((t, d), dtype=torch.bfloat16, device="cuda")
     ms = timed(lambda: layer(x, logits, out=out), args.steps, args.warmup)
     ops = 8.0 * t * 2 * (2 * inter * d + d * inter)
-    return {"tokens": t, "ms": ms, "tokens_per_s": t / ms * 1e3, "tops": ops / ms / 1e9}
+    # Minimum HBM bytes: the codes and scales of every expert with a route (all
+    # 128 at 4096 tokens), x and the logits read once, the output written once.
+    nbytes = 128 * (3 * inter * d // 2 + 4 * (2 * inter + d)) + t * (2 * d + 2 * 128) + 2 * t * d
+    return {"tokens": t, "ms": ms, "tokens_per_s": t / ms * 1e3, "tops": ops / ms / 1e9, "ops": ops,
+            "bytes": nbytes}
 
 
 def copy_leg(args):
@@ -334,6 +342,17 @@ def cpu_leg():
     oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k)
     gemm_s = time.perf_counter() - t0
 
+    # c1, the single linear M512 K2048 N2048 (quantize + GEMM), repeated so
+    # the sample is long enough to time.
+    m1, n1, k1, reps = 512, 2048, 2048, 20
+    x1 = oracle.f32_to_bf16(rng.standard_normal((m1, k1)).astype(np.float32))
+    w1 = codes(n1 * k1 // 8), np.full(n1, 1e-3, dtype=np.float32)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        c1_codes, c1_scales, _ = oracle.prepare(x1, oracle.activation_stride(k1))
+        oracle.gemm(c1_codes, c1_scales, w1[0], w1[1], n1, k1)
+    c1_s = (time.perf_counter() - t0) / reps
+
     t, d, inter = 4096, 2048, 768
     xs = oracle.f32_to_bf16(rng.standard_normal((t, d)).astype(np.float32))
     lg = oracle.f32_to_bf16(rng.standard_normal((t, 128)).astype(np.float32))
@@ -349,7 +368,9 @@ def cpu_leg():
         "cores": threads,
         "kind": "port",
         "sample": f"full INT4 GEMM M{m} N{n} K{k} incl. activation quantize ({gemm_s:.2f} s); "
+                  f"{reps} x the M{m1} K{k1} N{n1} linear incl. quantize ({c1_s * 1e3:.1f} ms each); "
                   f"full MoE layer T{t} D{d} I{inter} ({moe_s:.2f} s)",
+        "c1_tops": round(2.0 * m1 * n1 * k1 / c1_s / 1e12, 4),
         "moe_tokens_per_s": round(t / moe_s, 1),
     }
 
@@ -367,8 +388,6 @@ def main():
     clef_i4.lib()
     torch.cuda.init()
     res = {}
-    if args.only in (None, "gemm"):
-        res["gemm"] = gemm_leg(args)
     if args.only in (None, "moe"):
         res["moe"] = moe_leg(args)
     if args.only in (None, "mlp"):
@@ -382,6 +401,11 @@ def main():
         res["attn"] = attention_leg(args)
     if args.only in (None, "moe65536"):
         res["moe65536"] = moe_skewed_leg(args)
+    # The headline GEMM runs last: the other legs keep the device busy for
+    # seconds before it, so its timed launches see the sustained clock of a
+    # loaded device rather than the ramp of an idle one.
+    if args.only in (None, "gemm"):
+        res["gemm"] = gemm_leg(args)
     if args.only == "peaks":
         import subprocess
         probe = os.path.join(ROOT, "clef-hrx_amd", "lib", "peaks")
@@ -417,8 +441,9 @@ def main():
         line["pct_int8_peak"] = round(100.0 * g["tops"] / INT8_PEAK_TOPS, 2)
         line["prepare_ms"] = round(g["prepare_ms"], 4)
         line["roofline"] = {"bound": "mfma", "achieved": round(g["tops"], 1), "peak": INT8_PEAK_TOPS,
-                            "unit": "TFLOP/s", "frac": round(g["tops"] / INT8_PEAK_TOPS, 4),
+                            "unit": "TOPS", "frac": round(g["tops"] / INT8_PEAK_TOPS, 4),
                             "traffic": GEMM_TRAFFIC_BYTES,
+                            "traffic_source": "profiles/int4_gemm_m4096_k4096_n12288.txt (FETCH_SIZE, WRITE_SIZE)",
                             "algorithmic_bytes": g["bytes"]}
     if "moe" in res:
         if res["moe"]["tokens"] != 4096:
@@ -426,6 +451,16 @@ def main():
         line["moe_tokens_per_s"] = round(res["moe"]["tokens_per_s"], 1)
         line["moe_layer_ms"] = round(res["moe"]["ms"], 4)
         line["moe_tops"] = round(res["moe"]["tops"], 1)
+        m = res["moe"]
+        # The layer is MFMA-bound (3.09e11 ops at 5.0 POP/s = 61.8 us against
+        # 0.34 GB at 8 TB/s = 42 us).
+        line["moe_roofline"] = {"bound": "mfma", "achieved": round(m["tops"], 1), "peak": INT8_PEAK_TOPS,
+                                "unit": "TOPS", "frac": round(m["tops"] / INT8_PEAK_TOPS, 4),
+                                "roofline_us": round(max(m["ops"] / INT8_PEAK_TOPS / 1e6,
+                                                         m["bytes"] / HBM_PEAK_GBS / 1e3), 1),
+                                "hbm_gbs": round(m["bytes"] / m["ms"] / 1e6, 1),
+                                "algorithmic_bytes": m["bytes"], "traffic": MOE_TRAFFIC_BYTES,
+                                "traffic_source": "profiles/omni_int4_moe_t4096.txt (FETCH_SIZE, WRITE_SIZE)"}
     if "mlp" in res:
         line["mlp_block_ms"] = round(res["mlp"]["ms"], 4)
         line["mlp_tops"] = round(res["mlp"]["tops"], 1)

@@ -58,6 +58,9 @@ SIGNATURES = {
                                                   _P, _SZ, _P]),
     "clef_moe_expert_i4": (ctypes.c_int, [_P, _I32, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P,
                                           _P, _SZ, _P]),
+    "clef_moe_expert_ungrouped_workspace_bytes": (_SZ, [_I64, _I32]),
+    "clef_moe_expert_i4_ungrouped": (ctypes.c_int, [_P, _I32, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P,
+                                                    _P, _SZ, _P]),
     "clef_swiglu": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
     "clef_moe_combine": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _I32, _P, _P]),
     "clef_pack_cache_path": (ctypes.c_int, [_P, _P, _P, _SZ]),
@@ -505,6 +508,23 @@ def omni_expert(a: Prepared, w: QuantizedWeight, groups: torch.Tensor, tokens: i
     _check(lib().clef_moe_expert_i4(_ptr(a.storage), a.stride, _ptr(a.scales), _ptr(w.codes),
                                     _ptr(w.scales), _ptr(groups), tokens, topk, w.cols, n,
                                     int(input_routed), _ptr(out), _ptr(ws), ws_bytes, _stream()))
+    return out
+
+
+def omni_expert_ungrouped(a: Prepared, w: QuantizedWeight, routes: torch.Tensor, input_routed: bool
+                          ) -> torch.Tensor:
+    """Engine::omni_expert (src/omni.rs:280-288), the expert GEMM without a
+    groups table: every route slot computed on its own. Rows of slots naming
+    no expert stay zero."""
+    tokens = routes.shape[0]
+    topk = routes.shape[1] // 2
+    n = w.rows // 128
+    out = torch.zeros((tokens * topk, n), dtype=torch.bfloat16, device=routes.device)
+    ws_bytes = int(lib().clef_moe_expert_ungrouped_workspace_bytes(tokens, topk))
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=routes.device)
+    _check(lib().clef_moe_expert_i4_ungrouped(_ptr(a.storage), a.stride, _ptr(a.scales), _ptr(w.codes),
+                                              _ptr(w.scales), _ptr(routes), tokens, topk, w.cols, n,
+                                              int(input_routed), _ptr(out), _ptr(ws), ws_bytes, _stream()))
     return out
 
 

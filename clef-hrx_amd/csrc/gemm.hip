@@ -725,7 +725,7 @@ __global__ __launch_bounds__(T::THREADS, 2) void expert_dmah_kernel(
     const uint32_t* __restrict__ a, int a_words, uint32_t a_bytes, const float* __restrict__ as,
     const uint32_t* __restrict__ w, const float* __restrict__ ws, const uint32_t* __restrict__ w2,
     const float* __restrict__ ws2, const float* __restrict__ groups, const int32_t* __restrict__ schedule,
-    int64_t tokens, int topk, int kb, int n, int input_routed, uint16_t* __restrict__ out, int tiles_n) {
+    int64_t list_stride, int topk, int kb, int n, int input_routed, uint16_t* __restrict__ out, int tiles_n) {
 #if defined(__HIP_DEVICE_COMPILE__)
   extern __shared__ __align__(16) char lds[];
   const int64_t items = (int64_t)schedule[0] * tiles_n;
@@ -738,7 +738,7 @@ __global__ __launch_bounds__(T::THREADS, 2) void expert_dmah_kernel(
   const int tn = (int)(item - (int64_t)tile * tiles_n);
   const int e = schedule[1 + 2 * tile];
   const int row0 = schedule[2 + 2 * tile];
-  const float* list = groups + (int64_t)e * (tokens + 1);
+  const float* list = groups + (int64_t)e * list_stride;
   const int count = (int)list[0];
   constexpr int COLS = GU ? T::BN / 2 : T::BN;  // output columns per tile
   const int n0 = tn * COLS;
@@ -944,8 +944,8 @@ __global__ __launch_bounds__(T::THREADS, 2) void expert_dmah_kernel(
 template <class T, bool GU>
 hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, const float* as, const uint32_t* w,
                               const float* ws, const uint32_t* w2, const float* ws2, const float* groups,
-                              const int32_t* schedule, int64_t tokens, int topk, int k, int n, int input_routed,
-                              uint16_t* out, hipStream_t stream);
+                              const int32_t* schedule, int64_t routes, int64_t list_stride, int topk, int k, int n,
+                              int input_routed, uint16_t* out, hipStream_t stream);
 
 // Small-M G1: with few activation rows the weight stream is the whole cost,
 // and N / 128 workgroups walking all of K leave most of the GPU and of HBM
@@ -1115,7 +1115,7 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
     const uint32_t* __restrict__ a, int a_words, uint32_t a_bytes, const float* __restrict__ as,
     const uint32_t* __restrict__ w, const float* __restrict__ ws, const uint32_t* __restrict__ w2,
     const float* __restrict__ ws2, const float* __restrict__ groups, const int32_t* __restrict__ schedule,
-    int64_t tokens, int topk, int kb, int n, int input_routed, uint16_t* __restrict__ out, int slices) {
+    int64_t list_stride, int topk, int kb, int n, int input_routed, uint16_t* __restrict__ out, int slices) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int NA = GU ? 2 : 1;
   const int NW = (int)blockDim.x >> 6;
@@ -1127,7 +1127,7 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
   const int c0 = (int)(item - (int64_t)tile * slices) * 32;  // first output column within the expert
   const int e = schedule[1 + 2 * tile];
   const int row0 = schedule[2 + 2 * tile];
-  const float* list = groups + (int64_t)e * (tokens + 1);
+  const float* list = groups + (int64_t)e * list_stride;
   const int count = (int)list[0];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1226,8 +1226,8 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
 template <bool GU>
 hipError_t launch_expert_skinny(const uint32_t* a, int a_words, int64_t a_bytes, const float* as,
                                 const uint32_t* w, const float* ws, const uint32_t* w2, const float* ws2,
-                                const float* groups, const int32_t* schedule, int64_t tokens, int topk, int k,
-                                int n, int input_routed, uint16_t* out, hipStream_t stream);
+                                const float* groups, const int32_t* schedule, int64_t routes, int64_t list_stride,
+                                int topk, int k, int n, int input_routed, uint16_t* out, hipStream_t stream);
 
 }  // namespace
 
@@ -1296,14 +1296,14 @@ namespace {
 template <bool GU>
 hipError_t launch_expert_skinny(const uint32_t* a, int a_words, int64_t a_bytes, const float* as,
                                 const uint32_t* w, const float* ws, const uint32_t* w2, const float* ws2,
-                                const float* groups, const int32_t* schedule, int64_t tokens, int topk, int k,
-                                int n, int input_routed, uint16_t* out, hipStream_t stream) {
+                                const float* groups, const int32_t* schedule, int64_t routes, int64_t list_stride,
+                                int topk, int k, int n, int input_routed, uint16_t* out, hipStream_t stream) {
   if (a_bytes >= ((int64_t)1 << 31) || n % 32 != 0) return hipErrorInvalidValue;
   const int slices = n / 32;
-  const int64_t blocks = expert_max_tiles(tokens * topk) * slices;
+  const int64_t blocks = expert_max_tiles(routes) * slices;
   const int waves = k / 256 < 16 ? k / 256 : 16;  // one k-step per wave at most needs no more waves
   expert_skinny_kernel<GU><<<(unsigned)blocks, 64 * waves, 0, stream>>>(a, a_words, (uint32_t)a_bytes, as, w, ws, w2,
-                                                                   ws2, groups, schedule, tokens, topk, k / 256,
+                                                                   ws2, groups, schedule, list_stride, topk, k / 256,
                                                                    n, input_routed, out, slices);
   return hipGetLastError();
 }
@@ -1313,15 +1313,15 @@ namespace {
 template <class T, bool GU>
 hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, const float* as, const uint32_t* w,
                               const float* ws, const uint32_t* w2, const float* ws2, const float* groups,
-                              const int32_t* schedule, int64_t tokens, int topk, int k, int n, int input_routed,
-                              uint16_t* out, hipStream_t stream) {
+                              const int32_t* schedule, int64_t routes, int64_t list_stride, int topk, int k, int n,
+                              int input_routed, uint16_t* out, hipStream_t stream) {
   static LaunchCache cache;
   const void* kern = reinterpret_cast<const void*>(&expert_dmah_kernel<T, GU>);
   if (hipError_t e = ensure_dynamic_lds(cache, kern, expert_lds_bytes<T, GU>())) return e;
   const int tiles_n = n / (GU ? T::BN / 2 : T::BN);
-  const int64_t blocks = 8 * ((expert_max_tiles(tokens * topk) * tiles_n + 7) / 8);
+  const int64_t blocks = 8 * ((expert_max_tiles(routes) * tiles_n + 7) / 8);
   expert_dmah_kernel<T, GU><<<(unsigned)blocks, T::THREADS, expert_lds_bytes<T, GU>(), stream>>>(
-      a, a_words, (uint32_t)a_bytes, as, w, ws, w2, ws2, groups, schedule, tokens, topk, k / 256, n, input_routed,
+      a, a_words, (uint32_t)a_bytes, as, w, ws, w2, ws2, groups, schedule, list_stride, topk, k / 256, n, input_routed,
       out, tiles_n);
   return hipGetLastError();
 }
@@ -1331,14 +1331,16 @@ hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, c
 hipError_t launch_expert_gate_up(const uint32_t* a, int a_words, const float* as, const uint32_t* gate_w,
                                  const float* gate_s, const uint32_t* up_w, const float* up_s, const float* groups,
                                  const int32_t* schedule, int64_t tokens, int topk, int k, int n, uint16_t* h,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, int64_t list_stride) {
   const int64_t a_bytes = tokens * a_words * 4;
+  const int64_t routes = tokens * topk;
+  if (list_stride <= 0) list_stride = tokens + 1;
   if (a_bytes >= ((int64_t)1 << 31) || n % 128 != 0) return hipErrorInvalidValue;
-  if (expert_tile_rows(tokens * topk) == kExpertSkinnyBM)
-    return launch_expert_skinny<true>(a, a_words, a_bytes, as, gate_w, gate_s, up_w, up_s, groups, schedule, tokens,
-                                      topk, k, n, 0, h, stream);
+  if (expert_tile_rows(routes) == kExpertSkinnyBM)
+    return launch_expert_skinny<true>(a, a_words, a_bytes, as, gate_w, gate_s, up_w, up_s, groups, schedule, routes,
+                                      list_stride, topk, k, n, 0, h, stream);
   return launch_expert_dmah<ExpertGUTile, true>(a, a_words, a_bytes, as, gate_w, gate_s, up_w, up_s, groups,
-                                                schedule, tokens, topk, k, n, 0, h, stream);
+                                                schedule, routes, list_stride, topk, k, n, 0, h, stream);
 }
 
 size_t expert_schedule_bytes(int64_t routes) {
@@ -1359,16 +1361,18 @@ hipError_t launch_expert_tasks(const float* groups, int64_t tokens, float* tasks
 hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* as, const uint32_t* w,
                             const float* ws, const float* groups, const int32_t* schedule,
                             int64_t tokens, int topk, int k, int n, int input_routed, uint16_t* out,
-                            hipStream_t stream) {
-  const int64_t a_rows = input_routed ? tokens * topk : tokens;
+                            hipStream_t stream, int64_t list_stride) {
+  const int64_t routes = tokens * topk;
+  const int64_t a_rows = input_routed ? routes : tokens;
   const int64_t a_bytes = a_rows * a_words * 4;
-  if (expert_tile_rows(tokens * topk) == kExpertSkinnyBM)
-    return launch_expert_skinny<false>(a, a_words, a_bytes, as, w, ws, w, ws, groups, schedule, tokens, topk, k, n,
-                                       input_routed, out, stream);
+  if (list_stride <= 0) list_stride = tokens + 1;
+  if (expert_tile_rows(routes) == kExpertSkinnyBM)
+    return launch_expert_skinny<false>(a, a_words, a_bytes, as, w, ws, w, ws, groups, schedule, routes, list_stride,
+                                       topk, k, n, input_routed, out, stream);
   // The callers reject activation operands of 2 GiB or more and n % 256 != 0.
   if (a_bytes >= ((int64_t)1 << 31) || n % 256 != 0) return hipErrorInvalidValue;
-  return launch_expert_dmah<ExpertHTile, false>(a, a_words, a_bytes, as, w, ws, w, ws, groups, schedule, tokens,
-                                                topk, k, n, input_routed, out, stream);
+  return launch_expert_dmah<ExpertHTile, false>(a, a_words, a_bytes, as, w, ws, w, ws, groups, schedule, routes,
+                                                list_stride, topk, k, n, input_routed, out, stream);
 }
 
 }  // namespace clef

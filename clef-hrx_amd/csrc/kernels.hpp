@@ -66,17 +66,26 @@ int64_t expert_max_tiles(int64_t routes);
 size_t expert_schedule_bytes(int64_t routes);
 hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int topk, int32_t* schedule,
                                   hipStream_t stream);
+// `list_stride` is the row pitch of `groups` in floats: tokens + 1 for the
+// reference's table (0 selects it), more for a table that lists every route
+// slot (ungrouped, duplicates included).
 hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* a_scales,
                             const uint32_t* w_tiled, const float* w_scales, const float* groups,
                             const int32_t* schedule, int64_t tokens, int topk, int k, int n,
-                            int input_routed, uint16_t* out, hipStream_t stream);
+                            int input_routed, uint16_t* out, hipStream_t stream, int64_t list_stride = 0);
 
 // Fused gate/up expert GEMMs with SwiGLU: h[route][c] = S1(E1(gate), E1(up)),
 // routed rows gathered from `a` by route / topk; n % 128 == 0.
 hipError_t launch_expert_gate_up(const uint32_t* a, int a_words, const float* as, const uint32_t* gate_w,
                                  const float* gate_s, const uint32_t* up_w, const float* up_s, const float* groups,
                                  const int32_t* schedule, int64_t tokens, int topk, int k, int n, uint16_t* h,
-                                 hipStream_t stream);
+                                 hipStream_t stream, int64_t list_stride = 0);
+
+// Every route slot of `routes` ([tokens][2 * topk]) as a one-slot token:
+// slots[j] = (routes[j / topk][j % topk], 0) for j < tokens * topk. Grouping
+// slots with topk 1 lists every slot naming an expert, duplicates included,
+// under its ordinal j = t * topk + r.
+hipError_t launch_route_slots(const float* routes, int64_t tokens, int topk, float* slots, hipStream_t stream);
 
 hipError_t launch_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h,
                          hipStream_t stream);

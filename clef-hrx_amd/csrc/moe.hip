@@ -512,6 +512,23 @@ size_t group_workspace_bytes(int64_t tokens) {
   return (size_t)blocks * 128 * sizeof(int);
 }
 
+namespace {
+__global__ __launch_bounds__(256) void route_slots_kernel(const float* __restrict__ routes, int64_t slots_n,
+                                                          int topk, float* __restrict__ slots) {
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= slots_n) return;
+  const int64_t t = j / topk;
+  slots[2 * j] = routes[t * 2 * topk + (j - t * topk)];
+  slots[2 * j + 1] = 0.0f;
+}
+}  // namespace
+
+hipError_t launch_route_slots(const float* routes, int64_t tokens, int topk, float* slots, hipStream_t stream) {
+  const int64_t n = tokens * topk;
+  route_slots_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(routes, n, topk, slots);
+  return hipGetLastError();
+}
+
 hipError_t launch_group_routes(const float* routes, int64_t tokens, int topk, float* groups,
                                float* order, void* workspace, hipStream_t stream, int32_t* schedule,
                                int schedule_bm) {

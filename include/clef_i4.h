@@ -257,6 +257,26 @@ int clef_moe_expert_i4(const uint32_t* a, int32_t stride, const float* a_scales,
                        uint16_t* out, void* workspace, size_t workspace_bytes,
                        clef_stream_t stream);
 
+/* Bytes of scratch clef_moe_expert_i4_ungrouped needs (0 for shapes it
+ * rejects). */
+size_t clef_moe_expert_ungrouped_workspace_bytes(int64_t tokens, int32_t topk);
+
+/* The expert GEMM without a groups table: for every route slot (t, r) whose
+ * expert id e = (int)routes[t][r] names one of the 128 experts, row
+ * t * topk + r of `out` gets the E1 values of expert e, with every slot
+ * computed on its own (duplicate experts of one token included), as the
+ * reference's ungrouped kernel computes them. Slots naming no expert (the
+ * reference assumes there are none) leave their rows unwritten. Replaces
+ * Engine::omni_expert (src/omni.rs:280-288: omni_expert_impl with groups =
+ * None) and kernels/omni_expert.loom:86-150, whose f32 FMA dot is exact on
+ * integer codes, so results equal clef_moe_expert_i4's bit for bit. The
+ * slots are grouped into the workspace (topk-1 grouping of the slots), then
+ * the grouped kernels run. Preconditions: those of clef_moe_expert_i4. */
+int clef_moe_expert_i4_ungrouped(const uint32_t* a, int32_t stride, const float* a_scales,
+                                 const uint32_t* w_tiled, const float* w_scales, const float* routes,
+                                 int64_t tokens, int32_t topk, int32_t k, int32_t n, int32_t input_routed,
+                                 uint16_t* out, void* workspace, size_t workspace_bytes, clef_stream_t stream);
+
 /* Fused gate/up expert GEMMs with SwiGLU: for every routed row r of every
  * expert e, h[r][c] = bf16(bf16(g/(1+exp(-g))) * u) where g and u are the E1
  * outputs (as clef_moe_expert_i4, input_routed = 0) of gate_w and up_w for

@@ -55,6 +55,8 @@ def lib() -> ctypes.CDLL:
             "orc_expert_i4": (ctypes.c_int, [_P, _I32, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P]),
             "orc_swiglu": (None, [_P, _P, _I64, _P]),
             "orc_combine": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _I32, _P]),
+            "orc_expert_i4_ungrouped": (ctypes.c_int, [_P, _I32, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32,
+                                                       _P]),
             "orc_moe_layer": (ctypes.c_int, [_P, _P, _I32, _I64, _I32, _I32, _I32, _I32,
                                              _P, _P, _P, _P, _P, _P, _P, _P]),
             "orc_tile_rows": (ctypes.c_int, [_P, _I64, _I32, _P]),
@@ -258,6 +260,21 @@ def expert_i4(a_codes, a_scales, w_tiled, w_scales, groups, tokens: int, topk: i
                                _ptr(w_tiled), _ptr(np.ascontiguousarray(w_scales, np.float32)),
                                _ptr(np.ascontiguousarray(groups, np.float32)), tokens, topk, k, n,
                                int(input_routed), _ptr(out)))
+    return out
+
+
+def expert_i4_ungrouped(a_codes, a_scales, w_tiled, w_scales, routes, k: int, n: int,
+                        input_routed: bool) -> np.ndarray:
+    """Every route slot of routes [T][2*topk] on its own; rows of slots naming
+    no expert stay zero."""
+    a_codes = np.ascontiguousarray(a_codes, dtype=np.uint32)
+    routes = np.ascontiguousarray(routes, dtype=np.float32)
+    tokens, topk = routes.shape[0], routes.shape[1] // 2
+    stride = a_codes.shape[1] * 8
+    out = np.zeros((tokens * topk, n), dtype=np.uint16)
+    _check(lib().orc_expert_i4_ungrouped(_ptr(a_codes), stride, _ptr(np.ascontiguousarray(a_scales, np.float32)),
+                                         _ptr(w_tiled), _ptr(np.ascontiguousarray(w_scales, np.float32)),
+                                         _ptr(routes), tokens, topk, k, n, int(input_routed), _ptr(out)))
     return out
 
 

@@ -18,6 +18,8 @@
  *   orc_group_routes  brute-force list construction, total-order sort of ids
  *   orc_expert_tasks  brute-force task list
  *   orc_expert_i4     dense oracle (orc_gemm_acc) restricted to routed rows
+ *   orc_expert_i4_ungrouped  orc_expert_i4 on duplicate-free routes; the
+ *                     dense oracle on every slot (duplicates included)
  *   orc_swiglu        float64 SiLU within one bf16 step per rounding
  *   orc_combine       the reference's sparse MoE test formula
  *   orc_expf          float64 exp, <= 2 ulp
@@ -571,6 +573,44 @@ int orc_expert_i4(const uint32_t* a, int32_t stride, const float* a_scales,
                     float s = as * w_scales[(int64_t)e * n + c];
                     out[route * n + c] = orc_f32_to_bf16((float)acc * s);
                 }
+            }
+        }
+        free(au);
+        free(wu);
+    }
+    return 0;
+}
+
+/* Ungrouped E1 (Engine::omni_expert, src/omni.rs:280-288;
+ * kernels/omni_expert.loom:86-150): every route slot (t, r) on its own, no
+ * groups table. The expert is (int)routes[t][r] (slots naming no expert in
+ * 0..127 are skipped); the dot is the exact integer sum the reference's f32
+ * FMA chain reaches on integer codes; out[t*topk + r][c] =
+ * bf16(RN(f32(dot) * RN(as[xr] * ws[e*n + c]))). */
+int orc_expert_i4_ungrouped(const uint32_t* a, int32_t stride, const float* a_scales,
+                            const uint32_t* w_tiled, const float* w_scales, const float* routes,
+                            int64_t tokens, int32_t topk, int32_t k, int32_t n, int32_t input_routed,
+                            uint16_t* out) {
+    if (!(k % 256 == 0 && n % 256 == 0 && k >= 256 && n >= 256 && stride >= k && stride % 8 == 0 &&
+          tokens >= 1 && topk >= 1))
+        return fail("unsupported Omni expert tile shape");
+    const int64_t a_words = stride / 8;
+#pragma omp parallel
+    {
+        int8_t* wu = (int8_t*)malloc((size_t)k);
+        int8_t* au = (int8_t*)malloc((size_t)k);
+#pragma omp for schedule(dynamic, 16)
+        for (int64_t slot = 0; slot < tokens * topk; ++slot) {
+            const int64_t t = slot / topk, r = slot % topk;
+            const float id = routes[t * 2 * topk + r];
+            if (!(id > -1.0f && id < 128.0f)) continue;
+            const int64_t e = (int32_t)id;
+            const int64_t xr = input_routed ? slot : t;
+            unpack_row(a + xr * a_words, k, 4, au);
+            for (int64_t c = 0; c < n; ++c) {
+                unpack_tiled_row(w_tiled, e * n + c, k, 4, wu);
+                float s = a_scales[xr] * w_scales[e * n + c];
+                out[slot * n + c] = orc_f32_to_bf16((float)dot_i8(au, wu, k) * s);
             }
         }
         free(au);

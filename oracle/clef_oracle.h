@@ -75,6 +75,10 @@ int orc_expert_i4(const uint32_t* a, int32_t stride, const float* a_scales,
 /* S1: SwiGLU with the reference's BF16 materialization. */
 void orc_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h);
 /* C1: weighted combine in ascending expert order; order may be NULL. */
+int orc_expert_i4_ungrouped(const uint32_t* a, int32_t stride, const float* a_scales,
+                            const uint32_t* w_tiled, const float* w_scales, const float* routes,
+                            int64_t tokens, int32_t topk, int32_t k, int32_t n, int32_t input_routed,
+                            uint16_t* out);
 int orc_combine(const uint16_t* values, const float* routes, const float* order,
                 int64_t tokens, int32_t width, int32_t topk, uint16_t* out);
 /* MoE block: route -> group -> Q1 -> E1 gate/up -> S1 -> Q1 -> E1 down -> C1. */

@@ -535,6 +535,35 @@ def test_expert_gemm_matches_oracle(tokens, hidden):
     assert_same_u16(bf16_host(got), want, "expert down")
 
 
+@pytest.mark.parametrize("tokens", [3, 64, 300])
+@pytest.mark.parametrize("input_routed", [False, True])
+def test_expert_ungrouped_matches_oracle(tokens, input_routed):
+    """Engine::omni_expert (src/omni.rs:280-288), the expert GEMM without a
+    groups table, on routes with a duplicate expert, an all-127 token and
+    ids naming no expert: every slot bit-exact against the oracle's ungrouped
+    E1 (both tile regimes: 24 / 512 routed rows on 32-slot tiles, 2400 on
+    128-slot tiles), and equal to the grouped entry point on router output."""
+    from test_oracle import duplicate_routes
+
+    rng = np.random.default_rng(tokens * 2 + input_routed)
+    k, n, topk = 512, 256, 8
+    rows = tokens * topk if input_routed else tokens
+    x = randn_bf16(rng, (rows, k))
+    sx = oracle.activation_stride(k)
+    codes, scales, _ = oracle.prepare(x, sx)
+    w_t, w_s = packed_experts(rng, n, k)
+    a, w = dev_prepared(x, sx), dev_weight(w_t, w_s, 128 * n, k)
+    routes = duplicate_routes(rng, tokens, topk)
+    want = oracle.expert_i4_ungrouped(codes, scales, w_t, w_s, routes, k, n, input_routed)
+    got = clef_i4.omni_expert_ungrouped(a, w, to_dev_f32(routes), input_routed)
+    assert_same_u16(bf16_host(got), want, f"ungrouped tokens={tokens} routed={input_routed}")
+    clean = random_routes(rng, tokens)
+    groups, _ = oracle.group_routes(clean)
+    grouped = clef_i4.omni_expert(a, w, to_dev_f32(groups), tokens, topk, input_routed)
+    got = clef_i4.omni_expert_ungrouped(a, w, to_dev_f32(clean), input_routed)
+    assert torch.equal(got.view(torch.int16), grouped.view(torch.int16))
+
+
 @pytest.mark.parametrize("tokens,wide", [(3, False), (64, False), (300, False), (300, True)])
 def test_expert_gate_up_swiglu_matches_oracle(tokens, wide):
     """Fused gate/up + SwiGLU (Engine::omni_gate_up, src/omni.rs:300-372) equals

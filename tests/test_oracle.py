@@ -368,6 +368,53 @@ def test_expert_matches_dense_oracle_on_routed_rows():
             assert np.array_equal(out[t * topk + r], want)
 
 
+def duplicate_routes(rng, tokens, topk=8):
+    """Router output with some slots rewritten: a token naming one expert
+    twice, a token naming expert 127 in every slot, and slots naming no
+    expert (-1.0 and 128.0), which the ungrouped kernel skips."""
+    routes = oracle.route(rng.standard_normal((tokens, 128)).astype(np.float32), topk)
+    if tokens >= 3:
+        routes[0, 3] = routes[0, 1]
+        routes[1, :topk] = 127.0
+        routes[2, 5] = -1.0
+        routes[2, 6] = 128.0
+    return routes
+
+
+@pytest.mark.parametrize("input_routed", [False, True])
+def test_expert_ungrouped_matches_grouped_and_dense(input_routed):
+    """Engine::omni_expert without groups (src/omni.rs:280-288,
+    kernels/omni_expert.loom:86-150): on router output (no duplicates) it
+    equals the grouped E1 bit for bit; on routes with a duplicate expert,
+    an all-127 token and out-of-range ids every slot naming an expert is the
+    dense oracle's value for that expert and row, and the others stay zero."""
+    rng = np.random.default_rng(5 + input_routed)
+    tokens, topk, k, n = 19, 8, 512, 256
+    rows = tokens * topk if input_routed else tokens
+    x = BF(rng.standard_normal((rows, k)).astype(np.float32))
+    codes, scales, _ = oracle.prepare(x, k, 4)
+    w_t, w_s = oracle.pack_weight(BF((0.02 * rng.standard_normal((128 * n, k))).astype(np.float32)))
+    routes = oracle.route(rng.standard_normal((tokens, 128)).astype(np.float32), topk)
+    groups, _ = oracle.group_routes(routes)
+    grouped = oracle.expert_i4(codes, scales, w_t, w_s, groups, tokens, topk, k, n, input_routed)
+    assert np.array_equal(oracle.expert_i4_ungrouped(codes, scales, w_t, w_s, routes, k, n, input_routed), grouped)
+    routes = duplicate_routes(rng, tokens, topk)
+    out = oracle.expert_i4_ungrouped(codes, scales, w_t, w_s, routes, k, n, input_routed)
+    acc = oracle.gemm_acc(codes, w_t, 128 * n, k)  # every row x every expert row
+    for t in range(tokens):
+        for r in range(topk):
+            slot = t * topk + r
+            xr = slot if input_routed else t
+            e = routes[t, r]
+            if not (-1.0 < e < 128.0):
+                assert np.all(out[slot] == 0)
+                continue
+            cols = slice(int(e) * n, (int(e) + 1) * n)
+            want = BF((acc[xr, cols].astype(np.float32) * (scales[xr] * w_s[cols]).astype(np.float32))
+                      .astype(np.float32))
+            assert np.array_equal(out[slot], want), (t, r)
+
+
 # ---------------------------------------------------------------- S1 / exp
 
 def test_expf_within_two_ulp():
