@@ -94,6 +94,16 @@ __device__ __forceinline__ uint32_t silu_lut_offset(uint32_t w, bool& inside) {
 }
 
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+typedef int16_t s16x2 __attribute__((ext_vector_type(2)));
+
+// 0x8000 in each half of a bf16 pair that holds +-0, 0xFFFF in the others:
+// ANDed into a result pair it keeps only the sign where the operand was zero.
+__device__ __forceinline__ uint32_t bf16x2_zero_keep(uint32_t pair) {
+  // bit 15 of each half of f: that half of pair is nonzero (no carry between
+  // halves: each is at most 0x7FFF + 0x7FFF)
+  const uint32_t f = (pair & 0x7FFF7FFFu) + 0x7FFF7FFFu;
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2, f) >> (int16_t)15) | 0x80008000u;
+}
 
 // silu_lut_offset of two bf16 values at once, with packed 16-bit operations:
 // `pair` holds the bf16 bits of two values (low and high half); the result
@@ -102,11 +112,13 @@ typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 // field is in the table's range, (t << 1) & 0x1FFF = (exponent - kSiluLutExp0)
 // << 8 | mantissa << 1 and h >> 2 puts the sign at bit 13, as in
 // silu_lut_offset. Bits 12..14 of either half of t are ORed into `outside`.
-__device__ __forceinline__ uint32_t silu_lut_offset2(uint32_t pair, uint32_t& outside) {
+// Halves whose bits in `flag_mask` are clear are not flagged.
+__device__ __forceinline__ uint32_t silu_lut_offset2(uint32_t pair, uint32_t& outside,
+                                                     uint32_t flag_mask = 0xFFFFFFFFu) {
   const u16x2 h = __builtin_bit_cast(u16x2, pair);
   const u16x2 t = h - (u16x2)(uint16_t)(kSiluLutExp0 << 7);
   const uint32_t tb = __builtin_bit_cast(uint32_t, t);
-  outside |= tb & 0x70007000u;
+  outside |= tb & flag_mask & 0x70007000u;
   const uint32_t lo = __builtin_bit_cast(uint32_t, (u16x2)(t << (uint16_t)1));
   const uint32_t sg = __builtin_bit_cast(uint32_t, (u16x2)(h >> (uint16_t)2));
   return (lo & 0x1FFF1FFFu) | (sg & 0xE000E000u);

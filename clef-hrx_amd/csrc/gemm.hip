@@ -14,6 +14,7 @@
 #include "silu_table.hpp"
 #include "gemm_dma.hpp"
 #include "gemm_dmah.hpp"
+#include "expert_persist.hpp"
 #include "kernels.hpp"
 
 namespace clef {
@@ -890,18 +891,36 @@ __global__ __launch_bounds__(T::THREADS, 2) void expert_dmah_kernel(
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
               gp[i][p] = pack_bf16x2(y[i][2 * p], y[i][2 * p + 1]);
+              // rows past the group's end (never stored) read as zero, which
+              // lies outside the table: give them 1.0 instead
+              if (row0 + wm * T::WM + 32 * i + lr >= count) gp[i][p] = 0x3F803F80u;
               const uint32_t off = silu_lut_offset2(gp[i][p], outside);
               act[i][2 * p] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(lds + LUT_OFF + (off & 0xFFFFu)));
               act[i][2 * p + 1] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(lds + LUT_OFF + (off >> 16)));
             }
           if (__any(outside != 0)) {
+            // silu(+-0) = +-0 (integer dot products are often zero): those
+            // directly, then the others outside the table only if there are any
+            bool others = false;
 #pragma unroll
             for (int i = 0; i < T::TM; ++i)
 #pragma unroll
               for (int t = 0; t < 4; ++t) {
                 const uint32_t gb = (t & 1) ? gp[i][t >> 1] >> 16 : gp[i][t >> 1] & 0xFFFFu;
-                if (((gb - ((uint32_t)kSiluLutExp0 << 7)) & 0x7000u) != 0) act[i][t] = silu_bf16(bf16_to_f32(gb));
+                const bool out = ((gb - ((uint32_t)kSiluLutExp0 << 7)) & 0x7000u) != 0;
+                if (out && (gb & 0x7FFFu) == 0) act[i][t] = bf16_to_f32(gb);
+                others = others | (out & ((gb & 0x7FFFu) != 0));
               }
+            if (__any(others)) {
+#pragma unroll
+              for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                  const uint32_t gb = (t & 1) ? gp[i][t >> 1] >> 16 : gp[i][t >> 1] & 0xFFFFu;
+                  if ((((gb - ((uint32_t)kSiluLutExp0 << 7)) & 0x7000u) != 0) & ((gb & 0x7FFFu) != 0))
+                    act[i][t] = silu_bf16(bf16_to_f32(gb));
+                }
+            }
           }
           // h = bf16(act * bf16(u)), u rounded two per register; the packing
           // below rounds h to bf16
@@ -1328,6 +1347,43 @@ hipError_t launch_expert_dmah(const uint32_t* a, int a_words, int64_t a_bytes, c
 }  // namespace
 
 
+namespace {
+// The persistent expert GEMM (expert_persist.hpp): kExpertWaves waves per
+// workgroup (4: two workgroups per CU on 128 x 256 items; 8: one per CU on
+// 128 x 512 items), a multiple of 8 workgroups so each XCD takes its range of
+// items.
+constexpr int kExpertWaves = 4;
+
+template <bool GU, int NW = kExpertWaves>
+hipError_t launch_expert_persist(const uint32_t* a, int a_words, int64_t a_bytes, const float* as, const uint32_t* w,
+                                 const float* ws, const uint32_t* w2, const float* ws2, const float* groups,
+                                 const int32_t* schedule, int64_t routes, int64_t list_stride, int topk, int k, int n,
+                                 int input_routed, uint16_t* out, hipStream_t stream) {
+  using P = ExpertPersist<GU, NW>;
+  static LaunchCache cache;
+  const void* kern = reinterpret_cast<const void*>(&expert_persist_kernel<GU, NW>);
+  if (hipError_t e = ensure_dynamic_lds(cache, kern, P::LDS)) return e;
+  int dev = 0, cus = 0;
+  if (hipError_t e = current_device(dev)) return e;
+  if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) return e;
+  const int grid = cus * P::PER_CU >= 8 ? cus * P::PER_CU / 8 * 8 : 8;
+  expert_persist_kernel<GU, NW><<<(unsigned)grid, P::THREADS, P::LDS, stream>>>(
+      a, a_words, (uint32_t)a_bytes, as, w, ws, w2, ws2, groups, schedule, list_stride, topk, k / 256, n,
+      input_routed, out, n / P::COLS);
+  return hipGetLastError();
+}
+
+// The persistent kernel takes items of ExpertPersist::COLS output columns and
+// needs at least two k-steps; other shapes run one workgroup per item
+// (expert_dmah_kernel).
+template <bool GU>
+bool use_expert_persist(int k, int n, int64_t routes) {
+  using P = ExpertPersist<GU, kExpertWaves>;
+  return k / 256 * 2 >= P::MIN_HALF_STEPS && n % P::COLS == 0 &&
+         routes * n * 2 <= ((int64_t)1 << 31);  // 32-bit store offsets
+}
+}  // namespace
+
 hipError_t launch_expert_gate_up(const uint32_t* a, int a_words, const float* as, const uint32_t* gate_w,
                                  const float* gate_s, const uint32_t* up_w, const float* up_s, const float* groups,
                                  const int32_t* schedule, int64_t tokens, int topk, int k, int n, uint16_t* h,
@@ -1339,6 +1395,9 @@ hipError_t launch_expert_gate_up(const uint32_t* a, int a_words, const float* as
   if (expert_tile_rows(routes) == kExpertSkinnyBM)
     return launch_expert_skinny<true>(a, a_words, a_bytes, as, gate_w, gate_s, up_w, up_s, groups, schedule, routes,
                                       list_stride, topk, k, n, 0, h, stream);
+  if (use_expert_persist<true>(k, n, routes))
+    return launch_expert_persist<true>(a, a_words, a_bytes, as, gate_w, gate_s, up_w, up_s, groups, schedule, routes,
+                                       list_stride, topk, k, n, 0, h, stream);
   return launch_expert_dmah<ExpertGUTile, true>(a, a_words, a_bytes, as, gate_w, gate_s, up_w, up_s, groups,
                                                 schedule, routes, list_stride, topk, k, n, 0, h, stream);
 }
@@ -1371,6 +1430,9 @@ hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* as, con
                                        topk, k, n, input_routed, out, stream);
   // The callers reject activation operands of 2 GiB or more and n % 256 != 0.
   if (a_bytes >= ((int64_t)1 << 31) || n % 256 != 0) return hipErrorInvalidValue;
+  if (use_expert_persist<false>(k, n, routes))
+    return launch_expert_persist<false>(a, a_words, a_bytes, as, w, ws, w, ws, groups, schedule, routes, list_stride,
+                                        topk, k, n, input_routed, out, stream);
   return launch_expert_dmah<ExpertHTile, false>(a, a_words, a_bytes, as, w, ws, w, ws, groups, schedule, routes,
                                                 list_stride, topk, k, n, input_routed, out, stream);
 }

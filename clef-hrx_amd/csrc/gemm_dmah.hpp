@@ -40,7 +40,7 @@ struct DmaHTile {
   static constexpr int NW = WAVES_M * WAVES_N;
   static constexpr int THREADS = 64 * NW;
   static constexpr int BM = WM * WAVES_M, BN = WN * WAVES_N;
-  static_assert(NW == 4, "four waves per workgroup");
+  static_assert(NW == 4 || NW == 8, "four or eight waves per workgroup");
   static_assert(WM % 32 == 0 && WN % 32 == 0 && BN % 128 == 0, "tile shape");
   static_assert(BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "whole DMA instructions per wave");
   static constexpr int TM = WM / 32, TN = WN / 32;

@@ -14,7 +14,8 @@ __device__ const uint16_t g_silu_lut[kSiluLutSize] __attribute__((unused, aligne
 };
 
 // bf16(silu(g)) for N bf16 values g (exact bf16 values in f32): table reads
-// for all, then one wave-uniform branch for values outside the table.
+// for all, then wave-uniform branches for values outside the table (zeros,
+// then the rest).
 // `table` is g_silu_lut or a copy of it (in LDS).
 template <int N>
 __device__ __forceinline__ void silu_lut(const float (&g)[N], float (&act)[N], const uint16_t* table = g_silu_lut) {
@@ -27,9 +28,18 @@ __device__ __forceinline__ void silu_lut(const float (&g)[N], float (&act)[N], c
     act[i] = bf16_to_f32(table[off >> 1]);
   }
   if (__any(slow)) {
+    // silu(+-0) = +-0 directly, then the other values outside the table
+    bool others = false;
 #pragma unroll
-    for (int i = 0; i < N; ++i)
-      if (!inside[i]) act[i] = silu_bf16(g[i]);
+    for (int i = 0; i < N; ++i) {
+      if (!inside[i] && g[i] == 0.0f) act[i] = g[i];
+      others = others | (!inside[i] & (g[i] != 0.0f));
+    }
+    if (__any(others)) {
+#pragma unroll
+      for (int i = 0; i < N; ++i)
+        if (!inside[i] & (g[i] != 0.0f)) act[i] = silu_bf16(g[i]);
+    }
   }
 }
 

@@ -596,6 +596,60 @@ def test_expert_gate_up_swiglu_matches_oracle(tokens, wide):
         assert_same_u16(bf16_host(got), want, "fused gate/up swiglu")
 
 
+@pytest.mark.parametrize("tokens,k,n,routed,skew", [
+    (300, 768, 512, True, 2.0),    # the down projection's regime: K = 768 (six half-steps)
+    (600, 512, 1024, False, 0.0),  # the shortest K the persistent kernel takes (four half-steps)
+    (1000, 1024, 512, True, 4.0),  # strongly skewed: some experts span many tiles, others are empty
+    (257, 2048, 512, False, 0.0),  # 2056 routed rows, just past the 32-slot regime
+])
+def test_expert_persistent_matches_oracle(tokens, k, n, routed, skew):
+    """The persistent grouped expert GEMM (every active expert's items in one
+    launch, taken from per-XCD queues) against the oracle's E1, the whole
+    output bit for bit; a second call on the same workspace gives the same
+    result (the queue counters are reset with each schedule)."""
+    rng = np.random.default_rng(tokens + k + n)
+    topk = 8
+    routes = random_routes(rng, tokens, skew=skew)
+    groups, _ = oracle.group_routes(routes)
+    rows = tokens * topk if routed else tokens
+    x = randn_bf16(rng, (rows, k))
+    sx = oracle.activation_stride(k)
+    codes, scales, _ = oracle.prepare(x, sx)
+    w_t, w_s = packed_experts(rng, n, k)
+    want = oracle.expert_i4(codes, scales, w_t, w_s, groups, tokens, topk, k, n, routed)
+    a, w = dev_prepared(x, sx), dev_weight(w_t, w_s, 128 * n, k)
+    g = to_dev_f32(groups)
+    got = clef_i4.omni_expert(a, w, g, tokens, topk, routed)
+    assert_same_u16(bf16_host(got), want, f"persistent expert tokens={tokens} k={k} n={n}")
+    again = clef_i4.omni_expert(a, w, g, tokens, topk, routed)
+    assert torch.equal(again.view(torch.int16), got.view(torch.int16))
+
+
+@pytest.mark.parametrize("tokens,k,n,skew", [(600, 2048, 768, 0.0), (700, 768, 256, 3.0), (300, 1024, 512, 1.0)])
+def test_expert_gate_up_persistent_matches_oracle(tokens, k, n, skew):
+    """The persistent fused gate/up + SwiGLU kernel (items of 256 gate and
+    256 up rows) at the Omni shape (K 2048, 768 columns: three column blocks)
+    and others, the whole h against E1, E1, S1 of the oracle, bit for bit."""
+    rng = np.random.default_rng(7 * tokens + k + n)
+    topk = 8
+    routes = random_routes(rng, tokens, skew=skew)
+    groups, _ = oracle.group_routes(routes)
+    x = randn_bf16(rng, (tokens, k))
+    sx = oracle.activation_stride(k)
+    codes, scales, _ = oracle.prepare(x, sx)
+    gw, gs = packed_experts(rng, n, k)
+    uw, us = packed_experts(rng, n, k)
+    g = oracle.expert_i4(codes, scales, gw, gs, groups, tokens, topk, k, n, False)
+    u = oracle.expert_i4(codes, scales, uw, us, groups, tokens, topk, k, n, False)
+    want = oracle.swiglu(g, u)
+    a = dev_prepared(x, sx)
+    gw_d, uw_d = dev_weight(gw, gs, 128 * n, k), dev_weight(uw, us, 128 * n, k)
+    got = clef_i4.omni_gate_up(a, gw_d, uw_d, to_dev_f32(groups), tokens, topk)
+    assert_same_u16(bf16_host(got), want, f"persistent gate/up tokens={tokens} k={k} n={n}")
+    again = clef_i4.omni_gate_up(a, gw_d, uw_d, to_dev_f32(groups), tokens, topk)
+    assert torch.equal(again.view(torch.int16), got.view(torch.int16))
+
+
 def test_swiglu_every_bf16_gate():
     """swiglu_preserves_materialized_rounding (src/ops.rs:482-520) over all
     65536 gate bit patterns."""
