@@ -43,10 +43,11 @@ HBM_PEAK_GBS = 8000.0
 # the reading for a plain 512 MiB copy (x2.000 fetch, x1.000 write); the runs
 # and raw readings are in profiles/int4_gemm_m4096_k4096_n12288.txt.
 GEMM_TRAFFIC_BYTES = 257.16e6
-# HBM bytes moved per MoE layer call at 4096 tokens (the same two counter
-# passes over `bench.py --only moe`, summed over the layer's kernels); None
-# until measured for the current kernels.
-MOE_TRAFFIC_BYTES = None
+# HBM bytes moved per MoE layer call at 4096 tokens: the same two counter
+# passes over `bench.py --only moe`, summed over the layer's eight kernels
+# (read 628.1 MB + written 235.3 MB; per kernel in
+# profiles/omni_int4_moe_t4096.txt).
+MOE_TRAFFIC_BYTES = 863.4e6
 
 
 def parse():
