@@ -46,6 +46,9 @@ SIGNATURES = {
     "clef_i4_gemm_config": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I64, _I32, _I32, _P, _P, _I32, _P]),
     "clef_i4_gemm_configs": (ctypes.c_int, []),
     "clef_i8_gemm": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P]),
+    "clef_i4_f6_activation": (ctypes.c_int, [_P, _I32, _I64, _I32, _P, _P]),
+    "clef_i4_f6_weight": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
+    "clef_i4_gemm_f6": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P]),
     "clef_i4_project_workspace_bytes": (_SZ, [_I64, _I32]),
     "clef_i4_project": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _I32, _P, _P, _P, _SZ, _P]),
     "clef_moe_router_logits": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P]),
@@ -428,6 +431,54 @@ def project_prepared(a: Prepared, w: QuantizedWeight, residual: torch.Tensor | N
                                      _ptr(w.scales), a.rows, w.rows, w.cols, _ptr(residual), _ptr(out),
                                      config, _stream()))
     return out
+
+
+@dataclass
+class F6Weight:
+    """A 4-bit QuantizedWeight re-encoded for the bf6 GEMM (clef_i4_f6_weight):
+    the same codes as 6-bit e3m2 values, rows x cols x 3/4 bytes."""
+    codes: torch.Tensor   # uint8 bf6 tiled
+    scales: torch.Tensor  # f32 [rows], shared with the source weight
+    rows: int
+    cols: int
+
+
+def f6_weight(w: QuantizedWeight) -> F6Weight:
+    """bf6 form of a 4-bit tiled weight (no counterpart in the reference)."""
+    if w.bits != 4:
+        raise ClefError(-1, "unsupported integer projection shape")
+    codes = torch.empty(w.rows * w.cols * 3 // 4, dtype=torch.uint8, device=w.codes.device)
+    _check(lib().clef_i4_f6_weight(_ptr(w.codes), w.rows, w.cols, _ptr(codes), _stream()))
+    return F6Weight(codes, w.scales, w.rows, w.cols)
+
+
+def f6_activation(a: Prepared, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf6 rows [rows][width * 3/4] of a 4-bit prepared activation."""
+    if a.bits != 4:
+        raise ClefError(-1, "unsupported integer projection shape")
+    if out is None:
+        out = torch.empty((a.rows, a.width * 3 // 4), dtype=torch.uint8, device=a.storage.device)
+    _check(lib().clef_i4_f6_activation(_ptr(a.storage), a.stride, a.rows, a.width, _ptr(out), _stream()))
+    return out
+
+
+def gemm_f6(a_f6: torch.Tensor, a_scales: torch.Tensor, w: F6Weight, residual: torch.Tensor | None = None,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+    """G1 on bf6 operands: equal to project_prepared on the operands they came from."""
+    rows = a_f6.shape[0]
+    if out is None:
+        out = _empty((rows, w.rows), torch.bfloat16, a_f6.device)
+    _check(lib().clef_i4_gemm_f6(_ptr(a_f6), _ptr(a_scales), _ptr(w.codes), _ptr(w.scales), rows, w.rows, w.cols,
+                                 _ptr(residual), _ptr(out), _stream()))
+    return out
+
+
+def project_prepared_f6(a: Prepared, w: F6Weight, residual: torch.Tensor | None = None,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """project_prepared through the bf6 GEMM: the activation re-encoded, then G1."""
+    if a.width != w.cols:
+        raise ClefError(-1, "unsupported integer projection shape")
+    return gemm_f6(f6_activation(a), a.scales, w, residual, out)
 
 
 def project_quantized(x: torch.Tensor, w: QuantizedWeight, residual: torch.Tensor | None = None

@@ -93,6 +93,11 @@ __device__ __forceinline__ uint32_t silu_lut_offset(uint32_t w, bool& inside) {
   return ((t >> 15) & 0x1FFFu) | ((w >> 18) & ~0x1FFFu);  // w >> 18 < 2^14: bit 13 is the sign
 }
 
+// Makes v opaque to the compiler (an empty asm that "changes" it in its
+// VGPR): later uses take the register, never a re-read of the memory it came
+// from. For values read from LDS that other lanes overwrite afterwards.
+__device__ __forceinline__ void pin_vgpr(float& v) { asm volatile("" : "+v"(v)); }
+
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 typedef int16_t s16x2 __attribute__((ext_vector_type(2)));
 

@@ -410,8 +410,8 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
         }
 #pragma unroll
         for (int s = 0; s < RB; ++s)
-          __builtin_amdgcn_raw_buffer_store_b128(v4i{(int)v[s].x, (int)v[s].y, (int)v[s].z, (int)v[s].w}, out_rsrc,
-                                                 (int)(dst[s] + (col0 + 8 * (lane & 3)) * 2), 0, 0);
+          store_b128(out_rsrc, (int)(dst[s] + (col0 + 8 * (lane & 3)) * 2),
+                     v4i{(int)v[s].x, (int)v[s].y, (int)v[s].z, (int)v[s].w});
       };
       auto values = [&](auto fast_tag) {
         constexpr bool FAST = decltype(fast_tag)::value;

@@ -16,48 +16,11 @@
 #include "gemm_dmah.hpp"
 #include "expert_persist.hpp"
 #include "kernels.hpp"
+#include "launch.hpp"
 
 namespace clef {
 
 namespace {
-
-constexpr float kBf16Max = 3.3895313892515355e38f;
-
-// Per-device launch facts of one kernel: whether its dynamic LDS limit has
-// been raised (an attribute HIP keeps per device) and how many of its
-// workgroups a CU holds. Devices 0..31 are cached, safe to share between host
-// threads; any other device is queried on every launch.
-struct LaunchCache {
-  std::atomic<uint32_t> lds_set{0};
-  std::atomic<int> per_cu[32] = {};
-};
-
-hipError_t current_device(int& dev) { return hipGetDevice(&dev); }
-
-hipError_t ensure_dynamic_lds(LaunchCache& c, const void* kern, int bytes) {
-  int dev = 0;
-  if (hipError_t e = current_device(dev)) return e;
-  const uint32_t bit = dev >= 0 && dev < 32 ? 1u << dev : 0u;
-  if (bit && (c.lds_set.load(std::memory_order_acquire) & bit)) return hipSuccess;
-  if (hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes)) return e;
-  c.lds_set.fetch_or(bit, std::memory_order_release);
-  return hipSuccess;
-}
-
-// Workgroups per CU (at least 1) and the CU count of the current device.
-hipError_t resident_per_cu(LaunchCache& c, const void* kern, int threads, int lds_bytes, int& per_cu, int& cus) {
-  int dev = 0;
-  if (hipError_t e = current_device(dev)) return e;
-  if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) return e;
-  const bool cached = dev >= 0 && dev < 32;
-  per_cu = cached ? c.per_cu[dev].load(std::memory_order_relaxed) : 0;
-  if (per_cu > 0) return hipSuccess;
-  int nb = 0;
-  if (hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, threads, lds_bytes)) return e;
-  per_cu = nb > 0 ? nb : 1;
-  if (cached) c.per_cu[dev].store(per_cu, std::memory_order_relaxed);
-  return hipSuccess;
-}
 
 template <int SHIFT = 8>
 __device__ __forceinline__ uint32_t g1_value(int32_t acc, float ws, float as) {
@@ -189,22 +152,6 @@ __device__ __forceinline__ void dense_epilogue(const v16i (&acc)[T::TM][T::TN], 
   }
 }
 
-// Block -> output tile. Workgroups are dispatched round-robin over the 8
-// XCDs (block b runs on XCD b % 8), so block b is renumbered to make each
-// XCD's blocks consecutive, then the renumbered order walks 8-tile-tall
-// column bands: 32 co-resident blocks of one XCD cover an 8 x 4 patch and
-// share its A and B panels in that XCD's L2.
-__device__ __forceinline__ void tile_of_block(int64_t b, int64_t blocks, int tiles_m, int tiles_n,
-                                              int64_t& tm, int& tn) {
-  const int64_t per = blocks / 8;
-  const int64_t r = b < 8 * per ? (b % 8) * per + b / 8 : b;
-  const int64_t band = 8 * (int64_t)tiles_n;
-  const int64_t group = r / band, within = r - group * band;
-  const int64_t first = group * 8;
-  const int64_t height = tiles_m - first < 8 ? tiles_m - first : 8;
-  tm = first + within % height;
-  tn = (int)(within / height);
-}
 
 template <class T, bool RESID>
 __global__ __launch_bounds__(T::THREADS) void gemm_dma_kernel(
@@ -322,8 +269,12 @@ __device__ __forceinline__ EpiScales<T> epi_scales_from_lds(const char* __restri
   bool ok = true;
   float amax = 0.0f, amin = inf, wmax = 0.0f, wmin = inf;
 #pragma unroll
+  // The staged store overwrites this block (other lanes' rows) after these
+  // reads, so every scale is pinned in a register: the compiler may not
+  // re-read it from LDS later (per thread the location looks unchanged).
   for (int i = 0; i < T::TM; ++i) {
     e.asr[i] = *reinterpret_cast<const float*>(wlds + (32 * i + lr) * 4);
+    pin_vgpr(e.asr[i]);
     const float a = e.asr[i];
     if (m0 + wm * T::WM + 32 * i + lr < M) {
       ok = ok && a > 0.0f && a < inf;
@@ -336,6 +287,10 @@ __device__ __forceinline__ EpiScales<T> epi_scales_from_lds(const char* __restri
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       e.wsr[j][q] = *reinterpret_cast<const float4*>(wlds + 512 + (32 * j + 8 * q + 4 * h) * 4);
+      pin_vgpr(e.wsr[j][q].x);
+      pin_vgpr(e.wsr[j][q].y);
+      pin_vgpr(e.wsr[j][q].z);
+      pin_vgpr(e.wsr[j][q].w);
       const float w4[4] = {e.wsr[j][q].x, e.wsr[j][q].y, e.wsr[j][q].z, e.wsr[j][q].w};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -425,7 +380,7 @@ __device__ __forceinline__ void staged_epilogue_store(const v16i (&acc)[T::TM][T
           v[t] = pack_bf16x2(bf16_lo(rr) + bf16_lo(p), bf16_hi(rr) + bf16_hi(p));
         }
       }
-      __builtin_amdgcn_raw_buffer_store_b128(v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]}, out_rsrc, voff, soff, 0);
+      store_b128(out_rsrc, voff + soff, v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]});
     }
   }
 }

@@ -66,6 +66,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// 16-byte buffer store with a zero scalar offset. A buffer store of more than
+// 8 bytes reads its data VGPRs after issue, so a VALU write to them must not
+// follow at once (one wait state). The compiler inserts that wait only for
+// stores whose soffset is not an SGPR; with an SGPR soffset the data was
+// measured to be overwritten on gfx950 (the last lanes of each 16-lane group
+// stored the next value of the register). Callers fold any scalar part of
+// the offset into `voff`.
+__device__ __forceinline__ void store_b128(__amdgpu_buffer_rsrc_t rsrc, int voff, v4i v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, 0, 0);
+}
+
 // s_waitcnt vmcnt(n) with the other counters unconstrained (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

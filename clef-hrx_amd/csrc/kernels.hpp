@@ -35,6 +35,13 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* a_scales,
 // INT8 x INT8 G1 (codes 4 per word, weights tiled as retile_codes with bits 8).
 hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream);
+// bf6 (e3m2) operands for G1 (gemm_f6.hip): packed activation rows -> bf6
+// rows of k * 3/4 bytes; tiled INT4 weight -> bf6 tiled weight; the GEMM on
+// them (k % 128 == 0, n % 256 == 0).
+hipError_t launch_f6_rows(const uint32_t* a, int a_words, int64_t rows, int k, uint8_t* out, hipStream_t stream);
+hipError_t launch_f6_tiled(const uint32_t* w_tiled, int64_t n, int k, uint8_t* out, hipStream_t stream);
+hipError_t launch_gemm_f6(const uint8_t* a, const float* as, const uint8_t* w, const float* ws, int64_t m, int n,
+                          int k, const uint16_t* residual, uint16_t* out, hipStream_t stream);
 // Records msg as clef_last_error() of this thread; returns CLEF_EINVAL.
 int set_last_error(const char* msg);
 // G1 tile configurations (clef_i4_gemm_config): 128x128 tiles, 256x256

@@ -191,6 +191,32 @@ int clef_i4_gemm_config(const uint32_t* a, int32_t k_stride, const float* a_scal
                         clef_stream_t stream);
 int clef_i4_gemm_configs(void);
 
+/* bf6 form of G1's operands (no counterpart in the reference: a gfx950
+ * re-encoding of the same INT4 codes). Every code -8..7 is exact in bf6
+ * (e3m2), so v_mfma_scale_f32_32x32x64_f8f6f4 on these operands gives the
+ * exact integer dot products, and clef_i4_gemm_f6 returns exactly what
+ * clef_i4_gemm returns for the operands they were made from, with no
+ * unpacking in the GEMM and twice the int8 MFMA's k per instruction.
+ * - clef_i4_f6_activation: packed activation codes (as clef_i4_gemm's `a`,
+ *   row pitch k_stride/8 words) -> bf6 rows: value k of a row at bits 6k of
+ *   the row's k*3/4 bytes. Preconditions: rows >= 1, k % 128 == 0,
+ *   k_stride >= k, k_stride % 32 == 0 -> "unsupported integer projection
+ *   shape"; 16-byte aligned pointers.
+ * - clef_i4_f6_weight: tiled weight codes (clef_i4_retile, bits 4, [n][k])
+ *   -> bf6 tiled weight: 128-row x 128-k blocks of 96-byte rows (12 KiB) at
+ *   ((row/128)*(k/128) + k/128)*12288, the 16-byte chunk c of block row r
+ *   stored at chunk c ^ ((r >> 3) & 1); n*k*3/4 bytes. Preconditions:
+ *   n % 128 == 0, k % 256 == 0 -> "unsupported integer projection shape".
+ * - clef_i4_gemm_f6: G1 on them, with clef_i4_gemm's epilogue and residual.
+ *   Preconditions: m >= 1, n % 256 == 0, k % 256 == 0, k >= 256 ->
+ *   "unsupported integer projection shape"; 16-byte aligned pointers. */
+int clef_i4_f6_activation(const uint32_t* a, int32_t k_stride, int64_t rows, int32_t k, uint8_t* out,
+                          clef_stream_t stream);
+int clef_i4_f6_weight(const uint32_t* w_tiled, int64_t n, int32_t k, uint8_t* out, clef_stream_t stream);
+int clef_i4_gemm_f6(const uint8_t* a_f6, const float* a_scales, const uint8_t* w_f6, const float* w_scales,
+                    int64_t m, int32_t n, int32_t k, const uint16_t* residual, uint16_t* out,
+                    clef_stream_t stream);
+
 /* Bytes of scratch clef_i4_project needs (the packed activation). */
 size_t clef_i4_project_workspace_bytes(int64_t m, int32_t k);
 

@@ -739,3 +739,159 @@ def test_c1_linear_full_output():
     for cfg in range(clef_i4.gemm_configs()):
         got = clef_i4.project_prepared(a, qw, config=cfg)
         assert_same_u16(bf16_host(got), want, f"c1 config={cfg}")
+
+
+# ---------------------------------------------------------------- bf6 G1
+# The bf6 (e3m2) re-encoding of G1's operands (clef_i4_f6_activation,
+# clef_i4_f6_weight, clef_i4_gemm_f6) must give exactly what G1 gives on the
+# INT4 operands they came from.
+
+E3M2 = np.array([0x00, 0x0C, 0x10, 0x12, 0x14, 0x15, 0x16, 0x17,
+                 0x38, 0x37, 0x36, 0x35, 0x34, 0x32, 0x30, 0x2C], dtype=np.uint64)
+
+
+def e3m2_value(bits):
+    """Value of e3m2 bits (sign, exponent with bias 3, 2 mantissa bits)."""
+    bits = np.asarray(bits, dtype=np.int64)
+    sign = np.where(bits & 0x20, -1.0, 1.0)
+    e, m = (bits >> 2) & 7, bits & 3
+    return sign * np.where(e == 0, m / 4.0 * 2.0 ** -2, (1 + m / 4.0) * 2.0 ** (e - 3))
+
+
+def test_e3m2_table_is_exact_for_every_int4_code():
+    codes = np.arange(16)
+    signed = np.where(codes < 8, codes, codes - 16)
+    assert np.array_equal(e3m2_value(E3M2), signed.astype(np.float64))
+
+
+def f6_rows_numpy(codes_u32: np.ndarray, k: int) -> np.ndarray:
+    """bf6 rows of packed codes ([rows][words], nibble p of word q = column
+    8q+p): value j at bits 6j of the row's k*3/4 bytes."""
+    rows = codes_u32.shape[0]
+    nib = (codes_u32[:, : k // 8, None] >> (4 * np.arange(8, dtype=np.uint32))) & 15
+    v = E3M2[nib.reshape(rows, k)]  # [rows][k] 6-bit values
+    v = v.reshape(rows, k // 32, 32)
+    words = np.zeros((rows, k // 32, 3), dtype=np.uint64)  # 64-bit words: 32 values = 192 bits
+    for j in range(32):
+        bit = 6 * j
+        words[:, :, bit // 64] |= v[:, :, j] << np.uint64(bit % 64)
+        if bit % 64 > 58:
+            words[:, :, bit // 64 + 1] |= v[:, :, j] >> np.uint64(64 - bit % 64)
+    return words.reshape(rows, -1).view(np.uint8).reshape(rows, k * 3 // 4)
+
+
+def test_f6_converters_match_numpy_layout():
+    """Activation rows plainly packed; tiled weight in 12 KiB blocks of 96-byte
+    rows with chunk c of block row r at c ^ ((r >> 3) & 1)."""
+    rng = np.random.default_rng(61)
+    m, n, k = 37, 256, 768
+    x, w, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
+    a_codes = a_codes.copy()
+    a_codes[0, : k // 8] = 0x89ABCDEF  # every negative code, -8 included
+    storage = np.concatenate([a_codes.reshape(-1), a_scales.view(np.uint32)])
+    a = clef_i4.Prepared(to_dev_u32(storage), m, k, stride, 4)
+    got = clef_i4.f6_activation(a).cpu().numpy()
+    assert np.array_equal(got, f6_rows_numpy(a_codes, k))
+    # weight: untile the reference layout to rows, pack, then block + swizzle
+    kb4 = k // 256
+    rows_u32 = w_tiled.reshape(n // 128, kb4, 128, 32).transpose(0, 2, 1, 3).reshape(n, k // 8)
+    flat = f6_rows_numpy(rows_u32, k)  # [n][k*3/4]
+    blocks = flat.reshape(n // 128, 128, k // 128, 6, 16)  # panel, row, k-block, chunk, byte
+    swz = np.empty_like(blocks)
+    for r in range(128):
+        s = (r >> 3) & 1
+        for c in range(6):
+            swz[:, r, :, c ^ s] = blocks[:, r, :, c]
+    want_w = swz.transpose(0, 2, 1, 3, 4).reshape(-1)
+    qw = dev_weight(w_tiled, w_scales, n, k)
+    got_w = clef_i4.f6_weight(qw).codes.cpu().numpy()
+    assert np.array_equal(got_w, want_w)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 256, 256), (17, 256, 768), (128, 512, 2048), (300, 768, 1024),
+                                   (257, 512, 4096), (64, 1024, 12288)])
+def test_gemm_f6_matches_oracle(m, n, k):
+    rng = np.random.default_rng(m * 11 + n + k)
+    x, w, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
+    want = oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k)
+    a = dev_prepared(x, stride)
+    fw = clef_i4.f6_weight(dev_weight(w_tiled, w_scales, n, k))
+    got = clef_i4.project_prepared_f6(a, fw)
+    assert_same_u16(bf16_host(got), want, f"gemm_f6 m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("m", [1, 129, 256, 257, 4032])
+def test_gemm_f6_residual_matches_oracle(m):
+    n, k = 256, 1024
+    rng = np.random.default_rng(m + 5)
+    x, w, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
+    res = randn_bf16(rng, (m, n), std=4.0)
+    want = oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k, residual=res)
+    a = dev_prepared(x, stride)
+    fw = clef_i4.f6_weight(dev_weight(w_tiled, w_scales, n, k))
+    got = clef_i4.project_prepared_f6(a, fw, residual=to_dev_bf16(res))
+    assert_same_u16(bf16_host(got), want, f"gemm_f6 residual m={m}")
+
+
+@pytest.mark.parametrize("resid", [False, True])
+def test_gemm_f6_several_tiles_per_workgroup(resid):
+    """M8292 N4096 K512: 33 x 16 tiles, two or three per persistent
+    workgroup, ragged last row tile; the whole output equals G1's."""
+    m, n, k = 8292, 4096, 512
+    rng = np.random.default_rng(77 + resid)
+    x, w, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
+    a = dev_prepared(x, stride)
+    qw = dev_weight(w_tiled, w_scales, n, k)
+    res = to_dev_bf16(randn_bf16(rng, (m, n), std=2.0)) if resid else None
+    want = bf16_host(clef_i4.project_prepared(a, qw, residual=res))
+    got = bf16_host(clef_i4.project_prepared_f6(a, clef_i4.f6_weight(qw), residual=res))
+    assert_same_u16(got, want, f"gemm_f6 several tiles resid={resid}")
+    rows = [0, 1, 255, 256, 4097, 8191, 8291]
+    sub = oracle.gemm(a_codes[rows], a_scales[rows], w_tiled, w_scales, n, k,
+                      residual=bf16_host(res)[rows] if resid else None)
+    assert_same_u16(got[rows], sub, "gemm_f6 sampled rows vs oracle")
+
+
+def test_gemm_f6_extreme_codes_and_saturation():
+    """Codes -8 and +7 (|acc| up to 64 K), huge scales (clamp), infinite and
+    NaN activation scales, as test_gemm_extreme_codes_and_saturation."""
+    m, n, k = 64, 256, 4096
+    stride = oracle.activation_stride(k)
+    a_words = np.full((m, stride // 8), 0x77777777, dtype=np.uint32)
+    a_words[1::2, : k // 8] = 0x88888888  # -8
+    w_codes = np.full((n, stride // 8), 0x88888888, dtype=np.uint32)
+    w_codes[::3, : k // 8] = 0x77777777
+    w_codes[1::7, : k // 8] = 0x0F1E2D3C
+    w_tiled = oracle.retile(w_codes, k)
+    a_scales = np.full(m, 1e30, dtype=np.float32)
+    a_scales[5] = np.inf
+    a_scales[6] = np.nan
+    a_scales[7] = 1e-3
+    a_scales[8:12] = [1e-38, 2e-45, 0.0, -3.0]
+    w_scales = np.full(n, 1e10, dtype=np.float32)
+    w_scales[::5] = 1e-30
+    want = oracle.gemm(a_words, a_scales, w_tiled, w_scales, n, k)
+    storage = np.concatenate([a_words.reshape(-1), a_scales.view(np.uint32)])
+    a = clef_i4.Prepared(to_dev_u32(storage), m, k, stride, 4)
+    got = clef_i4.project_prepared_f6(a, clef_i4.f6_weight(dev_weight(w_tiled, w_scales, n, k)))
+    assert_same_bf16_nan_aware(bf16_host(got), want, "gemm_f6 extreme")
+
+
+def test_gemm_f6_zero_rows_give_positive_zero():
+    """An all-zero activation row against negative weights: the MFMA's f32 sum
+    of -0 products is -0, and the epilogue's + 0 must still give +0 as G1's
+    integer accumulator does."""
+    m, n, k = 3, 256, 512
+    stride = oracle.activation_stride(k)
+    a_words = np.zeros((m, stride // 8), dtype=np.uint32)
+    a_words[1, : k // 8] = 0x11111111
+    w_codes = np.full((n, stride // 8), 0x99999999, dtype=np.uint32)
+    w_tiled = oracle.retile(w_codes, k)
+    a_scales = np.ones(m, dtype=np.float32)
+    w_scales = np.ones(n, dtype=np.float32)
+    want = oracle.gemm(a_words, a_scales, w_tiled, w_scales, n, k)
+    assert (want[0] == 0).all() and (want[2] == 0).all()
+    storage = np.concatenate([a_words.reshape(-1), a_scales.view(np.uint32)])
+    a = clef_i4.Prepared(to_dev_u32(storage), m, k, stride, 4)
+    got = clef_i4.project_prepared_f6(a, clef_i4.f6_weight(dev_weight(w_tiled, w_scales, n, k)))
+    assert_same_u16(bf16_host(got), want, "gemm_f6 zero rows")
