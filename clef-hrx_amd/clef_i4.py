@@ -49,6 +49,9 @@ SIGNATURES = {
     "clef_i4_f6_activation": (ctypes.c_int, [_P, _I32, _I64, _I32, _P, _P]),
     "clef_i4_f6_weight": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
     "clef_i4_gemm_f6": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P]),
+    "clef_i4_f6_prepared_bytes": (ctypes.c_int64, [_I64, _I32]),
+    "clef_i4_prepare_f6": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
+    "clef_i4_prepare_swiglu_f6": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _P]),
     "clef_i4_project_workspace_bytes": (_SZ, [_I64, _I32]),
     "clef_i4_project": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _I32, _P, _P, _P, _SZ, _P]),
     "clef_moe_router_logits": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P]),
@@ -471,6 +474,59 @@ def gemm_f6(a_f6: torch.Tensor, a_scales: torch.Tensor, w: F6Weight, residual: t
     _check(lib().clef_i4_gemm_f6(_ptr(a_f6), _ptr(a_scales), _ptr(w.codes), _ptr(w.scales), rows, w.rows, w.cols,
                                  _ptr(residual), _ptr(out), _stream()))
     return out
+
+
+@dataclass
+class PreparedF6:
+    """Q1 output in bf6 form (clef_i4_prepare_f6): one uint8 buffer holding
+    rows x width*3/4 bytes of e3m2 codes, then rows f32 scales."""
+    storage: torch.Tensor  # uint8 [rows * (width * 3/4 + 4)]
+    rows: int
+    width: int
+
+    @property
+    def codes(self) -> torch.Tensor:
+        return self.storage[: self.rows * self.width * 3 // 4].view(self.rows, self.width * 3 // 4)
+
+    @property
+    def scales(self) -> torch.Tensor:
+        start = self.rows * self.width * 3 // 4
+        return self.storage[start: start + 4 * self.rows].view(torch.float32)
+
+
+def _prepared_f6_storage(rows: int, width: int, device, out: torch.Tensor | None) -> torch.Tensor:
+    nbytes = int(lib().clef_i4_f6_prepared_bytes(rows, width))
+    if out is None:
+        return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+    if out.dtype != torch.uint8 or out.numel() < nbytes:
+        raise ClefError(-1, "bf6 activation buffer too small")
+    return out
+
+
+def prepare_f6(x: torch.Tensor, out: torch.Tensor | None = None) -> PreparedF6:
+    """prepare (bits 4) with the codes written as bf6: the same codes and
+    scales as prepare followed by f6_activation, in one pass."""
+    rows, width = x.shape
+    out = _prepared_f6_storage(rows, width, x.device, out)
+    _check(lib().clef_i4_prepare_f6(_ptr(x), rows, width, _ptr(out), _stream()))
+    return PreparedF6(out, rows, width)
+
+
+def prepare_swiglu_f6(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> PreparedF6:
+    """prepare_swiglu (bits 4) with the codes written as bf6."""
+    rows, width = gate.shape
+    out = _prepared_f6_storage(rows, width, gate.device, out)
+    _check(lib().clef_i4_prepare_swiglu_f6(_ptr(gate), _ptr(up), rows, width, _ptr(out), _stream()))
+    return PreparedF6(out, rows, width)
+
+
+def project_f6(a: PreparedF6, w: F6Weight, residual: torch.Tensor | None = None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """G1 through the bf6 GEMM on a bf6-prepared activation: equal to
+    project_prepared(prepare(x), w) for the weight w came from."""
+    if a.width != w.cols:
+        raise ClefError(-1, "unsupported integer projection shape")
+    return gemm_f6(a.codes, a.scales, w, residual, out)
 
 
 def project_prepared_f6(a: Prepared, w: F6Weight, residual: torch.Tensor | None = None,

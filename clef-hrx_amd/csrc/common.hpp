@@ -98,6 +98,16 @@ __device__ __forceinline__ uint32_t silu_lut_offset(uint32_t w, bool& inside) {
 // from. For values read from LDS that other lanes overwrite afterwards.
 __device__ __forceinline__ void pin_vgpr(float& v) { asm volatile("" : "+v"(v)); }
 
+// e3m2 (bf6: sign, 3 exponent bits with bias 3, 2 mantissa bits) of the int4
+// code held in nibble n (two's complement); every code -8..7 is exact.
+__host__ __device__ constexpr uint32_t e3m2_of_nibble(uint32_t n) {
+  // magnitudes 0..7: 0, 1.0*2^0, 1.0*2^1, 1.5*2^1, 1.0*2^2, 1.25*2^2, 1.5*2^2, 1.75*2^2
+  constexpr uint64_t kPos = 0x1716151412100C00ull;
+  const uint32_t m = n < 8 ? n : 16 - n;  // |code|, 8 for n == 8
+  const uint32_t mag = m == 8 ? 0x18u : (uint32_t)(kPos >> (8 * m)) & 0xFFu;
+  return n < 8 ? mag : (mag | 0x20u);
+}
+
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 typedef int16_t s16x2 __attribute__((ext_vector_type(2)));
 

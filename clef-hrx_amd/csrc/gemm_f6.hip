@@ -24,10 +24,10 @@
 //    c ^ ((r >> 3) & 1) (the LDS swizzle, applied on the global side).
 //
 // Tile: 256 x 256 outputs per workgroup of 8 waves (2 x 4 waves of 128 rows x
-// 64 columns), k-steps of 128 k (48 KiB of LDS per stage, two stages), a
+// 64 columns), k-steps of 128 k (48 KiB of LDS per stage, three stages), a
 // persistent grid walking tiles on the workgroup's XCD; while a k-step
-// computes, the DMA of the next one (or of the next tile's first) fills the
-// other stage. Lane half h of a 32-row fragment reads bytes 48h .. 48h+47 of
+// computes, the DMAs of the next two (running into the next tile's first)
+// fill the other stages. Lane half h of a 32-row fragment reads bytes 48h .. 48h+47 of
 // the row's 96 (k = 64h .. 64h+63): the first 24 are the operand of the
 // k-step's first MFMA, the last 24 of its second; A and B use the same map,
 // so the two MFMAs of a k-step together cover its 128 k exactly once.
@@ -47,15 +47,6 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef unsigned f6_v2u __attribute__((ext_vector_type(2)));
 typedef unsigned f6_v4u __attribute__((ext_vector_type(4)));
-
-// e3m2 bits of the int4 code held in nibble n (two's complement).
-__host__ __device__ constexpr uint32_t e3m2_of_nibble(uint32_t n) {
-  // magnitudes 0..7: 0, 1.0*2^0, 1.0*2^1, 1.5*2^1, 1.0*2^2, 1.25*2^2, 1.5*2^2, 1.75*2^2
-  constexpr uint64_t kPos = 0x1716151412100C00ull;
-  const uint32_t m = n < 8 ? n : 16 - n;  // |code|, 8 for n == 8
-  const uint32_t mag = m == 8 ? 0x18u : (uint32_t)(kPos >> (8 * m)) & 0xFFu;
-  return n < 8 ? mag : (mag | 0x20u);
-}
 
 // 32 codes (four packed words, code j in nibble j % 8 of word j / 8) -> 32
 // e3m2 values, value j at bits 6j of out[0..5].

@@ -16,6 +16,10 @@
 // returns natural order so each lane packs two (int4) or four (int8) whole
 // words. A 256-thread workgroup holds 16 groups: 16/G rows of G groups when
 // the row has G <= 16 groups, else one row over P passes kept in registers.
+//
+// A third output form (this library's, for the bf6 projection): the INT4
+// codes written as e3m2 values, 6 bits each, value c of a row at bits 6c of
+// its width * 3/4 bytes, with the same f32 row scales after the rows.
 #include "common.hpp"
 #include "silu_table.hpp"
 #include "kernels.hpp"
@@ -221,6 +225,47 @@ __device__ __forceinline__ uint32_t pack_codes(const float* v, float inv, bool v
   return valid ? word : 0u;
 }
 
+// The 16 codes clamp(rint(v * inv), -7, 7) of one lane as e3m2 (exact for
+// these integers), value i at bits 6i of o[0..2]: the bf6 form of the INT4
+// codes, for the bf6 projection.
+__device__ __forceinline__ void pack_codes_f6(const float* v, float inv, bool valid, uint32_t (&o)[3]) {
+  constexpr float magic = 12582912.0f;  // as in pack_codes
+  o[0] = o[1] = o[2] = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float t = v[i] * inv + magic;
+    t = __builtin_fminf(__builtin_fmaxf(t, magic - 7.0f), magic + 7.0f);
+    const uint32_t e = e3m2_of_nibble(as_uint(t) & 0xfu);
+    const int bit = 6 * i, d = bit >> 5, sh = bit & 31;
+    o[d] |= e << sh;
+    if (sh > 26) o[d + 1] |= e >> (32 - sh);
+  }
+  if (!valid) o[0] = o[1] = o[2] = 0;
+}
+
+// Codes of the 16 values at column col of a row whose output starts at
+// row_out: BITS 4 and 8 pack two's complement fields (32 / BITS per word),
+// BITS 6 writes bf6 (12 bytes at byte col * 3/4).
+template <int BITS>
+__device__ __forceinline__ void store_codes(uint32_t* row_out, int col, const float* nat, float inv, bool valid) {
+  if constexpr (BITS == 4) {
+    *reinterpret_cast<uint2*>(row_out + col / 8) =
+        make_uint2(pack_codes<4>(nat, inv, valid), pack_codes<4>(nat + 8, inv, valid));
+  } else if constexpr (BITS == 8) {
+    *reinterpret_cast<uint4*>(row_out + col / 4) =
+        make_uint4(pack_codes<8>(nat, inv, valid), pack_codes<8>(nat + 4, inv, valid),
+                   pack_codes<8>(nat + 8, inv, valid), pack_codes<8>(nat + 12, inv, valid));
+  } else {
+    static_assert(BITS == 6, "codes of 4 or 8 bits, or bf6");
+    uint32_t o[3];
+    pack_codes_f6(nat, inv, valid, o);
+    uint32_t* dst = row_out + col * 3 / 16;
+    dst[0] = o[0];
+    dst[1] = o[1];
+    dst[2] = o[2];
+  }
+}
+
 template <int P, int BITS, class Src>
 __global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int width,
                                                       int out_words, uint32_t* __restrict__ out) {
@@ -333,7 +378,6 @@ __global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int
   const bool valid = scale < __builtin_huge_valf();
   const float inv = 0.0625f / scale;
 
-  constexpr int per = 32 / BITS;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int grp = grp0 + 16 * p;
@@ -352,17 +396,7 @@ __global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int
       nat[4 * c + 3] = t.w;
     }
     __syncthreads();
-    if (on) {
-      uint32_t* dst = out + row * out_words + (grp * 256 + 16 * L) / per;
-      if (BITS == 4) {
-        uint2 w = make_uint2(pack_codes<4>(nat, inv, valid), pack_codes<4>(nat + 8, inv, valid));
-        *reinterpret_cast<uint2*>(dst) = w;
-      } else {
-        uint4 w = make_uint4(pack_codes<8>(nat, inv, valid), pack_codes<8>(nat + 4, inv, valid),
-                             pack_codes<8>(nat + 8, inv, valid), pack_codes<8>(nat + 12, inv, valid));
-        *reinterpret_cast<uint4*>(dst) = w;
-      }
-    }
+    if (on) store_codes<BITS>(out + row * out_words, grp * 256 + 16 * L, nat, inv, valid);
   }
   if (active && grp0 == 0 && L == 0) {
     float* scales = reinterpret_cast<float*>(out + rows * out_words);
@@ -392,7 +426,6 @@ __device__ __forceinline__ void prepare_loop_body(Src src, int64_t rows, int wid
   const bool lane_on = row_local < rows_per_block;
   const int64_t nblk = (rows + rows_per_block - 1) / rows_per_block;
   float* buf = lds + lg * kGroupLds;
-  constexpr int per = 32 / BITS;
   constexpr float qmax = BITS == 8 ? 127.0f : 7.0f;
 
   // The row and its input and output offsets advance by one grid stride per
@@ -472,14 +505,7 @@ __device__ __forceinline__ void prepare_loop_body(Src src, int64_t rows, int wid
     }
     __syncthreads();
     if (on) {
-      uint32_t* dst = out + out_off + col / per;
-      if (BITS == 4) {
-        *reinterpret_cast<uint2*>(dst) = make_uint2(pack_codes<4>(nat, inv, valid), pack_codes<4>(nat + 8, inv, valid));
-      } else {
-        *reinterpret_cast<uint4*>(dst) = make_uint4(pack_codes<8>(nat, inv, valid), pack_codes<8>(nat + 4, inv, valid),
-                                                    pack_codes<8>(nat + 8, inv, valid),
-                                                    pack_codes<8>(nat + 12, inv, valid));
-      }
+      store_codes<BITS>(out + out_off, col, nat, inv, valid);
       if (grp == 0 && L == 0) reinterpret_cast<float*>(out + rows * out_words)[row] = scale;
     }
   }
@@ -540,9 +566,12 @@ hipError_t launch_prepare_bits(const Src& src, int64_t rows, int width, int out_
   return hipGetLastError();
 }
 
+// bits 4 or 8: packed codes of `stride` columns per row; bits 6: bf6 rows of
+// width * 3/4 bytes (stride == width).
 template <class Src>
 hipError_t launch_prepare_src(const Src& src, int64_t rows, int width, int stride, int bits,
                               uint32_t* out, hipStream_t stream) {
+  if (bits == 6) return launch_prepare_bits<6>(src, rows, width, width * 3 / 16, out, stream);
   const int out_words = stride / (32 / bits);
   if (bits == 4) return launch_prepare_bits<4>(src, rows, width, out_words, out, stream);
   return launch_prepare_bits<8>(src, rows, width, out_words, out, stream);

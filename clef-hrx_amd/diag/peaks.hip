@@ -4,6 +4,8 @@
 //     independent accumulators per wave, 4 waves per SIMD), for several
 //     operand forms: the board's power limit lowers the clock as operand bit
 //     activity rises, so the sustainable rate depends on the data;
+//   - v_mfma_scale_f32_32x32x64_f8f6f4 on bf6 operands (unit scales) the
+//     same way, zeros and the e3m2 form of the same gaussian int4 codes;
 //   - the shader clock under that load (s_memtime cycles against the 100 MHz
 //     s_memrealtime counter, read by one wave);
 //   - HBM streaming read, write and copy over 1 GiB buffers (well past the
@@ -19,6 +21,8 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned u4 __attribute__((ext_vector_type(4)));
 
 __device__ uint32_t mix(uint32_t x) {
@@ -72,6 +76,61 @@ __global__ __launch_bounds__(256) void mfma_kernel(int iters, int* out, unsigned
   for (int j = 0; j < 8; ++j)
     for (int e = 0; e < 16; ++e) s ^= acc[j][e];
   if (s == 0x7fffffff) out[t] = s;  // keeps the MFMAs live; never true in practice
+  if (timer && threadIdx.x == 0) {
+    const unsigned long long c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    clock[0] = c1 - c0;
+    clock[1] = r1 - r0;
+  }
+}
+
+// A gaussian int4 code: round(2z) of a normal z, clamped to +-7.
+__device__ int gaussian_code(uint32_t seed) {
+  const uint32_t h1 = mix(seed), h2 = mix(seed ^ 0x9e3779b9u);
+  const float u1 = (h1 >> 8) * (1.0f / 16777216.0f) + 1e-7f, u2 = (h2 >> 8) * (1.0f / 16777216.0f);
+  const float r = sqrtf(-2.0f * logf(u1));
+  return (int)rintf(fminf(fmaxf(2.0f * r * cosf(6.2831853f * u2), -7.0f), 7.0f));
+}
+
+// e3m2 bits of an integer code -7..7.
+__device__ uint32_t e3m2_code(int c) {
+  const uint32_t mag[8] = {0x00, 0x0C, 0x10, 0x12, 0x14, 0x15, 0x16, 0x17};
+  return c < 0 ? (mag[-c] | 0x20u) : mag[c];
+}
+
+// bf6 operand forms: 0 zeros; 1 the e3m2 codes of gaussian int4 codes, 32
+// per lane in six words (value j at bits 6j).
+template <int FORM>
+__global__ __launch_bounds__(256) void mfma_f6_kernel(int iters, int* out, unsigned long long* clock) {
+  const uint32_t t = blockIdx.x * 256 + threadIdx.x;
+  v8i a = v8i{}, b = v8i{};
+  if (FORM == 1) {
+    for (int j = 0; j < 32; ++j) {
+      const uint32_t ea = e3m2_code(gaussian_code(t * 64 + j)), eb = e3m2_code(gaussian_code(t * 64 + 32 + j));
+      const int bit = 6 * j, d = bit >> 5, sh = bit & 31;
+      a[d] |= (int)(ea << sh);
+      b[d] |= (int)(eb << sh);
+      if (sh > 26) {
+        a[d + 1] |= (int)(ea >> (32 - sh));
+        b[d + 1] |= (int)(eb >> (32 - sh));
+      }
+    }
+  }
+  v16f acc[8];
+  for (int j = 0; j < 8; ++j) acc[j] = v16f{};
+  unsigned long long c0 = 0, r0 = 0;
+  const bool timer = blockIdx.x == 0 && threadIdx.x < 64;
+  if (timer) {
+    c0 = __builtin_amdgcn_s_memtime();
+    r0 = __builtin_amdgcn_s_memrealtime();
+  }
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc[j], 3, 3, 0, 127, 0, 127);
+  float s = 0.0f;
+  for (int j = 0; j < 8; ++j)
+    for (int e = 0; e < 16; ++e) s += acc[j][e];
+  if (s == 12345.678f) out[t] = 1;  // keeps the MFMAs live; never true in practice
   if (timer && threadIdx.x == 0) {
     const unsigned long long c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
     clock[0] = c1 - c0;
@@ -137,6 +196,29 @@ int main() {
     const double mhz = c[1] ? (double)c[0] / (double)c[1] * 100.0 : 0.0;
     std::printf("%s\"%s\": {\"tops\": %.1f, \"pct_of_5000\": %.1f, \"sclk_mhz\": %.0f}", f ? ", " : "", names[f],
                 ops / ms / 1e9, ops / ms / 1e9 / 50.0, mhz);
+  }
+  std::printf("}, \"mfma_bf6\": {");
+  const char* names6[2] = {"zeros", "int4_gaussian_codes_as_e3m2"};
+  for (int f = 0; f < 2; ++f) {
+    const int it6 = iters / 2;
+    auto launch = [&](int it) {
+      if (f == 0) mfma_f6_kernel<0><<<blocks, 256>>>(it, out, clk);
+      if (f == 1) mfma_f6_kernel<1><<<blocks, 256>>>(it, out, clk);
+    };
+    for (int w = 0; w < 3; ++w) launch(it6);
+    CHECK(hipDeviceSynchronize());
+    CHECK(hipEventRecord(e0));
+    launch(it6);
+    CHECK(hipEventRecord(e1));
+    CHECK(hipEventSynchronize(e1));
+    float ms = 0;
+    CHECK(hipEventElapsedTime(&ms, e0, e1));
+    unsigned long long c[2];
+    CHECK(hipMemcpy(c, clk, sizeof(c), hipMemcpyDeviceToHost));
+    const double ops = (double)blocks * 4 * it6 * 8 * 32.0 * 32 * 64 * 2;
+    const double mhz = c[1] ? (double)c[0] / (double)c[1] * 100.0 : 0.0;
+    std::printf("%s\"%s\": {\"tops\": %.1f, \"pct_of_10100\": %.1f, \"sclk_mhz\": %.0f}", f ? ", " : "",
+                names6[f], ops / ms / 1e9, ops / ms / 1e9 / 101.0, mhz);
   }
   std::printf("}, \"hbm_gbs\": {");
   const size_t bytes = 1ull << 30, n = bytes / 16;

@@ -207,12 +207,23 @@ int clef_i4_gemm_configs(void);
  *   ((row/128)*(k/128) + k/128)*12288, the 16-byte chunk c of block row r
  *   stored at chunk c ^ ((r >> 3) & 1); n*k*3/4 bytes. Preconditions:
  *   n % 128 == 0, k % 256 == 0 -> "unsupported integer projection shape".
+ * - clef_i4_prepare_f6 / clef_i4_prepare_swiglu_f6: Q1 (as clef_i4_prepare /
+ *   clef_i4_prepare_swiglu with bits 4) writing the codes as bf6 rows
+ *   directly: rows * width*3/4 bytes of codes, then rows f32 scales (at byte
+ *   rows * width*3/4); clef_i4_f6_prepared_bytes gives the size. Same codes
+ *   and scales as clef_i4_prepare then clef_i4_f6_activation, in one pass.
+ *   Preconditions as clef_i4_prepare (width % 256 == 0, 256 <= width <=
+ *   32768, 1 <= rows <= 2^20 -> "unsupported rotated integer operand").
  * - clef_i4_gemm_f6: G1 on them, with clef_i4_gemm's epilogue and residual.
  *   Preconditions: m >= 1, n % 256 == 0, k % 256 == 0, k >= 256 ->
  *   "unsupported integer projection shape"; 16-byte aligned pointers. */
 int clef_i4_f6_activation(const uint32_t* a, int32_t k_stride, int64_t rows, int32_t k, uint8_t* out,
                           clef_stream_t stream);
 int clef_i4_f6_weight(const uint32_t* w_tiled, int64_t n, int32_t k, uint8_t* out, clef_stream_t stream);
+int64_t clef_i4_f6_prepared_bytes(int64_t rows, int32_t width);
+int clef_i4_prepare_f6(const uint16_t* x, int64_t rows, int32_t width, uint8_t* out, clef_stream_t stream);
+int clef_i4_prepare_swiglu_f6(const uint16_t* gate, const uint16_t* up, int64_t rows, int32_t width,
+                              uint8_t* out, clef_stream_t stream);
 int clef_i4_gemm_f6(const uint8_t* a_f6, const float* a_scales, const uint8_t* w_f6, const float* w_scales,
                     int64_t m, int32_t n, int32_t k, const uint16_t* residual, uint16_t* out,
                     clef_stream_t stream);

@@ -895,3 +895,62 @@ def test_gemm_f6_zero_rows_give_positive_zero():
     a = clef_i4.Prepared(to_dev_u32(storage), m, k, stride, 4)
     got = clef_i4.project_prepared_f6(a, clef_i4.f6_weight(dev_weight(w_tiled, w_scales, n, k)))
     assert_same_u16(bf16_host(got), want, "gemm_f6 zero rows")
+
+
+def f6_prepared_numpy(codes_u32: np.ndarray, scales: np.ndarray, width: int) -> np.ndarray:
+    """clef_i4_prepare_f6's buffer from the oracle's INT4 codes and scales:
+    bf6 rows, then the f32 scales."""
+    return np.concatenate([f6_rows_numpy(codes_u32, width).reshape(-1),
+                           np.ascontiguousarray(scales, dtype=np.float32).view(np.uint8)])
+
+
+@pytest.mark.parametrize("width,rows", [(256, 5), (768, 37), (2048, 1000), (4096, 33), (8192, 3), (17408, 7)])
+def test_prepare_f6_matches_oracle(width, rows):
+    """The bf6 quantizer writes the oracle's INT4 codes as e3m2 and its
+    scales, byte for byte: both the grid-stride kernel (width <= 4096) and the
+    one-row kernel (more than 16 groups), random rows and the exceptional
+    rows (NaN, inf, bf16::MAX, zero)."""
+    rng = np.random.default_rng(width + rows)
+    x = np.concatenate([randn_bf16(rng, (rows, width), std=3.0), exceptional_rows(width)])
+    stride = oracle.activation_stride(width)
+    codes, scales, _ = oracle.prepare(x, stride)
+    got = clef_i4.prepare_f6(to_dev_bf16(x))
+    assert np.array_equal(got.storage.cpu().numpy(), f6_prepared_numpy(codes, scales, width)), \
+        f"prepare_f6 width={width} rows={rows}"
+
+
+@pytest.mark.parametrize("width", [768, 2048, 17408])
+def test_prepare_swiglu_f6_matches_oracle(width):
+    rng = np.random.default_rng(width + 3)
+    rows = 19
+    g = randn_bf16(rng, (rows, width), std=2.0)
+    u = randn_bf16(rng, (rows, width), std=2.0)
+    stride = oracle.activation_stride(width)
+    codes, scales, _ = oracle.prepare_swiglu(g, u, stride)
+    got = clef_i4.prepare_swiglu_f6(to_dev_bf16(g), to_dev_bf16(u))
+    assert np.array_equal(got.storage.cpu().numpy(), f6_prepared_numpy(codes, scales, width)), \
+        f"prepare_swiglu_f6 width={width}"
+
+
+def test_prepare_f6_equals_prepare_then_convert():
+    """M4096 K4096 (the benchmark activation): one pass gives what
+    clef_i4_prepare + clef_i4_f6_activation give, codes and scales."""
+    x = torch.randn((4096, 4096), generator=torch.Generator(device=DEV).manual_seed(5), device=DEV,
+                    dtype=torch.float32).to(torch.bfloat16)
+    a = clef_i4.prepare(x)
+    f = clef_i4.prepare_f6(x)
+    assert torch.equal(f.codes, clef_i4.f6_activation(a))
+    assert torch.equal(f.scales.view(torch.int32), a.scales.view(torch.int32))
+
+
+@pytest.mark.parametrize("m,n,k,resid", [(1, 256, 256, False), (300, 768, 1024, True), (257, 512, 4096, False)])
+def test_project_f6_matches_oracle(m, n, k, resid):
+    """bf16 x -> prepare_f6 -> gemm_f6 against the oracle's quantize + G1."""
+    rng = np.random.default_rng(m + n + k)
+    x, w, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
+    res = randn_bf16(rng, (m, n), std=4.0) if resid else None
+    want = oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k, residual=res)
+    fw = clef_i4.f6_weight(dev_weight(w_tiled, w_scales, n, k))
+    got = clef_i4.project_f6(clef_i4.prepare_f6(to_dev_bf16(x)), fw,
+                             residual=to_dev_bf16(res) if resid else None)
+    assert_same_u16(bf16_host(got), want, f"project_f6 m={m} n={n} k={k} resid={resid}")
