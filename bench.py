@@ -17,7 +17,9 @@ M=4096 on one MI355X.
                down 4096 x 12288: quantize -> GEMM -> SwiGLU+quantize -> GEMM.
   int8_gemm_*  the INT8 x INT8 projection at the GEMM's shape.
   small_m_*    M = 1, 16, 64 on the GEMM's weight (K4096 N12288): GPU time per
-               call (HIP graph replay) and HBM GB/s of the bytes the call moves.
+               call (HIP graph replay) and HBM GB/s of the bytes the call moves,
+               cycling through more weight copies than the last-level cache
+               holds; us_cached repeats one weight (cache-resident).
   linear_m512_k2048_n2048  the single INT4 linear M512 K2048 N2048: GPU time
                per call (graph replay), TOPS and HBM GB/s.
   attn_proj_*  INT4 attention projections at M=16384 (Q, K, V, O + residual).
@@ -163,20 +165,33 @@ def graph_timed(fn, calls=50, replays=8):
 def small_m_leg(args):
     """Decode-sized projections on the headline weight (K4096 N12288): the
     weight stream is the whole cost, so the figure of merit is HBM GB/s
-    (weight codes and scales, activation, output)."""
+    (weight codes and scales, activation, output). Two figures per M: `us`
+    cycles the calls through 14 copies of the weight (352 MB, more than the
+    256 MB last-level cache, as a multi-layer decode does), so every call
+    streams its weight from HBM; `us_cached` repeats one weight, which then
+    stays in the last-level cache."""
     import torch
 
     import clef_i4
 
     k, n = 4096, 12288
-    qw = clef_i4.load_quantized_weight(bf16_randn((n, k), 0.02, 1002 * 16 + 1))
+    w = bf16_randn((n, k), 0.02, 1002 * 16 + 1)
+    qws = [clef_i4.load_quantized_weight(w) for _ in range(14)]
+    del w
     res = {}
     for m in (1, 16, 64):
         a = clef_i4.prepare(bf16_randn((m, k), 1.0, 1002 * 16 + 0))
         out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-        ms = graph_timed(lambda: clef_i4.project_prepared(a, qw, out=out))
+        turn = [0]
+
+        def rotating():
+            turn[0] = (turn[0] + 1) % len(qws)
+            clef_i4.project_prepared(a, qws[turn[0]], out=out)
+
+        ms = graph_timed(rotating, calls=56)
+        ms_cached = graph_timed(lambda: clef_i4.project_prepared(a, qws[0], out=out))
         nbytes = n * k // 2 + 4 * n + m * (k // 2 + 4) + 2 * m * n
-        res[m] = {"us": ms * 1e3, "gbs": nbytes / ms / 1e6}
+        res[m] = {"us": ms * 1e3, "gbs": nbytes / ms / 1e6, "us_cached": ms_cached * 1e3}
     return res
 
 
@@ -506,7 +521,8 @@ def main():
         line["attn_proj_m16384_ms"] = round(res["attn"]["ms"], 4)
         line["attn_proj_tops"] = round(res["attn"]["tops"], 1)
     if "smallm" in res:
-        line["small_m_k4096_n12288"] = {f"m{m}": {"us": round(v["us"], 2), "hbm_gbs": round(v["gbs"], 1)}
+        line["small_m_k4096_n12288"] = {f"m{m}": {"us": round(v["us"], 2), "hbm_gbs": round(v["gbs"], 1),
+                                                  "us_cached": round(v["us_cached"], 2)}
                                         for m, v in res["smallm"].items()}
     if cpu:
         line["cpu_baseline"] = cpu

@@ -998,6 +998,27 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny_kernel(const uint32_t* __
   };
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
+  // Epilogue item g = (row block f, register quad rq, lane) gives row
+  // m0 + 32 f + lane % 32 and columns n0 + 8 rq + 4 (lane / 32) + 0..3. Its
+  // scales (and residual) are fetched here, with the first loads, so their
+  // latency is not paid again after the reduction; with more than one row
+  // block there is no register room for them (the kernel would spill).
+  constexpr int IPT = (MT * 256 + NW * 64 - 1) / (NW * 64);
+  constexpr bool PRE = MT == 1;
+  float e_as[IPT];
+  float4 e_ws[IPT];
+  uint2 e_res[IPT];
+#pragma unroll
+  for (int i = 0; i < IPT && PRE; ++i) {
+    const int g = threadIdx.x + i * NW * 64;
+    const int f = g >> 8, rq = (g >> 6) & 3, ln = g & 63;
+    const int64_t m = m0 + 32 * f + (ln & 31);
+    const int col = n0 + 8 * rq + 4 * (ln >> 5);
+    const bool ok = g < MT * 256 && m < M;
+    e_as[i] = ok ? as[m] : 0.0f;
+    e_ws[i] = ok ? *reinterpret_cast<const float4*>(ws + col) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    e_res[i] = RESID && ok ? *reinterpret_cast<const uint2*>(residual + m * N + col) : make_uint2(0, 0);
+  }
   const int k0 = wave * kb / NW, k1 = (wave + 1) * kb / NW;
   if (k0 < k1) {
     // The load after the last k-step repeats it (never used), so the body has
@@ -1019,21 +1040,21 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny_kernel(const uint32_t* __
     for (int r = 0; r < 16; ++r) atomicAdd(&red[f][r][lane], acc[f][r]);
   __syncthreads();
 
-  // Epilogue: item g = (row block f, register quad rq, lane) gives row
-  // m0 + 32 f + lane % 32 and columns n0 + 8 rq + 4 (lane / 32) + 0..3.
-  for (int g = threadIdx.x; g < MT * 256; g += NW * 64) {
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int g = threadIdx.x + i * NW * 64;
     const int f = g >> 8, rq = (g >> 6) & 3, ln = g & 63;
     const int64_t m = m0 + 32 * f + (ln & 31);
-    if (m >= M) continue;
+    if (g >= MT * 256 || m >= M) continue;
     const int col = n0 + 8 * rq + 4 * (ln >> 5);
-    const float asv = as[m];
-    const float4 wsv = *reinterpret_cast<const float4*>(ws + col);
+    const float asv = PRE ? e_as[i] : as[m];
+    const float4 wsv = PRE ? e_ws[i] : *reinterpret_cast<const float4*>(ws + col);
     constexpr int SH = I8 ? 0 : 8;
     uint32_t p0 = g1_value<SH>(red[f][4 * rq + 0][ln], wsv.x, asv) | (g1_value<SH>(red[f][4 * rq + 1][ln], wsv.y, asv) << 16);
     uint32_t p1 = g1_value<SH>(red[f][4 * rq + 2][ln], wsv.z, asv) | (g1_value<SH>(red[f][4 * rq + 3][ln], wsv.w, asv) << 16);
     uint16_t* dst = out + m * N + col;
     if (RESID) {
-      const uint2 rv = *reinterpret_cast<const uint2*>(residual + m * N + col);
+      const uint2 rv = PRE ? e_res[i] : *reinterpret_cast<const uint2*>(residual + m * N + col);
       p0 = pack_bf16x2(bf16_lo(rv.x) + bf16_lo(p0), bf16_hi(rv.x) + bf16_hi(p0));
       p1 = pack_bf16x2(bf16_lo(rv.y) + bf16_lo(p1), bf16_hi(rv.y) + bf16_hi(p1));
     }
@@ -1068,11 +1089,301 @@ hipError_t launch_skinny_any(const uint32_t* a, int a_words, const float* as, co
   return launch_skinny_m<false, I8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
 }
 
-// Few rows, INT4: the skinny kernel where 128x128 tiles would leave most CUs
-// idle (see launch_gemm_i4).
-bool use_skinny(int64_t m, int n) {
-  const int64_t tiles128 = (m + 127) / 128 * (n / 128);
-  return m <= 64 || (m <= 512 && tiles128 < 96);
+// Decode-sized G1 (M <= MR <= 8) on the VALU. v_dot8_i32_i4 multiplies eight
+// packed signed 4-bit codes pairwise and adds the products to an i32 exactly,
+// so both operands are used as packed (no unpack, no MFMA): the kernel only
+// has to stream the weight. A workgroup of NW waves owns RW output columns
+// (weight rows n0 .. n0+RW-1); wave w takes k-steps w, w + NW, ..., U of them
+// per round with all their loads in flight. Lane l reads 16 bytes (32 k) at
+// k-segment l % 8 of weight rows l / 8 + 8j, j < RW / 8: one load
+// instruction covers 8 whole 128-byte rows of a tiled block. The activation
+// segment of row m is one 16-byte load; rows past M and k-steps past K read
+// as zero (the weight's leave the buffer's range, so they move no data). The
+// eight lanes of a row are summed by DPP and the waves' sums through LDS
+// (integer adds: exact in any order), then the G1 epilogue runs on the totals.
+template <int MR, int NW, int U, int RW, bool RESID>
+__global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint32_t* __restrict__ a, int a_words,
+                                                          const float* __restrict__ as, const uint32_t* __restrict__ w,
+                                                          const float* __restrict__ ws, int64_t M, int N, int kb,
+                                                          const uint16_t* __restrict__ residual,
+                                                          uint16_t* __restrict__ out) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int J = RW / 8;
+  static_assert(RW % 8 == 0 && 128 % RW == 0 && MR * RW <= NW * 64, "decode tile");
+  __shared__ int red[NW][MR][RW];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int seg = lane & 7, r8 = lane >> 3;
+  const int n0 = blockIdx.x * RW;
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(w + (int64_t)(n0 / 128) * kb * 4096, (uint32_t)(kb * 16384));
+  const int w_voff = ((n0 % 128) + r8) * 128 + 16 * seg;
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a, (uint32_t)(M * a_words * 4));
+  const int a_voff = 16 * seg;
+  // The epilogue's scales are fetched with the first loads, so their latency
+  // is not paid again after the reduction.
+  const int em = threadIdx.x / RW, er = threadIdx.x % RW;
+  const bool epi = threadIdx.x < MR * RW && em < M;
+  float e_ws = 0.0f, e_as = 0.0f;
+  uint32_t e_res = 0;
+  if (epi) {
+    e_ws = ws[n0 + er];
+    e_as = as[em];
+    if (RESID) e_res = residual[(int64_t)em * N + n0 + er];
+  }
+  int acc[J][MR];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[j][m] = 0;
+  for (int kt0 = wave; kt0 < kb; kt0 += NW * U) {
+    v4i wv[U][J], av[U][MR];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // k-steps past kb: the weight offset leaves the resource (reads 0)
+      const int kt = kt0 + NW * u;
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        wv[u][j] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff + 1024 * j, kt * 16384, 0);
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        av[u][m] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff + m * a_words * 4, (kt < kb ? kt : 0) * 128, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc[j][m] = __builtin_amdgcn_sdot8(wv[u][j][c], av[u][m][c], acc[j][m], false);
+  }
+  // Sum the 8 segments of each row: lane xor 1 and xor 2 by DPP quad_perm
+  // [1,0,3,2] and [2,3,0,1], then lane xor 4 by a swizzle; every lane of the
+  // eight ends with the row's sum.
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      int v = acc[j][m];
+      v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+      v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+      v += __builtin_amdgcn_ds_swizzle(v, 0x101F);  // bit mode: and 0x1F, or 0, xor 4
+      if (seg == 0) red[wave][m][r8 + 8 * j] = v;
+    }
+  __syncthreads();
+  if (epi) {
+    int sum = 0;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) sum += red[q][em][er];
+    uint32_t v = g1_value<0>(sum, e_ws, e_as);
+    if (RESID) v = f32_to_bf16(bf16_lo(e_res) + bf16_lo(v));
+    out[(int64_t)em * N + n0 + er] = (uint16_t)v;
+  }
+#endif
+}
+
+template <int MR, bool RESID>
+hipError_t launch_decode_mr(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                            int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  // 16 columns and 8 waves per workgroup: N12288 gives 768 workgroups, three
+  // per CU (32 columns gave 1.5 per CU and half the CUs twice the bytes).
+  // Two k-steps per round where K has them (measured against one, and
+  // against 4 or 16 waves: M1 N12288 K4096 2.9 us with the weight in the
+  // last-level cache, 6.3 us streaming it from HBM).
+  const int kb = k / 256;
+  if (kb >= 16)
+    gemm_decode_kernel<MR, 8, 2, 16, RESID><<<(unsigned)(n / 16), 512, 0, stream>>>(a, a_words, as, w, ws, m, n, kb,
+                                                                                 residual, out);
+  else
+    gemm_decode_kernel<MR, 8, 1, 16, RESID><<<(unsigned)(n / 16), 512, 0, stream>>>(a, a_words, as, w, ws, m, n, kb,
+                                                                                 residual, out);
+  return hipGetLastError();
+}
+
+template <bool RESID>
+hipError_t launch_decode_m(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  if (m == 1) return launch_decode_mr<1, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (m == 2) return launch_decode_mr<2, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (m <= 4) return launch_decode_mr<4, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (m <= 8) return launch_decode_mr<8, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_decode(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                         int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  if (residual) return launch_decode_m<true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return launch_decode_m<false>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+}
+
+// Mid-sized G1 with the K split inside the workgroup: output tiles of 32 MT
+// activation rows x 32 NT columns, small enough that the grid covers the CUs
+// (M512 N2048: 256 tiles of 64 x 64), and the tile's k-steps shared among its
+// NW waves instead of walked by one set of waves. Each wave DMAs whole k-steps
+// (activation rows and weight rows, 128 bytes each, swizzled as in the DMA
+// cores: physical chunk c of row r holds logical chunk c ^ ((r >> 1) & 7))
+// into its own LDS stages, so it only ever waits for its own loads; NB = 2
+// keeps the next k-step's DMA in flight while one computes. The partial
+// accumulators (256 x the dot products, exact) are then summed through LDS in
+// wave order and the G1 epilogue writes 8-byte column quads.
+template <int MT, int NT, int NW, int NB, bool RESID>
+__global__ __launch_bounds__(NW * 64) void gemm_ksplit_kernel(const uint32_t* __restrict__ a, int a_words,
+                                                          const float* __restrict__ as, const uint32_t* __restrict__ w,
+                                                          const float* __restrict__ ws, int64_t M, int N, int kb,
+                                                          const uint16_t* __restrict__ residual,
+                                                          uint16_t* __restrict__ out) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int BM = 32 * MT, BN = 32 * NT;  // activation rows, weight rows of the tile
+  constexpr int STAGE = (BM + BN) * 128;
+  constexpr int NF = MT + NT;
+  constexpr int QUADS = MT * NT * 256;       // output column quads of the tile
+  constexpr int IPT = (QUADS + NW * 64 - 1) / (NW * 64);
+  static_assert(NB * STAGE >= MT * NT * 4096, "a wave's accumulators fit its stages");
+  __shared__ __align__(16) char lds[NW * NB * STAGE];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 31, h = lane >> 5;
+  const int n0 = blockIdx.x * BN;
+  const int64_t m0 = (int64_t)blockIdx.y * BM;
+  const int64_t rows = M - m0 < BM ? M - m0 : BM;
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a + m0 * a_words, (uint32_t)(rows * a_words * 4));
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(w + (int64_t)(n0 / 128) * kb * 4096, (uint32_t)(kb * 16384));
+  // DMA instruction q moves rows 8q .. 8q+7; lane -> row 8q + lane / 8,
+  // physical chunk lane % 8 = logical (lane % 8) ^ (((8q + lane / 8) >> 1) & 7),
+  // which depends on q only through q & 1.
+  const int c_even = ((lane & 7) ^ (lane >> 4)) * 16, c_odd = ((lane & 7) ^ (4 | (lane >> 4))) * 16;
+  const int a_voff = (lane >> 3) * a_words * 4, w_voff = ((n0 & 127) + (lane >> 3)) * 128;
+
+  // Epilogue quads of this thread: their scales (and residual) load now.
+  float e_as[IPT];
+  float4 e_ws[IPT];
+  uint2 e_res[IPT];
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int qd = threadIdx.x + i * NW * 64;
+    const int b = qd >> 8, rq = (qd >> 6) & 3, ln = qd & 63;
+    const int64_t m = m0 + 32 * (b % MT) + (ln & 31);
+    const int n = n0 + 32 * (b / MT) + 8 * rq + 4 * (ln >> 5);
+    const bool ok = qd < QUADS && m < M;
+    e_as[i] = ok ? as[m] : 0.0f;
+    e_ws[i] = ok ? *reinterpret_cast<const float4*>(ws + n) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    e_res[i] = RESID && ok ? *reinterpret_cast<const uint2*>(residual + m * N + n) : make_uint2(0, 0);
+  }
+
+  char* my = lds + wave * NB * STAGE;
+  auto issue = [&](char* stage, int kt) {
+#pragma unroll
+    for (int q = 0; q < MT * 4; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(stage + q * 1024), 16,
+                                               a_voff + ((q & 1) ? c_odd : c_even), 8 * q * a_words * 4 + kt * 128,
+                                               0, 0);
+#pragma unroll
+    for (int q = 0; q < NT * 4; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(stage + BM * 128 + q * 1024), 16,
+                                               w_voff + ((q & 1) ? c_odd : c_even), kt * 16384 + q * 1024, 0, 0);
+  };
+  v16i acc[NT][MT];
+#pragma unroll
+  for (int i = 0; i < NT; ++i)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[i][j] = v16i{};
+  auto compute = [&](const char* stage) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      uint4 raw[NF];
+      const int off = lr * 128 + (((4 * h + p) ^ ((lr >> 1) & 7)) << 4);
+#pragma unroll
+      for (int f = 0; f < NF; ++f) raw[f] = *reinterpret_cast<const uint4*>(stage + f * 4096 + off);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        v4i u[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          u[f] = half ? unpack_pair(raw[f].z, raw[f].w) : unpack_pair(raw[f].x, raw[f].y);
+#pragma unroll
+        for (int i = 0; i < NT; ++i)
+#pragma unroll
+          for (int j = 0; j < MT; ++j) acc[i][j] = mfma32_i8(u[MT + i], u[j], acc[i][j]);
+      }
+    }
+  };
+  // k-steps wave, wave + NW, ...; with two stages the next one's DMA is in
+  // flight while one computes (vector memory completes in issue order).
+  const int steps = wave < kb ? (kb - 1 - wave) / NW + 1 : 0;
+  if (steps > 0) {
+    issue(my, wave);
+    if (NB == 2 && steps > 1) issue(my + STAGE, wave + NW);
+    for (int s = 0; s < steps; ++s) {
+      char* stage = my + (NB == 2 ? (s & 1) * STAGE : 0);
+      if (NB == 2 && s + 1 < steps)
+        wait_vmcnt<4 * (MT + NT)>();
+      else
+        wait_vmcnt<0>();
+      compute(stage);
+      if (s + NB < steps) issue(stage, wave + NW * (s + NB));
+    }
+  }
+  __syncthreads();  // every wave is done reading its stages
+  // Partial sums: block b = i * MT + j, register quad rq, lane -> 16 bytes.
+#pragma unroll
+  for (int i = 0; i < NT; ++i)
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq)
+        *reinterpret_cast<v4i*>(my + (((i * MT + j) * 4 + rq) * 64 + lane) * 16) =
+            v4i{acc[i][j][4 * rq], acc[i][j][4 * rq + 1], acc[i][j][4 * rq + 2], acc[i][j][4 * rq + 3]};
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int qd = threadIdx.x + i * NW * 64;
+    const int b = qd >> 8, rq = (qd >> 6) & 3, ln = qd & 63;
+    const int64_t m = m0 + 32 * (b % MT) + (ln & 31);
+    if (qd >= QUADS || m >= M) continue;
+    const int n = n0 + 32 * (b / MT) + 8 * rq + 4 * (ln >> 5);
+    v4i sum = *reinterpret_cast<const v4i*>(lds + qd * 16);
+#pragma unroll
+    for (int q = 1; q < NW; ++q) sum += *reinterpret_cast<const v4i*>(lds + q * NB * STAGE + qd * 16);
+    uint32_t p0 = g1_value<8>(sum.x, e_ws[i].x, e_as[i]) | (g1_value<8>(sum.y, e_ws[i].y, e_as[i]) << 16);
+    uint32_t p1 = g1_value<8>(sum.z, e_ws[i].z, e_as[i]) | (g1_value<8>(sum.w, e_ws[i].w, e_as[i]) << 16);
+    if (RESID) {
+      const uint2 rv = e_res[i];
+      p0 = pack_bf16x2(bf16_lo(rv.x) + bf16_lo(p0), bf16_hi(rv.x) + bf16_hi(p0));
+      p1 = pack_bf16x2(bf16_lo(rv.y) + bf16_lo(p1), bf16_hi(rv.y) + bf16_hi(p1));
+    }
+    *reinterpret_cast<uint2*>(out + m * N + n) = make_uint2(p0, p1);
+  }
+#endif
+}
+
+template <int MT, int NT, int NW, int NB>
+hipError_t launch_ksplit_t(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  const int64_t groups = (m + 32 * MT - 1) / (32 * MT);
+  if (groups > 65535 || n % (32 * NT) != 0) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(n / (32 * NT)), (unsigned)groups);
+  if (residual)
+    gemm_ksplit_kernel<MT, NT, NW, NB, true><<<grid, NW * 64, 0, stream>>>(a, a_words, as, w, ws, m, n, k / 256,
+                                                                          residual, out);
+  else
+    gemm_ksplit_kernel<MT, NT, NW, NB, false><<<grid, NW * 64, 0, stream>>>(a, a_words, as, w, ws, m, n, k / 256,
+                                                                           residual, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_ksplit(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
+                         int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  // The largest tile that still gives about one per CU (>= 192 tiles), with
+  // 32-row tiles when m <= 32 (a 64-row tile would be half padding); else
+  // 32 x 32 tiles with two stages per wave. Measured (graph replay, us):
+  // M512 N2048 K2048 64x64 5.7 (32x64 7.2, 32x32 9.9); M16 N12288 K4096
+  // 32x64 4.7 (64x64 6.4); M64 N12288 K4096 64x64 6.9 (32x64 8.8); M64 N4096
+  // K4096 32x32 4.5 (32x64 4.8); M32 N4096 K12288 32x32 6.8 (32x64 8.7).
+  auto tiles = [&](int bm, int bn) { return (m + bm - 1) / bm * (n / bn); };
+  if (m > 32 && tiles(64, 64) >= 192)
+    return launch_ksplit_t<2, 2, 8, 1>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (tiles(32, 64) >= 192) return launch_ksplit_t<1, 2, 8, 1>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return launch_ksplit_t<1, 1, 8, 2>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
 }
 
 // Grouped expert GEMM for few routed rows per expert (decode-sized batches),
@@ -1232,9 +1543,18 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
     // M1 N4096 K4096 5.1 us against 17.4; M64 N12288 K4096 13.0 against
     // 17.8; M512 N2048 K2048 7.5 against 11.3; M128 N12288 K4096 29.1
     // against 18.3, where 96 tiles of 128x128 already cover most CUs).
+    // At most 8 rows: the VALU dot-product kernel (graph replay, weight in
+    // the last-level cache: M1 N12288 K4096 2.9 us against 8.4 for the
+    // skinny kernel, M8 6.6 against 8.2; M8 N2048 K2048 3.3 against 3.8).
+    // Up to 255 tiles of 128x128: the split-K tiles (M512 N2048 K2048 5.7 us
+    // against 7.4 for the skinny kernel and 11.4 for 128x128 tiles; M128
+    // N12288 K4096 12.6 against 18.3).
     const int64_t tiles256 = (m + 255) / 256 * (n / 256);
-    if (use_skinny(m, n))
-      config = kGemmSkinny;
+    const int64_t tiles128 = (m + 127) / 128 * (n / 128);
+    if (m <= 8)
+      config = kGemmDecode;
+    else if (tiles128 < 256)
+      config = kGemmKsplit;
     else
       config = (n % 256 == 0 && m >= 1024 && tiles256 >= 192) ? kGemmPersist256 : kGemmTile128;
   }
@@ -1248,6 +1568,10 @@ hipError_t launch_gemm_i4(const uint32_t* a, int a_words, const float* as, const
     case kGemmPersist256:
       return launch_dma_persist_any<Dma256x256W8Pin>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     case kGemmSkinny: return launch_skinny_any(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case kGemmDecode:
+      if (m > 8) return launch_skinny_any(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+      return launch_decode(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+    case kGemmKsplit: return launch_ksplit(a, a_words, as, w, ws, m, n, k, residual, out, stream);
     default: return hipErrorInvalidValue;
   }
 }

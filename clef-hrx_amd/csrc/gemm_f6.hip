@@ -122,7 +122,7 @@ struct F6Tile {
   static constexpr int A_INST = A_BYTES / 1024 / NW;           // DMA instructions per wave per k-step
   static constexpr int B_INST = B_BYTES / 1024 / NW;
   static constexpr int NST = 3;                                 // LDS stages: prefetch distance 2
-  static constexpr int INST = A_INST + B_INST;                  // DMA instructions per wave per k-step
+  [[maybe_unused]] static constexpr int INST = A_INST + B_INST;  // DMA instructions per wave per k-step
   static constexpr int EPI_WAVE = 32 * WN * 2;                  // staging bytes per wave (32 rows of WN bf16)
   static constexpr int SCALE_WAVE = 1024;                       // per-wave epilogue scales (768 bytes used)
   static constexpr int LDS = NST * STAGE_BYTES + NW * SCALE_WAVE;  // 152 KiB

@@ -47,7 +47,15 @@ int set_last_error(const char* msg);
 // G1 tile configurations (clef_i4_gemm_config): 128x128 tiles, 256x256
 // tiles with one workgroup per tile, 256x256 tiles walked by a persistent
 // grid, and the K-split small-M kernel.
-enum GemmConfig { kGemmTile128 = 0, kGemmTile256 = 1, kGemmPersist256 = 2, kGemmSkinny = 3, kGemmConfigs = 4 };
+enum GemmConfig {
+  kGemmTile128 = 0,
+  kGemmTile256 = 1,
+  kGemmPersist256 = 2,
+  kGemmSkinny = 3,
+  kGemmDecode = 4,
+  kGemmKsplit = 5,
+  kGemmConfigs = 6
+};
 int gemm_config_count();
 
 hipError_t launch_router_gate(const uint16_t* x, const uint16_t* w, int64_t tokens, int hidden, int experts,

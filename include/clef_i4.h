@@ -183,7 +183,8 @@ int clef_i8_gemm(const uint32_t* a, int32_t k_stride, const float* a_scales, con
 /* Same, with an explicit tile configuration (0..clef_i4_gemm_configs()-1;
  * -1 = automatic): 0 = 128x128 tiles, 1 = 256x256 tiles (one workgroup per
  * tile), 2 = 256x256 tiles on a persistent grid, 3 = the K-split small-M
- * kernel. Configurations 1 and 2 fall back to 0 when n % 256 != 0, and 2 to 1
+ * kernel, 4 = the VALU dot-product kernel for m <= 8 (3 for larger m),
+ * 5 = small tiles with the K split among a workgroup's waves. Configurations 1 and 2 fall back to 0 when n % 256 != 0, and 2 to 1
  * when k < 512. For tuning and tests. */
 int clef_i4_gemm_config(const uint32_t* a, int32_t k_stride, const float* a_scales,
                         const uint32_t* w_tiled, const float* w_scales, int64_t m, int32_t n,

@@ -954,3 +954,75 @@ def test_project_f6_matches_oracle(m, n, k, resid):
     got = clef_i4.project_f6(clef_i4.prepare_f6(to_dev_bf16(x)), fw,
                              residual=to_dev_bf16(res) if resid else None)
     assert_same_u16(bf16_host(got), want, f"project_f6 m={m} n={n} k={k} resid={resid}")
+
+
+# ---------------------------------------------------------------- decode-sized G1
+# Configuration 4: v_dot8_i32_i4 on the packed codes for m <= 8.
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("n,k", [(128, 256), (256, 768), (384, 2304), (1024, 4096), (128, 12544)])
+def test_gemm_decode_matches_oracle(m, n, k):
+    """Few rows against the oracle, with and without the residual: one
+    k-step (fewer than the kernel's eight waves), k-step counts that leave
+    some waves a round short (9, 49), ragged m inside the 4- and 8-row forms."""
+    rng = np.random.default_rng(m * 1000 + n + k)
+    x, w, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
+    a = dev_prepared(x, stride)
+    qw = dev_weight(w_tiled, w_scales, n, k)
+    want = oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k)
+    assert_same_u16(bf16_host(clef_i4.project_prepared(a, qw, config=4)), want, f"decode m={m} n={n} k={k}")
+    res = randn_bf16(rng, (m, n), std=3.0)
+    want_r = oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k, residual=res)
+    got_r = clef_i4.project_prepared(a, qw, residual=to_dev_bf16(res), config=4)
+    assert_same_u16(bf16_host(got_r), want_r, f"decode residual m={m} n={n} k={k}")
+    if m <= 4:  # the automatic choice
+        assert_same_u16(bf16_host(clef_i4.project_prepared(a, qw)), want, f"auto m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_gemm_decode_extreme_codes_and_scales(m):
+    """Codes -8 and +7 (|acc| up to 8 * 8 * 4096), huge, infinite, NaN, zero,
+    negative and tiny scales through the dot-product kernel."""
+    n, k = 256, 4096
+    stride = oracle.activation_stride(k)
+    a_words = np.full((m, stride // 8), 0x88888888, dtype=np.uint32)
+    a_words[1::2, : k // 8] = 0x77777777
+    w_codes = np.full((n, stride // 8), 0x88888888, dtype=np.uint32)
+    w_codes[::3, : k // 8] = 0x77777777
+    w_codes[1::7, : k // 8] = 0x0F1E2D3C
+    w_tiled = oracle.retile(w_codes, k)
+    a_scales = np.array([1e30, 1e-3, np.inf, np.nan, 0.0, -3.0, 1e-38, 2e-45][:m], dtype=np.float32)
+    w_scales = np.full(n, 1e10, dtype=np.float32)
+    w_scales[::5] = 1e-30
+    w_scales[2::11] = 0.0
+    want = oracle.gemm(a_words, a_scales, w_tiled, w_scales, n, k)
+    storage = np.concatenate([a_words.reshape(-1), a_scales.view(np.uint32)])
+    a = clef_i4.Prepared(to_dev_u32(storage), m, k, stride, 4)
+    got = clef_i4.project_prepared(a, dev_weight(w_tiled, w_scales, n, k), config=4)
+    assert_same_bf16_nan_aware(bf16_host(got), want, f"decode extreme m={m}")
+
+
+# ---------------------------------------------------------------- split-K tiles
+# Configuration 5: 64x64, 32x64 or 32x32 tiles (chosen by shape) whose
+# k-steps are shared among the workgroup's eight waves.
+
+@pytest.mark.parametrize("m,n,k", [
+    (100, 8192, 768),     # 64x64 tiles, 3 k-steps for 8 waves, ragged last row tile
+    (512, 2048, 2048),    # 64x64 tiles: the 512 x 2048 x 2048 linear
+    (20, 12288, 2304),    # 32x64 tiles (m <= 32), 9 k-steps
+    (40, 1024, 12544),    # 32x32 tiles, two stages per wave, 49 k-steps
+    (9, 128, 256),        # one k-step, one tile column
+    (300, 384, 1024),
+])
+def test_gemm_ksplit_matches_oracle(m, n, k):
+    rng = np.random.default_rng(m * 3 + n + k)
+    x, w, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
+    a = dev_prepared(x, stride)
+    qw = dev_weight(w_tiled, w_scales, n, k)
+    want = oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k)
+    assert_same_u16(bf16_host(clef_i4.project_prepared(a, qw, config=5)), want, f"ksplit m={m} n={n} k={k}")
+    res = randn_bf16(rng, (m, n), std=3.0)
+    want_r = oracle.gemm(a_codes, a_scales, w_tiled, w_scales, n, k, residual=res)
+    got_r = clef_i4.project_prepared(a, qw, residual=to_dev_bf16(res), config=5)
+    assert_same_u16(bf16_host(got_r), want_r, f"ksplit residual m={m} n={n} k={k}")
+    assert_same_u16(bf16_host(clef_i4.project_prepared(a, qw)), want, f"auto m={m} n={n} k={k}")
