@@ -1225,7 +1225,9 @@ hipError_t launch_decode(const uint32_t* a, int a_words, const float* as, const 
 // into its own LDS stages, so it only ever waits for its own loads; NB = 2
 // keeps the next k-step's DMA in flight while one computes. The partial
 // accumulators (256 x the dot products, exact) are then summed through LDS in
-// wave order and the G1 epilogue writes 8-byte column quads.
+// wave order, and each thread runs the G1 epilogue on 8 consecutive columns of
+// one row (16-byte stores); consecutive threads take consecutive rows, so
+// their LDS reads are consecutive 16-byte slots.
 template <int MT, int NT, int NW, int NB, bool RESID>
 __global__ __launch_bounds__(NW * 64) void gemm_ksplit_kernel(const uint32_t* __restrict__ a, int a_words,
                                                           const float* __restrict__ as, const uint32_t* __restrict__ w,
@@ -1236,8 +1238,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_ksplit_kernel(const uint32_t* __
   constexpr int BM = 32 * MT, BN = 32 * NT;  // activation rows, weight rows of the tile
   constexpr int STAGE = (BM + BN) * 128;
   constexpr int NF = MT + NT;
-  constexpr int QUADS = MT * NT * 256;       // output column quads of the tile
-  constexpr int IPT = (QUADS + NW * 64 - 1) / (NW * 64);
+  constexpr int CHUNKS = BM * NT * 4;        // 8-column row chunks of the tile
+  constexpr int IPT = (CHUNKS + NW * 64 - 1) / (NW * 64);
   static_assert(NB * STAGE >= MT * NT * 4096, "a wave's accumulators fit its stages");
   __shared__ __align__(16) char lds[NW * NB * STAGE];
   const int lane = threadIdx.x & 63;
@@ -1254,20 +1256,21 @@ __global__ __launch_bounds__(NW * 64) void gemm_ksplit_kernel(const uint32_t* __
   const int c_even = ((lane & 7) ^ (lane >> 4)) * 16, c_odd = ((lane & 7) ^ (4 | (lane >> 4))) * 16;
   const int a_voff = (lane >> 3) * a_words * 4, w_voff = ((n0 & 127) + (lane >> 3)) * 128;
 
-  // Epilogue quads of this thread: their scales (and residual) load now.
+  // Epilogue chunk c of this thread: tile row c % BM, columns
+  // 8 (c / BM) .. +7. Its scales (and residual) load now.
   float e_as[IPT];
-  float4 e_ws[IPT];
-  uint2 e_res[IPT];
+  float4 e_ws[IPT][2];
+  uint4 e_res[IPT];
 #pragma unroll
   for (int i = 0; i < IPT; ++i) {
-    const int qd = threadIdx.x + i * NW * 64;
-    const int b = qd >> 8, rq = (qd >> 6) & 3, ln = qd & 63;
-    const int64_t m = m0 + 32 * (b % MT) + (ln & 31);
-    const int n = n0 + 32 * (b / MT) + 8 * rq + 4 * (ln >> 5);
-    const bool ok = qd < QUADS && m < M;
+    const int c = threadIdx.x + i * NW * 64;
+    const int64_t m = m0 + c % BM;
+    const int n = n0 + 8 * (c / BM);
+    const bool ok = c < CHUNKS && m < M;
     e_as[i] = ok ? as[m] : 0.0f;
-    e_ws[i] = ok ? *reinterpret_cast<const float4*>(ws + n) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    e_res[i] = RESID && ok ? *reinterpret_cast<const uint2*>(residual + m * N + n) : make_uint2(0, 0);
+    e_ws[i][0] = ok ? *reinterpret_cast<const float4*>(ws + n) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    e_ws[i][1] = ok ? *reinterpret_cast<const float4*>(ws + n + 4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    e_res[i] = RESID && ok ? *reinterpret_cast<const uint4*>(residual + m * N + n) : make_uint4(0, 0, 0, 0);
   }
 
   char* my = lds + wave * NB * STAGE;
@@ -1336,22 +1339,33 @@ __global__ __launch_bounds__(NW * 64) void gemm_ksplit_kernel(const uint32_t* __
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < IPT; ++i) {
-    const int qd = threadIdx.x + i * NW * 64;
-    const int b = qd >> 8, rq = (qd >> 6) & 3, ln = qd & 63;
-    const int64_t m = m0 + 32 * (b % MT) + (ln & 31);
-    if (qd >= QUADS || m >= M) continue;
-    const int n = n0 + 32 * (b / MT) + 8 * rq + 4 * (ln >> 5);
-    v4i sum = *reinterpret_cast<const v4i*>(lds + qd * 16);
+    const int c = threadIdx.x + i * NW * 64;
+    const int rr = c % BM, cc = c / BM;
+    const int64_t m = m0 + rr;
+    if (c >= CHUNKS || m >= M) continue;
+    const int n = n0 + 8 * cc;
+    // columns 8 cc .. 8 cc + 3 and + 4 .. + 7: register quad cc % 4 of weight
+    // block cc / 4, lane halves 0 and 1, lane rr % 32 of activation block rr / 32
+    const int qd = (((cc >> 2) * MT + (rr >> 5)) * 4 + (cc & 3)) * 64 + (rr & 31);
+    v4i lo = *reinterpret_cast<const v4i*>(lds + qd * 16);
+    v4i hi = *reinterpret_cast<const v4i*>(lds + (qd + 32) * 16);
 #pragma unroll
-    for (int q = 1; q < NW; ++q) sum += *reinterpret_cast<const v4i*>(lds + q * NB * STAGE + qd * 16);
-    uint32_t p0 = g1_value<8>(sum.x, e_ws[i].x, e_as[i]) | (g1_value<8>(sum.y, e_ws[i].y, e_as[i]) << 16);
-    uint32_t p1 = g1_value<8>(sum.z, e_ws[i].z, e_as[i]) | (g1_value<8>(sum.w, e_ws[i].w, e_as[i]) << 16);
-    if (RESID) {
-      const uint2 rv = e_res[i];
-      p0 = pack_bf16x2(bf16_lo(rv.x) + bf16_lo(p0), bf16_hi(rv.x) + bf16_hi(p0));
-      p1 = pack_bf16x2(bf16_lo(rv.y) + bf16_lo(p1), bf16_hi(rv.y) + bf16_hi(p1));
+    for (int q = 1; q < NW; ++q) {
+      lo += *reinterpret_cast<const v4i*>(lds + q * NB * STAGE + qd * 16);
+      hi += *reinterpret_cast<const v4i*>(lds + q * NB * STAGE + (qd + 32) * 16);
     }
-    *reinterpret_cast<uint2*>(out + m * N + n) = make_uint2(p0, p1);
+    const float4 w0 = e_ws[i][0], w1 = e_ws[i][1];
+    const float av = e_as[i];
+    uint32_t p[4] = {g1_value<8>(lo.x, w0.x, av) | (g1_value<8>(lo.y, w0.y, av) << 16),
+                     g1_value<8>(lo.z, w0.z, av) | (g1_value<8>(lo.w, w0.w, av) << 16),
+                     g1_value<8>(hi.x, w1.x, av) | (g1_value<8>(hi.y, w1.y, av) << 16),
+                     g1_value<8>(hi.z, w1.z, av) | (g1_value<8>(hi.w, w1.w, av) << 16)};
+    if (RESID) {
+      const uint32_t rv[4] = {e_res[i].x, e_res[i].y, e_res[i].z, e_res[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) p[j] = pack_bf16x2(bf16_lo(rv[j]) + bf16_lo(p[j]), bf16_hi(rv[j]) + bf16_hi(p[j]));
+    }
+    *reinterpret_cast<uint4*>(out + m * N + n) = make_uint4(p[0], p[1], p[2], p[3]);
   }
 #endif
 }
