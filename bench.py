@@ -14,7 +14,8 @@ M=4096 on one MI355X.
                top-8, expert intermediate 768: route -> group -> expert GEMMs
                -> SwiGLU -> combine, timed over --steps layer calls.
   mlp_*        INT4-MLP dense block, 4096 x 4096 input, gate|up 24576 x 4096,
-               down 4096 x 12288: quantize -> GEMM -> SwiGLU+quantize -> GEMM.
+               down 4096 x 12288: quantize -> GEMM -> SwiGLU+quantize -> GEMM
+               (bf6 form of the codes, checked against the INT4 block).
   int8_gemm_*  the INT8 x INT8 projection at the GEMM's shape.
   small_m_*    M = 1, 16, 64 on the GEMM's weight (K4096 N12288): GPU time per
                call (HIP graph replay) and HBM GB/s of the bytes the call moves,
@@ -22,7 +23,8 @@ M=4096 on one MI355X.
                holds; us_cached repeats one weight (cache-resident).
   linear_m512_k2048_n2048  the single INT4 linear M512 K2048 N2048: GPU time
                per call (graph replay), TOPS and HBM GB/s.
-  attn_proj_*  INT4 attention projections at M=16384 (Q, K, V, O + residual).
+  attn_proj_*  INT4 attention projections at M=16384 (Q, K, V, O + residual)
+               on a prepared activation (bf6 form, checked against INT4).
   moe_skewed_t65536  the MoE layer at 65536 tokens with skewed routing (a few
                experts take most rows, eight none).
   roofline     the GEMM kernel against the peak of the MFMA it runs on (fp6
@@ -244,31 +246,32 @@ def attention_leg(args):
     """INT4 attention projections at M=16384: Q 4096->4096, K and V 4096->1024
     on one shared quantized activation, and O 4096->4096 with the residual
     (fed the same activation here: its real input, the attention output, has
-    the same shape)."""
+    the same shape). Run on the bf6 form of the codes (weights re-encoded
+    once, the activation quantized straight into bf6); the outputs are
+    checked against the INT4-operand projections bit for bit."""
     import torch
 
     import clef_i4
 
     m, d, kv = 16384, 4096, 1024
     x = bf16_randn((m, d), 1.0, 1003 * 16 + 0)
-    wq = clef_i4.load_quantized_weight(bf16_randn((d, d), 0.02, 1003 * 16 + 1))
-    wk = clef_i4.load_quantized_weight(bf16_randn((kv, d), 0.02, 1003 * 16 + 2))
-    wv = clef_i4.load_quantized_weight(bf16_randn((kv, d), 0.02, 1003 * 16 + 3))
-    wo = clef_i4.load_quantized_weight(bf16_randn((d, d), 0.02, 1003 * 16 + 4))
+    ws = [clef_i4.load_quantized_weight(bf16_randn((n, d), 0.02, 1003 * 16 + 1 + i))
+          for i, n in enumerate((d, kv, kv, d))]
+    fws = [clef_i4.f6_weight(w) for w in ws]
     res = bf16_randn((m, d), 1.0, 1003 * 16 + 5)
-    ax = clef_i4.prepare(x)
-    q = torch.empty((m, d), dtype=torch.bfloat16, device="cuda")
-    kk = torch.empty((m, kv), dtype=torch.bfloat16, device="cuda")
-    v = torch.empty((m, kv), dtype=torch.bfloat16, device="cuda")
-    o = torch.empty((m, d), dtype=torch.bfloat16, device="cuda")
+    ax = clef_i4.prepare_f6(x)
+    outs = [torch.empty((m, n), dtype=torch.bfloat16, device="cuda") for n in (d, kv, kv, d)]
 
     def step():
-        clef_i4.project_prepared(ax, wq, out=q)
-        clef_i4.project_prepared(ax, wk, out=kk)
-        clef_i4.project_prepared(ax, wv, out=v)
-        clef_i4.project_prepared(ax, wo, residual=res, out=o)
+        for i in range(4):
+            clef_i4.project_f6(ax, fws[i], residual=res if i == 3 else None, out=outs[i])
 
     ms = timed(step, args.steps, max(1, args.warmup // 4))
+    a4 = clef_i4.prepare(x)
+    for i in range(4):
+        want = clef_i4.project_prepared(a4, ws[i], residual=res if i == 3 else None)
+        if not torch.equal(want.view(torch.int16), outs[i].view(torch.int16)):
+            raise SystemExit("bf6 attention projection differs from the INT4 one")
     ops = 2.0 * m * d * (d + kv + kv + d)
     return {"ms": ms, "tops": ops / ms / 1e9}
 
@@ -290,6 +293,10 @@ def i8_leg(args):
 
 
 def mlp_leg(args):
+    """The INT4-MLP block M4096 D4096 F12288 on the bf6 form of the codes:
+    Q1(x) -> gate and up projections -> SwiGLU-fused Q1(h) -> down
+    projection, each quantizer writing bf6, the weights re-encoded once. The
+    output is checked bit for bit against the same block on INT4 operands."""
     import torch
 
     import clef_i4
@@ -299,23 +306,25 @@ def mlp_leg(args):
     wg = clef_i4.load_quantized_weight(bf16_randn((f, d), 0.02, 1002 * 16 + 2))
     wu = clef_i4.load_quantized_weight(bf16_randn((f, d), 0.02, 1002 * 16 + 3))
     wd = clef_i4.load_quantized_weight(bf16_randn((d, f), 0.02, 1002 * 16 + 4))
+    fg, fu, fd = clef_i4.f6_weight(wg), clef_i4.f6_weight(wu), clef_i4.f6_weight(wd)
     gate = torch.empty((m, f), dtype=torch.bfloat16, device="cuda")
     up = torch.empty((m, f), dtype=torch.bfloat16, device="cuda")
     y = torch.empty((m, d), dtype=torch.bfloat16, device="cuda")
-    a = clef_i4.prepare(x)
-    sh = clef_i4.activation_stride(f)
-    h = clef_i4.Prepared(torch.zeros(m * (sh // 8 + 1), dtype=torch.int32, device="cuda"), m, f, sh, 4)
-    stream = torch.cuda.current_stream().cuda_stream
+    a = clef_i4.prepare_f6(x)
+    h = clef_i4.prepare_swiglu_f6(gate, up)
 
     def block():
-        clef_i4.prepare(x, out=a.storage)
-        clef_i4.project_prepared(a, wg, out=gate)
-        clef_i4.project_prepared(a, wu, out=up)
-        clef_i4._check(clef_i4.lib().clef_i4_prepare_swiglu(gate.data_ptr(), up.data_ptr(), m, f, sh, 4,
-                                                            h.storage.data_ptr(), stream))
-        clef_i4.project_prepared(h, wd, out=y)
+        clef_i4.prepare_f6(x, out=a.storage)
+        clef_i4.project_f6(a, fg, out=gate)
+        clef_i4.project_f6(a, fu, out=up)
+        clef_i4.prepare_swiglu_f6(gate, up, out=h.storage)
+        clef_i4.project_f6(h, fd, out=y)
 
     ms = timed(block, args.steps, max(1, args.warmup // 2))
+    a4 = clef_i4.prepare(x)
+    h4 = clef_i4.prepare_swiglu(clef_i4.project_prepared(a4, wg), clef_i4.project_prepared(a4, wu))
+    if not torch.equal(clef_i4.project_prepared(h4, wd).view(torch.int16), y.view(torch.int16)):
+        raise SystemExit("bf6 MLP block differs from the INT4 one")
     ops = 2.0 * m * (2 * f) * d + 2.0 * m * d * f
     return {"ms": ms, "tops": ops / ms / 1e9}
 
