@@ -1101,7 +1101,9 @@ hipError_t launch_skinny_any(const uint32_t* a, int a_words, const float* as, co
 // as zero (the weight's leave the buffer's range, so they move no data). The
 // eight lanes of a row are summed by DPP and the waves' sums through LDS
 // (integer adds: exact in any order), then the G1 epilogue runs on the totals.
-template <int MR, int NW, int U, int RW, bool RESID>
+// I8: INT8 codes (h3_gemm_i8_256's operands), v_dot4_i32_i8 on k-steps of
+// 128 k; the layout and the 16 bytes per lane are the same.
+template <int MR, int NW, int U, int RW, bool RESID, bool I8 = false>
 __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint32_t* __restrict__ a, int a_words,
                                                           const float* __restrict__ as, const uint32_t* __restrict__ w,
                                                           const float* __restrict__ ws, int64_t M, int N, int kb,
@@ -1155,7 +1157,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint32_t* __
 #pragma unroll
         for (int m = 0; m < MR; ++m)
 #pragma unroll
-          for (int c = 0; c < 4; ++c) acc[j][m] = __builtin_amdgcn_sdot8(wv[u][j][c], av[u][m][c], acc[j][m], false);
+          for (int c = 0; c < 4; ++c)
+            acc[j][m] = I8 ? __builtin_amdgcn_sdot4(wv[u][j][c], av[u][m][c], acc[j][m], false)
+                           : __builtin_amdgcn_sdot8(wv[u][j][c], av[u][m][c], acc[j][m], false);
   }
   // Sum the 8 segments of each row: lane xor 1 and xor 2 by DPP quad_perm
   // [1,0,3,2] and [2,3,0,1], then lane xor 4 by a swizzle; every lane of the
@@ -1182,7 +1186,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint32_t* __
 #endif
 }
 
-template <int MR, bool RESID>
+template <int MR, bool RESID, bool I8>
 hipError_t launch_decode_mr(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                             int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
   // 16 columns and 8 waves per workgroup: N12288 gives 768 workgroups, three
@@ -1190,30 +1194,35 @@ hipError_t launch_decode_mr(const uint32_t* a, int a_words, const float* as, con
   // Two k-steps per round where K has them (measured against one, and
   // against 4 or 16 waves: M1 N12288 K4096 2.9 us with the weight in the
   // last-level cache, 6.3 us streaming it from HBM).
-  const int kb = k / 256;
-  if (kb >= 16)
-    gemm_decode_kernel<MR, 8, 2, 16, RESID><<<(unsigned)(n / 16), 512, 0, stream>>>(a, a_words, as, w, ws, m, n, kb,
-                                                                                 residual, out);
+  // Four per round for 32 k-steps or more (INT8 K4096) with at most two rows.
+  const int kb = I8 ? k / 128 : k / 256;
+  if (MR <= 2 && kb >= 32)
+    gemm_decode_kernel<MR, 8, 4, 16, RESID, I8><<<(unsigned)(n / 16), 512, 0, stream>>>(a, a_words, as, w, ws, m, n,
+                                                                                     kb, residual, out);
+  else if (kb >= 16)
+    gemm_decode_kernel<MR, 8, 2, 16, RESID, I8><<<(unsigned)(n / 16), 512, 0, stream>>>(a, a_words, as, w, ws, m, n,
+                                                                                     kb, residual, out);
   else
-    gemm_decode_kernel<MR, 8, 1, 16, RESID><<<(unsigned)(n / 16), 512, 0, stream>>>(a, a_words, as, w, ws, m, n, kb,
-                                                                                 residual, out);
+    gemm_decode_kernel<MR, 8, 1, 16, RESID, I8><<<(unsigned)(n / 16), 512, 0, stream>>>(a, a_words, as, w, ws, m, n,
+                                                                                     kb, residual, out);
   return hipGetLastError();
 }
 
-template <bool RESID>
+template <bool RESID, bool I8>
 hipError_t launch_decode_m(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                            int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
-  if (m == 1) return launch_decode_mr<1, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-  if (m == 2) return launch_decode_mr<2, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-  if (m <= 4) return launch_decode_mr<4, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-  if (m <= 8) return launch_decode_mr<8, RESID>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (m == 1) return launch_decode_mr<1, RESID, I8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (m == 2) return launch_decode_mr<2, RESID, I8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (m <= 4) return launch_decode_mr<4, RESID, I8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (m <= 8) return launch_decode_mr<8, RESID, I8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
   return hipErrorInvalidValue;
 }
 
+template <bool I8 = false>
 hipError_t launch_decode(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                          int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
-  if (residual) return launch_decode_m<true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
-  return launch_decode_m<false>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  if (residual) return launch_decode_m<true, I8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
+  return launch_decode_m<false, I8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
 }
 
 // Mid-sized G1 with the K split inside the workgroup: output tiles of 32 MT
@@ -1534,8 +1543,10 @@ int gemm_config_count() { return kGemmConfigs; }
 
 hipError_t launch_gemm_i8(const uint32_t* a, int a_words, const float* as, const uint32_t* w, const float* ws,
                           int64_t m, int n, int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
-  // Few rows: the skinny kernel with one 32-row block (graph replay, M1 N12288 K4096: 16.4 us against 24.2;
-  // at M64 the two-block form loses to 128x128 tiles, 34.1 us against 24.7, on the 50 MB INT8 weight).
+  // At most 8 rows: the dot-product kernel (v_dot4_i32_i8); up to 32 the skinny kernel with one 32-row
+  // block (graph replay, M1 N12288 K4096: 16.4 us against 24.2 for 128x128 tiles; at M64 the two-block
+  // form loses to 128x128 tiles, 34.1 us against 24.7, on the 50 MB INT8 weight).
+  if (m <= 8) return launch_decode<true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
   if (m <= 32) return launch_skinny_any<true>(a, a_words, as, w, ws, m, n, k, residual, out, stream);
   if (n % 256 == 0 && m >= 1024)
     return launch_dma8_any<Dma256x256W8>(a, a_words, as, w, ws, m, n, k, residual, out, stream);

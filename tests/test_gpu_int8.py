@@ -70,3 +70,18 @@ def test_i8_gemm_extreme_codes_and_nonfinite_rows():
     w[1::2] = -2.0e38
     got, want = run(BF(x), BF(w))
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+@pytest.mark.parametrize("n,k", [(256, 256), (512, 2304), (1024, 4096), (256, 12288)])
+def test_i8_gemm_decode_rows_match_oracle(m, n, k):
+    """At most 8 rows: the v_dot4_i32_i8 kernel, k-steps of 128 k (2 to 96 of
+    them over its 8 waves), with and without the residual."""
+    rng = np.random.default_rng(m * 100 + n + k)
+    x = BF(rng.standard_normal((m, k)).astype(np.float32))
+    w = BF((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    got, want = run(x, w)
+    assert np.array_equal(got, want), f"{np.sum(got != want)} mismatches"
+    res = BF(rng.standard_normal((m, n)).astype(np.float32))
+    got, want = run(x, w, res)
+    assert np.array_equal(got, want), f"residual: {np.sum(got != want)} mismatches"
