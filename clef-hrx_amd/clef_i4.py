@@ -52,6 +52,8 @@ SIGNATURES = {
     "clef_i4_f6_prepared_bytes": (ctypes.c_int64, [_I64, _I32]),
     "clef_i4_prepare_f6": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
     "clef_i4_prepare_swiglu_f6": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _P]),
+    "clef_i4_project_f6_workspace_bytes": (ctypes.c_size_t, [_I64, _I32]),
+    "clef_i4_project_f6": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _I32, _P, _P, _P, ctypes.c_size_t, _P]),
     "clef_i4_project_workspace_bytes": (_SZ, [_I64, _I32]),
     "clef_i4_project": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _I32, _P, _P, _P, _SZ, _P]),
     "clef_moe_router_logits": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P]),
@@ -527,6 +529,21 @@ def project_f6(a: PreparedF6, w: F6Weight, residual: torch.Tensor | None = None,
     if a.width != w.cols:
         raise ClefError(-1, "unsupported integer projection shape")
     return gemm_f6(a.codes, a.scales, w, residual, out)
+
+
+def project_quantized_f6(x: torch.Tensor, w: F6Weight, residual: torch.Tensor | None = None,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """project_quantized through the bf6 path in one C call
+    (clef_i4_project_f6): x quantized into bf6 in a workspace, then the bf6
+    GEMM. Same output as project_quantized(x, the 4-bit weight)."""
+    m, k = x.shape
+    if out is None:
+        out = _empty((m, w.rows), torch.bfloat16, x.device)
+    nbytes = int(lib().clef_i4_project_f6_workspace_bytes(m, k))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    _check(lib().clef_i4_project_f6(_ptr(x), m, k, _ptr(w.codes), _ptr(w.scales), w.rows, _ptr(residual), _ptr(out),
+                                    _ptr(ws), nbytes, _stream()))
+    return out
 
 
 def project_prepared_f6(a: Prepared, w: F6Weight, residual: torch.Tensor | None = None,

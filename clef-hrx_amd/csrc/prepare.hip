@@ -233,9 +233,16 @@ __device__ __forceinline__ void pack_codes_f6(const float* v, float inv, bool va
   o[0] = o[1] = o[2] = 0;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
+    // r = the code as an exact f32 (the biased sum minus the bias). For
+    // 1 <= |r| <= 7 its bits 21..30 are (exponent << 2) | top two mantissa
+    // bits, exponent 127..129, so that field minus (127 - 3) << 2 is the e3m2
+    // magnitude (bias 3); the saturating subtraction gives 0 for r = +0, and
+    // the f32 sign bit moves to bit 5. Equal to e3m2_of_nibble of the code.
     float t = v[i] * inv + magic;
     t = __builtin_fminf(__builtin_fmaxf(t, magic - 7.0f), magic + 7.0f);
-    const uint32_t e = e3m2_of_nibble(as_uint(t) & 0xfu);
+    const uint32_t b = as_uint(t - magic);
+    const uint32_t field = (b >> 21) & 0x3ffu;
+    const uint32_t e = (field > 496u ? field - 496u : 0u) | ((b >> 26) & 0x20u);
     const int bit = 6 * i, d = bit >> 5, sh = bit & 31;
     o[d] |= e << sh;
     if (sh > 26) o[d + 1] |= e >> (32 - sh);

@@ -239,6 +239,18 @@ int clef_i4_project(const uint16_t* x, int64_t m, int32_t k, const uint32_t* w_t
                     const float* w_scales, int32_t n, const uint16_t* residual, uint16_t* out,
                     void* workspace, size_t workspace_bytes, clef_stream_t stream);
 
+/* The same projection on the bf6 form of the codes (no counterpart in the
+ * reference): x quantized straight into bf6 (clef_i4_prepare_f6) into the
+ * workspace, then clef_i4_gemm_f6 with the bf6 weight (clef_i4_f6_weight of
+ * the 4-bit tiled weight) and its f32 scales. Same bf16 output as
+ * clef_i4_project bit for bit. Preconditions: those of clef_i4_prepare_f6 and
+ * clef_i4_gemm_f6; workspace_bytes >= clef_i4_project_f6_workspace_bytes(m, k)
+ * -> "workspace too small". */
+size_t clef_i4_project_f6_workspace_bytes(int64_t m, int32_t k);
+int clef_i4_project_f6(const uint16_t* x, int64_t m, int32_t k, const uint8_t* w_f6, const float* w_scales,
+                       int32_t n, const uint16_t* residual, uint16_t* out, void* workspace,
+                       size_t workspace_bytes, clef_stream_t stream);
+
 /* ------------------------------------------------------------------ MoE */
 
 /* Top-k router: ties -> lowest expert id, softmax over the selected logits,

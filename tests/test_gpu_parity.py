@@ -1026,3 +1026,16 @@ def test_gemm_ksplit_matches_oracle(m, n, k):
     got_r = clef_i4.project_prepared(a, qw, residual=to_dev_bf16(res), config=5)
     assert_same_u16(bf16_host(got_r), want_r, f"ksplit residual m={m} n={n} k={k}")
     assert_same_u16(bf16_host(clef_i4.project_prepared(a, qw)), want, f"auto m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("m,n,k,resid", [(5, 256, 512, True), (1000, 768, 2048, False)])
+def test_project_quantized_f6_matches_project_quantized(m, n, k, resid):
+    """clef_i4_project_f6 (bf6 quantize + GEMM in one call) against
+    clef_i4_project on the same bf16 input and weight, bit for bit."""
+    rng = np.random.default_rng(m + k)
+    x = to_dev_bf16(randn_bf16(rng, (m, k)))
+    qw = clef_i4.load_quantized_weight(to_dev_bf16(randn_bf16(rng, (n, k), std=0.02)))
+    res = to_dev_bf16(randn_bf16(rng, (m, n))) if resid else None
+    want = bf16_host(clef_i4.project_quantized(x, qw, residual=res))
+    got = bf16_host(clef_i4.project_quantized_f6(x, clef_i4.f6_weight(qw), residual=res))
+    assert_same_u16(got, want, f"project_quantized_f6 m={m} n={n} k={k}")
