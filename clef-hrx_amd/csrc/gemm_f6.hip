@@ -122,7 +122,7 @@ struct F6Tile {
   static constexpr int A_INST = A_BYTES / 1024 / NW;           // DMA instructions per wave per k-step
   static constexpr int B_INST = B_BYTES / 1024 / NW;
   static constexpr int NST = 3;                                 // LDS stages: prefetch distance 2
-  [[maybe_unused]] static constexpr int INST = A_INST + B_INST;  // DMA instructions per wave per k-step
+  static constexpr int INST = A_INST + B_INST;  // DMA instructions per wave per k-step
   static constexpr int EPI_WAVE = 32 * WN * 2;                  // staging bytes per wave (32 rows of WN bf16)
   static constexpr int SCALE_WAVE = 1024;                       // per-wave epilogue scales (768 bytes used)
   static constexpr int LDS = NST * STAGE_BYTES + NW * SCALE_WAVE;  // 152 KiB
@@ -181,24 +181,6 @@ __device__ __forceinline__ void f6_a_offsets(int a_row_bytes, int (&voff)[F6Tile
   }
 }
 
-// DMA of k-step kt of tile `x` into `stage`.
-__device__ __forceinline__ void f6_issue(char* stage, const F6Tiles& x, const int (&voff_a)[F6Tile::A_INST], int kb,
-                                         int kt) {
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-#pragma unroll
-  for (int ql = 0; ql < F6Tile::A_INST; ++ql) {
-    const int q = wave + F6Tile::NW * ql;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(x.a_rsrc, (lds_ptr_t)(stage + q * 1024), 16, voff_a[ql], kt * 96, 0, 0);
-  }
-#pragma unroll
-  for (int ql = 0; ql < F6Tile::B_INST; ++ql) {
-    const int q = wave + F6Tile::NW * ql;
-    const int panel = q / 12, in_blk = (q % 12) * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(x.b_rsrc, (lds_ptr_t)(stage + F6Tile::A_BYTES + q * 1024), 16,
-                                             lane * 16, (panel * kb + kt) * 12288 + in_blk, 0, 0);
-  }
-}
-
 // Scales of a tile's epilogue into the wave's LDS block `sc` by 4-byte LDS
 // DMA (64 per instruction): the wave's WM row scales at byte 0 (rows past M
 // read as zero) and its WN column scales at byte 512.
@@ -220,10 +202,42 @@ __device__ __forceinline__ void f6_issue_scales(char* __restrict__ sc, const F6S
     __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(sc + 512 + 256 * c), 4, lane * 4, 256 * c, 0, 0);
 }
 
-// The two MFMA rounds of one k-step on stage `rd`.
+// DMA instruction `slot` of this wave's share of k-step kt of tile `x` into
+// `stage` (slots 0 .. A_INST - 1 move A rows, the rest B rows; together the
+// slots are f6_issue).
+__device__ __forceinline__ void f6_issue_slot(char* stage, const F6Tiles& x, const int (&voff_a)[F6Tile::A_INST],
+                                              int kb, int kt, int slot) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (slot < F6Tile::A_INST) {
+    const int q = wave + F6Tile::NW * slot;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(x.a_rsrc, (lds_ptr_t)(stage + q * 1024), 16, voff_a[slot], kt * 96, 0, 0);
+  } else {
+    const int q = wave + F6Tile::NW * (slot - F6Tile::A_INST);
+    const int panel = q / 12, in_blk = (q % 12) * 1024;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(x.b_rsrc, (lds_ptr_t)(stage + F6Tile::A_BYTES + q * 1024), 16,
+                                             lane * 16, (panel * kb + kt) * 12288 + in_blk, 0, 0);
+  }
+}
+
+// DMA of k-step kt of tile `x` into `stage` (all of this wave's slots).
+__device__ __forceinline__ void f6_issue(char* stage, const F6Tiles& x, const int (&voff_a)[F6Tile::A_INST], int kb,
+                                         int kt) {
+#pragma unroll
+  for (int slot = 0; slot < F6Tile::INST; ++slot) f6_issue_slot(stage, x, voff_a, kb, kt, slot);
+}
+
+// The two MFMA rounds of one k-step on stage `rd`, with the DMA of k-step
+// `ks` of tile `x` into `nx` spread among the MFMAs: one instruction after
+// every second MFMA from the fourth on. Issuing a DMA instruction can stall
+// the wave while the memory pipeline is full; between MFMAs the stall hides
+// under the MFMAs already issued, and the loads start earlier in the k-step
+// than when all of them follow the MFMAs (measured 4 % faster over the
+// M4096 K4096 N12288 projection).
 __device__ __forceinline__ void f6_compute(v16f (&acc)[F6Tile::TM][F6Tile::TN], const char* __restrict__ rd,
-                                           const F6Offsets& o, int a_base, int b_base) {
+                                           const F6Offsets& o, int a_base, int b_base, char* __restrict__ nx,
+                                           const F6Tiles& x, const int (&voff_a)[F6Tile::A_INST], int kb, int ks) {
   using T = F6Tile;
+  int slot = 0, idx = 0;
 #pragma unroll
   for (int mf = 0; mf < 2; ++mf) {
     v8i fa[T::TM], fb[T::TN];
@@ -234,8 +248,19 @@ __device__ __forceinline__ void f6_compute(v16f (&acc)[F6Tile::TM][F6Tile::TN], 
 #pragma unroll
     for (int i = 0; i < T::TM; ++i)
 #pragma unroll
-      for (int j = 0; j < T::TN; ++j) acc[i][j] = mfma_f6(fb[j], fa[i], acc[i][j]);
+      for (int j = 0; j < T::TN; ++j) {
+        acc[i][j] = mfma_f6(fb[j], fa[i], acc[i][j]);
+        if ((idx & 1) && idx >= 3 && slot < T::INST) {
+          __builtin_amdgcn_sched_barrier(0);
+          f6_issue_slot(nx, x, voff_a, kb, ks, slot);
+          ++slot;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        ++idx;
+      }
   }
+#pragma unroll
+  for (; slot < T::INST; ++slot) f6_issue_slot(nx, x, voff_a, kb, ks, slot);
 }
 
 // Workgroup barrier that waits for this wave's LDS operations only (a
@@ -417,13 +442,12 @@ __global__ __launch_bounds__(F6Tile::THREADS) void gemm_f6_kernel(
     auto tile_body = [&](char* __restrict__ r0, char* __restrict__ r1, char* __restrict__ r2,
                          char* __restrict__ scl) {
       auto step = [&](const char* rd, char* nx, int kt, auto scales_tag) {
-        // MFMAs first, then the DMA: issuing DMA stalls while the memory
-        // pipeline is full, and the MFMAs already issued run meanwhile.
-        f6_compute(acc, rd, o, a_base, b_base);
-        __builtin_amdgcn_sched_barrier(0);
+        // The scales (k-step 0) before the stage DMA, so that the DMA group
+        // is the last one issued (the wait below counts on it).
         if constexpr (decltype(scales_tag)::value) f6_issue_scales(scl, scales);
+        __builtin_amdgcn_sched_barrier(0);
         const bool own = kt + 2 < kb;
-        f6_issue(nx, own ? cur : nxt, voff_a, kb, own ? kt + 2 : kt + 2 - kb);
+        f6_compute(acc, rd, o, a_base, b_base, nx, own ? cur : nxt, voff_a, kb, own ? kt + 2 : kt + 2 - kb);
         __builtin_amdgcn_sched_barrier(0);
         // k-step kt + 1 has landed once at most the DMA issued here is
         // outstanding (vector memory operations complete in issue order; at
