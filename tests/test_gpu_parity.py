@@ -1009,6 +1009,9 @@ def test_gemm_decode_extreme_codes_and_scales(m):
 @pytest.mark.parametrize("m,n,k", [
     (100, 8192, 768),     # 64x64 tiles, 3 k-steps for 8 waves, ragged last row tile
     (512, 2048, 2048),    # 64x64 tiles: the 512 x 2048 x 2048 linear
+    (65, 12288, 256),     # 64x64 tiles, one k-step (seven waves without one)
+    (200, 4096, 4864),    # 64x64 tiles, 19 k-steps (waves with 2 and 3 k-steps)
+    (64, 12288, 4096),    # 64x64 tiles, exactly one row tile
     (20, 12288, 2304),    # 32x64 tiles (m <= 32), 9 k-steps
     (40, 1024, 12544),    # 32x32 tiles, two stages per wave, 49 k-steps
     (9, 128, 256),        # one k-step, one tile column
