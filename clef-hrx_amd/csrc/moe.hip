@@ -21,7 +21,7 @@ namespace {
 __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ logits, int dtype,
                                                     int64_t tokens, int experts, int topk,
                                                     float* __restrict__ routes) {
-  route_impl::route_body(logits, dtype, tokens, experts, topk, routes, blockIdx.x);
+  route_impl::route_block(logits, dtype, tokens, experts, topk, routes, blockIdx.x);
 }
 
 // ---------------------------------------------------------------- grouping
@@ -502,7 +502,8 @@ hipError_t launch_router_gate(const uint16_t* x, const uint16_t* w, int64_t toke
 
 hipError_t launch_route(const void* logits, int dtype, int64_t tokens, int experts, int topk,
                         float* routes, hipStream_t stream) {
-  const int64_t blocks = (tokens + 3) / 4;
+  const int per = route_impl::route_tokens_per_block(topk);
+  const int64_t blocks = (tokens + per - 1) / per;
   route_kernel<<<(unsigned)blocks, 256, 0, stream>>>(logits, dtype, tokens, experts, topk, routes);
   return hipGetLastError();
 }

@@ -525,7 +525,7 @@ __global__ __launch_bounds__(256) void prepare_loop_kernel(Src src, int64_t rows
 }
 
 // The router and the INT4 quantizer of the MoE input in one launch: the first
-// route_blocks workgroups route four tokens each, the others run the
+// route_blocks workgroups route the tokens (16 or 4 per workgroup), the others run the
 // grid-stride quantizer. Neither needs the other's output, so they share the
 // GPU instead of running one after the other.
 __global__ __launch_bounds__(256) void route_prepare_kernel(const void* __restrict__ logits, int dtype,
@@ -534,7 +534,7 @@ __global__ __launch_bounds__(256) void route_prepare_kernel(const void* __restri
                                                             PlainSource src, int width, int out_words,
                                                             uint32_t* __restrict__ out) {
   if ((int64_t)blockIdx.x < route_blocks) {
-    route_impl::route_body(logits, dtype, tokens, experts, topk, routes, blockIdx.x);
+    route_impl::route_block(logits, dtype, tokens, experts, topk, routes, blockIdx.x);
     return;
   }
   prepare_loop_body<4, PlainSource>(src, tokens, width, out_words, out, blockIdx.x - route_blocks,
@@ -650,7 +650,8 @@ hipError_t launch_route_prepare(const void* logits, int dtype, int64_t tokens, i
   const int per_block = 16 / (width / 256);
   const int64_t blocks = (tokens + per_block - 1) / per_block;
   const int64_t prep = blocks < 2048 ? blocks : 2048;
-  const int64_t route_blocks = (tokens + 3) / 4;
+  const int per = route_impl::route_tokens_per_block(topk);
+  const int64_t route_blocks = (tokens + per - 1) / per;
   route_prepare_kernel<<<(unsigned)(route_blocks + prep), 256, 0, stream>>>(
       logits, dtype, tokens, experts, topk, routes, route_blocks, PlainSource{x}, width, stride / 8, out);
   return hipGetLastError();

@@ -110,5 +110,120 @@ __device__ __forceinline__ void route_body(const void* __restrict__ logits, int 
   }
 }
 
+// Reductions over one 16-lane DPP row (every lane ends with the row's result).
+__device__ __forceinline__ float row_max(float v) {
+  v = __builtin_fmaxf(v, as_float((uint32_t)dpp_row<0xB1>((int)as_uint(v))));
+  v = __builtin_fmaxf(v, as_float((uint32_t)dpp_row<0x4E>((int)as_uint(v))));
+  v = __builtin_fmaxf(v, as_float((uint32_t)dpp_row<0x124>((int)as_uint(v))));
+  return __builtin_fmaxf(v, as_float((uint32_t)dpp_row<0x128>((int)as_uint(v))));
+}
+
+__device__ __forceinline__ int row_min(int v) {
+  int o = dpp_row<0xB1>(v);
+  v = o < v ? o : v;
+  o = dpp_row<0x4E>(v);
+  v = o < v ? o : v;
+  o = dpp_row<0x124>(v);
+  v = o < v ? o : v;
+  o = dpp_row<0x128>(v);
+  return o < v ? o : v;
+}
+
+// Tokens per 256-thread workgroup of route_body16.
+constexpr int kRouteTokens16 = 16;
+
+// The same router with 16 lanes per token (topk <= 16): each 16-lane DPP row
+// of a wave routes one token, four per wave, and lane i of the row holds
+// expert slots 8i .. 8i+7. A rank is a row maximum (fmaxf: the order of the
+// maxima does not matter, NaN is ignored), the lowest valid slot holding it
+// (a row minimum of candidate ids) and that slot reset to -FLT_MAX: a third
+// of the instructions per token of the one-wave-per-token body, whose
+// reductions span 64 lanes for two slots each. Rank r is kept by lane r of
+// the row; the softmax sum runs in rank order over the row's lanes.
+__device__ __forceinline__ void route_body16(const void* __restrict__ logits, int dtype, int64_t tokens,
+                                             int experts, int topk, float* __restrict__ routes, int64_t block) {
+  const int lane = threadIdx.x & 63, li = lane & 15;
+  const int64_t t = block * kRouteTokens16 + (threadIdx.x >> 4);
+  const bool live = t < tokens;  // every lane stays on for the row reductions
+  const int e0 = 8 * li;
+  float v[8];
+  bool valid[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) valid[j] = e0 + j < experts;
+  // 16-byte loads when every row starts on a 16-byte boundary (the C ABI
+  // requires a 16-byte aligned logits pointer); element loads otherwise.
+  if (live && dtype == 0 && experts % 8 == 0 && e0 < experts) {
+    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(logits) + t * experts + e0);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = bf16_lo(w[j]);
+      v[2 * j + 1] = bf16_hi(w[j]);
+    }
+  } else if (live && dtype == 1 && experts % 4 == 0 && e0 < experts) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(logits) + t * experts + e0);
+    const float4 a = p[0];
+    const float4 b = e0 + 4 < experts ? p[1] : make_float4(kNegMax, kNegMax, kNegMax, kNegMax);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e = e0 + j;
+      if (!live || e >= experts)
+        v[j] = kNegMax;
+      else if (dtype == 0)
+        v[j] = bf16_to_f32(static_cast<const uint16_t*>(logits)[t * experts + e]);
+      else
+        v[j] = static_cast<const float*>(logits)[t * experts + e];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (!valid[j]) v[j] = kNegMax;
+  float rv = 0.0f;  // this lane's rank (r == li): value and id
+  int rid = 0;
+  for (int r = 0; r < topk; ++r) {
+    float m = v[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) m = __builtin_fmaxf(m, v[j]);
+    const float best = row_max(m);
+    int cand = kInvalidId;
+#pragma unroll
+    for (int j = 7; j >= 0; --j)
+      if (valid[j] && v[j] == best) cand = e0 + j;
+    const int id = row_min(cand);
+    if (li == r) {
+      rv = best;
+      rid = id;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (id == e0 + j) v[j] = kNegMax;
+  }
+  // exp of every rank in parallel, the sum in rank order (the reference's
+  // sequential loop) from the row's lanes, the divisions in parallel.
+  const int row0 = lane & 48;
+  const float vmax = __shfl(rv, row0, 64);
+  const float p = li < topk ? cephes_expf(rv - vmax) : 0.0f;
+  float sum = 0.0f;
+  for (int r = 0; r < topk; ++r) sum = sum + __shfl(p, row0 + r, 64);
+  if (live && li < topk) {
+    float* out = routes + t * 2 * topk;
+    out[li] = (float)rid;
+    out[topk + li] = bf16_round(p / sum);
+  }
+}
+
+// Tokens per 256-thread workgroup for a topk, and the body that routes them.
+__host__ __device__ __forceinline__ int route_tokens_per_block(int topk) { return topk <= 16 ? kRouteTokens16 : 4; }
+
+__device__ __forceinline__ void route_block(const void* __restrict__ logits, int dtype, int64_t tokens, int experts,
+                                            int topk, float* __restrict__ routes, int64_t block) {
+  if (topk <= 16)
+    route_body16(logits, dtype, tokens, experts, topk, routes, block);
+  else
+    route_body(logits, dtype, tokens, experts, topk, routes, block);
+}
+
 }  // namespace route_impl
 }  // namespace clef

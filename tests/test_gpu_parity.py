@@ -417,6 +417,33 @@ def test_route_matches_oracle(dtype, experts, topk):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "route probabilities"
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("experts,topk", [(128, 8), (100, 16), (66, 8), (72, 16), (128, 24), (72, 17), (8, 8)])
+def test_route_edge_values_match_oracle(dtype, experts, topk):
+    """Rows with quiet NaNs (ignored by the maximum), -inf, -FLT_MAX and
+    all-equal values (no +inf: exp(inf - inf) makes the probabilities NaN,
+    whose bits are not part of the contract); topk up to 16 runs 16 lanes per token, above that one
+    wave per token; rows of 100 or 66 experts are read element by element
+    (their row starts are not 16-byte aligned). Ids and probability bits
+    against the oracle."""
+    rng = np.random.default_rng(experts * 7 + topk)
+    tokens = 97
+    logits = tie_logits(rng, tokens, experts, "f32")
+    logits[5::6, ::5] = np.nan
+    logits[4::13, ::2] = -np.inf
+    logits[7::17] = -np.inf
+    logits[7::17, 3] = 1.5
+    logits[8::19, :] = 2.0
+    logits[9::23, ::3] = -3.402823466e38
+    if dtype == "bf16":
+        logits = BF(logits)
+    want = oracle.route(logits, topk)
+    dev = to_dev_bf16(logits) if dtype == "bf16" else to_dev_f32(logits)
+    got = clef_i4.omni_route(dev, topk).cpu().numpy()
+    assert np.array_equal(got[:, :topk], want[:, :topk]), "route ids"
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "route probabilities"
+
+
 def test_route_ids_are_stable_sort():
     """The selected ids equal a stable descending sort (src/omni.rs:997-1009)."""
     rng = np.random.default_rng(5)
