@@ -81,10 +81,14 @@ __device__ void build_masks(const float* __restrict__ routes, int64_t tokens, in
   __syncthreads();
 }
 
+// Block 0 also zeroes the workspace counter of group_scan_wide_kernel, which
+// runs after this kernel on the same stream.
 template <int KT>
 __global__ __launch_bounds__(64) void group_count_kernel(const float* __restrict__ routes, int64_t tokens,
-                                                         int topk, int* __restrict__ block_counts) {
+                                                         int topk, int* __restrict__ block_counts,
+                                                         unsigned* __restrict__ done) {
   __shared__ unsigned long long masks[128];
+  if (blockIdx.x == 0 && threadIdx.x == 0) *done = 0u;
   build_masks<KT>(routes, tokens, topk, masks);
   const int lane = threadIdx.x;
   int* dst = block_counts + (int64_t)blockIdx.x * 128;
@@ -165,6 +169,75 @@ __global__ __launch_bounds__(1024) void group_scan_kernel(int* __restrict__ bloc
   if (j == 7) groups[(int64_t)e * (tokens + 1)] = (float)run;
   if (schedule == nullptr) return;
   write_tile_schedule(run, j == 7, e, bm, tiles_scan, schedule);  // run of thread j == 7 is e's count
+}
+
+// The same scan with one 256-thread workgroup per expert, for many blocks
+// (above kGroupScanWideBlocks one workgroup's serial runs dominate: 34 us at
+// 65536 tokens). Workgroup e scans expert e's column of block counts (each
+// thread a contiguous run of blocks, then a workgroup scan of the run sums)
+// and writes groups[e][0]. The tile schedule needs every expert's count: the
+// workgroup that finishes last (a counter in the workspace, set to zero by
+// group_count_kernel earlier on the stream) writes it.
+constexpr int64_t kGroupScanWideBlocks = 64;
+
+__global__ __launch_bounds__(256) void group_scan_wide_kernel(int* __restrict__ block_counts, int64_t blocks,
+                                                              int64_t tokens, float* __restrict__ groups,
+                                                              int32_t* __restrict__ schedule, int bm,
+                                                              unsigned* __restrict__ done) {
+  __shared__ int wave_sums[4];
+  __shared__ int tiles_scan[128];
+  __shared__ int last;
+  const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t per = (blocks + 255) / 256;
+  const int64_t b0 = tid * per < blocks ? tid * per : blocks;
+  const int64_t b1 = b0 + per < blocks ? b0 + per : blocks;
+  int sum = 0;
+  for (int64_t b = b0; b < b1; b += 8) {
+    int c[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) c[u] = b + u < b1 ? block_counts[(b + u) * 128 + e] : 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) sum += c[u];
+  }
+  // exclusive prefix of the run sums over the workgroup
+  int incl = sum;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wave_sums[wave] = incl;
+  __syncthreads();
+  int run = incl - sum;
+  for (int w = 0; w < wave; ++w) run += wave_sums[w];
+  const int total = wave_sums[0] + wave_sums[1] + wave_sums[2] + wave_sums[3];
+  for (int64_t b = b0; b < b1; b += 8) {
+    int c[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) c[u] = b + u < b1 ? block_counts[(b + u) * 128 + e] : 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (b + u < b1) {
+        block_counts[(b + u) * 128 + e] = run;
+        run += c[u];
+      }
+  }
+  if (tid == 0) groups[(int64_t)e * (tokens + 1)] = (float)total;
+  if (schedule == nullptr) return;
+  // The last workgroup to finish reads every expert's count (released by the
+  // fence before each workgroup's increment) and writes the tile schedule.
+  if (tid == 0) {
+    __threadfence();
+    last = __hip_atomic_fetch_add(done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  int count = 0;
+  if (tid < 128)
+    count = (int)as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(groups + (int64_t)tid * (tokens + 1)),
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  write_tile_schedule(count, tid < 128, tid & 127, bm, tiles_scan, schedule);
 }
 
 // KT > 0: topk == KT, the token's route ids held in registers; KT == 0: any
@@ -508,9 +581,10 @@ hipError_t launch_route(const void* logits, int dtype, int64_t tokens, int exper
   return hipGetLastError();
 }
 
+// Block counts [blocks][128] and the wide scan's completion counter.
 size_t group_workspace_bytes(int64_t tokens) {
   const int64_t blocks = (tokens + kGroupBlock - 1) / kGroupBlock;
-  return (size_t)blocks * 128 * sizeof(int);
+  return (size_t)blocks * 128 * sizeof(int) + 16;
 }
 
 namespace {
@@ -539,11 +613,15 @@ hipError_t launch_group_routes(const float* routes, int64_t tokens, int topk, fl
   }
   const int64_t blocks = (tokens + kGroupBlock - 1) / kGroupBlock;
   int* counts = static_cast<int*>(workspace);
+  unsigned* done = reinterpret_cast<unsigned*>(counts + blocks * 128);
   if (topk == 8)
-    group_count_kernel<8><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts);
+    group_count_kernel<8><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts, done);
   else
-    group_count_kernel<0><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts);
-  group_scan_kernel<<<1, 1024, 0, stream>>>(counts, blocks, tokens, groups, schedule, schedule_bm);
+    group_count_kernel<0><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts, done);
+  if (blocks > kGroupScanWideBlocks)
+    group_scan_wide_kernel<<<128, 256, 0, stream>>>(counts, blocks, tokens, groups, schedule, schedule_bm, done);
+  else
+    group_scan_kernel<<<1, 1024, 0, stream>>>(counts, blocks, tokens, groups, schedule, schedule_bm);
   if (topk == 8)
     group_scatter_kernel<8><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts, groups, order);
   else

@@ -562,7 +562,7 @@ def test_expert_gemm_matches_oracle(tokens, hidden):
     assert_same_u16(bf16_host(got), want, "expert down")
 
 
-@pytest.mark.parametrize("tokens", [3, 64, 300])
+@pytest.mark.parametrize("tokens", [3, 64, 300, 600])
 @pytest.mark.parametrize("input_routed", [False, True])
 def test_expert_ungrouped_matches_oracle(tokens, input_routed):
     """Engine::omni_expert (src/omni.rs:280-288), the expert GEMM without a
@@ -707,11 +707,12 @@ def test_combine_matches_oracle(ordered, topk):
 
 
 @pytest.mark.parametrize("tokens,hidden,inter", [(5, 512, 256), (96, 2048, 768), (300, 1024, 512),
-                                                 (256, 512, 256), (257, 512, 256)])
+                                                 (256, 512, 256), (257, 512, 256), (4160, 512, 256)])
 def test_moe_layer_matches_oracle(tokens, hidden, inter):
     """Whole Omni INT4 MoE block (src/omni.rs:762-857) bit-exact vs the oracle.
     256 and 257 tokens (2048 and 2056 routed rows) sit on either side of the
-    switch from 32-slot to 128-slot expert tiles."""
+    switch from 32-slot to 128-slot expert tiles; 4160 tokens (65 blocks of
+    64) take the grouping scan with one workgroup per expert."""
     rng = np.random.default_rng(tokens + hidden)
     x = randn_bf16(rng, (tokens, hidden))
     logits = BF(rng.standard_normal((tokens, 128)).astype(np.float32))
