@@ -637,12 +637,25 @@ __global__ __launch_bounds__(128) void tile_list_kernel(const float* __restrict_
     scan[e] += v;
     __syncthreads();
   }
-  const int start = scan[e] - tiles;
-  for (int t = 0; t < tiles; ++t) {
-    list[1 + 2 * (start + t)] = (OutT)e;
-    list[2 + 2 * (start + t)] = (OutT)(t * bm);
+  // scan[e] is now the inclusive prefix: expert e owns tiles
+  // scan[e] - tiles .. scan[e] - 1. Every thread writes entries; tile t's
+  // expert is the first whose inclusive prefix exceeds t (one expert can own
+  // hundreds of tiles under skewed routing).
+  const int total = scan[127];
+  for (int t = e; t < total; t += 128) {
+    int lo = 0, hi = 127;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (scan[mid] > t)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+    const int first = lo > 0 ? scan[lo - 1] : 0;
+    list[1 + 2 * t] = (OutT)lo;
+    list[2 + 2 * t] = (OutT)((t - first) * bm);
   }
-  if (e == 127) list[0] = (OutT)scan[127];
+  if (e == 127) list[0] = (OutT)total;
 }
 
 // Grouped expert GEMM on the half-k-step core: 128 expert slots x 256 weight
