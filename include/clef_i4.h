@@ -347,6 +347,25 @@ int clef_moe_expert_gate_up_i4(const uint32_t* a, int32_t stride, const float* a
                                int32_t k, int32_t n, uint16_t* h, void* workspace,
                                size_t workspace_bytes, clef_stream_t stream);
 
+/* E1 and the fused gate/up on the bf6 form of the codes (no counterpart in
+ * the reference: a gfx950 re-encoding of the same INT4 codes). `a` holds bf6
+ * activation rows (clef_i4_prepare_f6 / clef_i4_f6_activation, k*3/4 bytes
+ * per row), the weights are clef_i4_f6_weight of the tiled expert weights
+ * (e * n rows). Every code is exact in bf6 and the f32 sums of integer dots
+ * are exact for k < 2^18, so out / h equal clef_moe_expert_i4 /
+ * clef_moe_expert_gate_up_i4 on the same codes bit for bit. Workspace: as
+ * clef_moe_expert_i4. Preconditions: those of clef_moe_expert_i4 /
+ * clef_moe_expert_gate_up_i4 (with the messages named there) and k >= 512;
+ * the bf6 activation operand under 2 GiB and routes * n * 2 bytes of output
+ * at most 2 GiB -> the shape message of each entry. */
+int clef_moe_expert_f6(const uint8_t* a, const float* a_scales, const uint8_t* w_f6, const float* w_scales,
+                       const float* groups, int64_t tokens, int32_t topk, int32_t k, int32_t n, int32_t input_routed,
+                       uint16_t* out, void* workspace, size_t workspace_bytes, clef_stream_t stream);
+int clef_moe_expert_gate_up_f6(const uint8_t* a, const float* a_scales, const uint8_t* gate_f6, const float* gate_s,
+                               const uint8_t* up_f6, const float* up_s, const float* groups, int64_t tokens,
+                               int32_t topk, int32_t k, int32_t n, uint16_t* h, void* workspace,
+                               size_t workspace_bytes, clef_stream_t stream);
+
 /* h = bf16(bf16(g/(1+exp(-g))) * u) elementwise over n values. Replaces
  * Engine::swiglu (src/ops.rs:9-29) and kernels/swiglu.loom. Precondition:
  * n >= 0 -> "SwiGLU shape/dtype mismatch". */
