@@ -29,12 +29,14 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 CLEF_HD uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
-CLEF_HD uint32_t f32_to_bf16(float f) { return pack_bf16x2(f, 0.0f) & 0xffffu; }
+// bf16(+0) is 0x0000, so the other half of the pair needs no mask: each of
+// these is the one conversion instruction.
+CLEF_HD uint32_t f32_to_bf16(float f) { return pack_bf16x2(f, 0.0f); }
 
 CLEF_HD float bf16_to_f32(uint32_t h) { return as_float(h << 16); }
 __device__ __forceinline__ float bf16_lo(uint32_t pair) { return as_float(pair << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t pair) { return as_float(pair & 0xffff0000u); }
-CLEF_HD float bf16_round(float f) { return as_float(pack_bf16x2(0.0f, f) & 0xffff0000u); }
+CLEF_HD float bf16_round(float f) { return as_float(pack_bf16x2(0.0f, f)); }
 
 // exp(x) by Cody-Waite reduction with ln 2 split as 0.693359375 - 2.12194440e-4
 // and the degree-5 minimax polynomial of the Cephes expf (S. L. Moshier, Cephes

@@ -200,3 +200,41 @@ def test_moe_layer_skewed_65536_tokens():
     counts = groups[:, 0]
     assert (counts == 0).sum() >= 8
     assert counts.max() > 20000
+
+
+@pytest.mark.parametrize("tokens,skewed", [(32768, False), (40000, True)])
+def test_expert_down_matches_row_halves(tokens, skewed):
+    """The routed expert GEMM at the down projection's shape (K 768 -> N 2048,
+    top-8) over 262144 and 320000 routed rows. E1 is row-local, so the whole
+    output for `tokens` tokens must equal the outputs for the first and the
+    second half of the tokens computed separately (their own groupings and
+    tile schedules), bit for bit; a sample of tokens is also checked against
+    the oracle's E1 (src/omni.rs:289-534, input_routed)."""
+    seed = 1006 + int(skewed)
+    d, inter, topk = 2048, 768, 8
+    logits = skewed_logits(tokens, seed * 16 + 1) if skewed else randn_bf16((tokens, 128), 1.0, seed * 16 + 1)
+    routes = clef_i4.omni_route(logits, topk)
+    h = randn_bf16((tokens * topk, inter), 1.0, seed * 16 + 2)
+    down = clef_i4.load_quantized_weight(randn_bf16((128 * d, inter), 0.02, seed * 16 + 3))
+    groups, _ = clef_i4.omni_group_routes(routes)
+    full = clef_i4.omni_expert(clef_i4.prepare(h), down, groups, tokens, topk, True)
+    half = tokens // 2
+    parts = []
+    for lo, hi in ((0, half), (half, tokens)):
+        g, _ = clef_i4.omni_group_routes(routes[lo:hi].contiguous())
+        a = clef_i4.prepare(h[lo * topk: hi * topk].contiguous())
+        parts.append(clef_i4.omni_expert(a, down, g, hi - lo, topk, True))
+    torch.cuda.synchronize()
+    assert torch.equal(full.view(torch.int16), torch.cat(parts).view(torch.int16)), "whole against halves"
+    del parts
+
+    rows = sample_rows(tokens, 64, seed)
+    slots = (rows[:, None] * topk + np.arange(topk)[None, :]).ravel()
+    sub_routes = routes[torch.from_numpy(rows).cuda()].cpu().numpy()
+    sub_groups, _ = oracle.group_routes(sub_routes)
+    stride = oracle.activation_stride(inter)
+    codes, scales, _ = oracle.prepare(u16(h[torch.from_numpy(slots).cuda()]), stride)
+    w_codes, w_scales = host_weight(down)
+    want = oracle.expert_i4(codes, scales, w_codes, w_scales, sub_groups, len(rows), topk, inter, d, True)
+    got = u16(full[torch.from_numpy(slots).cuda()])
+    assert_rows(got, want, slots, f"routed expert GEMM tokens={tokens}")

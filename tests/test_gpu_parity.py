@@ -691,12 +691,13 @@ def test_swiglu_every_bf16_gate():
 
 
 @pytest.mark.parametrize("ordered", [True, False])
-@pytest.mark.parametrize("topk", [8, 4])
-def test_combine_matches_oracle(ordered, topk):
+@pytest.mark.parametrize("topk,width", [(8, 2048), (8, 264), (4, 2048)])
+def test_combine_matches_oracle(ordered, topk, width):
     """OmniCombine paired check (src/benchmarking/omni.rs:387-431); top-8 runs
-    the kernel that loads every rank first, other topk the rank-by-rank one."""
-    rng = np.random.default_rng(int(ordered) + 2 * topk)
-    tokens, width = 77, 2048
+    the kernel that loads every rank first, other topk the rank-by-rank one;
+    width 264 leaves a partial last wave of 8-column chunks."""
+    rng = np.random.default_rng(int(ordered) + 2 * topk + width)
+    tokens = 77
     routes = random_routes(rng, tokens, topk=topk)
     _, order = oracle.group_routes(routes, topk=topk)
     values = randn_bf16(rng, (tokens * topk, width), std=2.0)
