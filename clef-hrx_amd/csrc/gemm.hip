@@ -1442,41 +1442,63 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
   const int NW = (int)blockDim.x >> 6;
   __shared__ int red[NA][16][64];  // [gate / up][accumulator register][lane]
   __shared__ int routes_s[32];
+  // The item's schedule entry is read together with the tile count (every
+  // launched item indexes inside the schedule buffer), so the exit test
+  // costs no extra round trip.
   const int64_t item = blockIdx.x;
-  if (item >= (int64_t)schedule[0] * slices) return;
   const int tile = (int)(item / slices);
   const int c0 = (int)(item - (int64_t)tile * slices) * 32;  // first output column within the expert
+  const int tiles = schedule[0];
   const int e = schedule[1 + 2 * tile];
   const int row0 = schedule[2 + 2 * tile];
+  if (item >= (int64_t)tiles * slices || e < 0) return;  // e >= 0 in every listed tile
   const float* list = groups + (int64_t)e * list_stride;
-  const int count = (int)list[0];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lr = lane & 31, h = lane >> 5;
-  for (int i = threadIdx.x; i < NA * 16 * 64; i += NW * 64) (&red[0][0][0])[i] = 0;
-  if (threadIdx.x < 32) routes_s[threadIdx.x] = row0 + (int)threadIdx.x < count ? (int)list[1 + row0 + threadIdx.x] : -1;
-
-  const int my_route = row0 + lr < count ? (int)list[1 + row0 + lr] : -1;
-  const int64_t xr = input_routed ? (int64_t)my_route : (int64_t)my_route / topk;
-  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a, a_bytes);
-  const int a_voff = my_route >= 0 ? (int)(xr * a_words * 4) + 64 * h : (int)0x80000000u;
+  // This lane's slot route, read through a resource bounded to the list (no
+  // wait for the count first; entries past it are masked below).
+  const int64_t cap = list_stride - 1 - row0;
+  const __amdgpu_buffer_rsrc_t l_rsrc =
+      make_rsrc(list + 1 + row0, (uint32_t)((cap < 32 ? (cap > 0 ? cap : 0) : 32) * 4));
+  const float route_f = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(l_rsrc, lr * 4, 0, 0));
+  const int count = (int)list[0];
   const int64_t nrow = (int64_t)e * n + c0;  // first weight row of the slice
   const int w_voff = (int)(nrow % 128 + lr) * 128 + 64 * h;
   const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(w + (nrow / 128) * kb * 4096, (uint32_t)(kb * 16384));
   const __amdgpu_buffer_rsrc_t w2_rsrc = make_rsrc((GU ? w2 : w) + (nrow / 128) * kb * 4096, (uint32_t)(kb * 16384));
+  for (int i = threadIdx.x; i < NA * 16 * 64; i += NW * 64) (&red[0][0][0])[i] = 0;
 
   v16i acc[NA];
 #pragma unroll
   for (int s = 0; s < NA; ++s) acc[s] = v16i{};
   v4i wr[2][NA][4], ar[2][4];
-  auto load = [&](auto buf, int kt) {
+  auto load_w = [&](auto buf, int kt) {
     constexpr int B = decltype(buf)::value;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       wr[B][0][c] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff + 16 * c, kt * 16384, 0);
       if constexpr (GU) wr[B][1][c] = __builtin_amdgcn_raw_buffer_load_b128(w2_rsrc, w_voff + 16 * c, kt * 16384, 0);
-      ar[B][c] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff + 16 * c, kt * 128, 0);
     }
+  };
+  // The first k-step's weights go out right behind the route load; the
+  // activation rows need the route (vector memory completes in issue order,
+  // so waiting for the route leaves the weight loads in flight).
+  const int k0 = wave * kb / NW, k1 = (wave + 1) * kb / NW;  // k0 < k1: NW <= kb
+  load_w(std::integral_constant<int, 0>{}, k0);
+  const int my_route = row0 + lr < count ? (int)route_f : -1;
+  if (threadIdx.x < 32) routes_s[threadIdx.x] = my_route;
+  const int64_t xr = input_routed ? (int64_t)my_route : (int64_t)my_route / topk;
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a, a_bytes);
+  const int a_voff = my_route >= 0 ? (int)(xr * a_words * 4) + 64 * h : (int)0x80000000u;
+  auto load_a = [&](auto buf, int kt) {
+    constexpr int B = decltype(buf)::value;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ar[B][c] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff + 16 * c, kt * 128, 0);
+  };
+  auto load = [&](auto buf, int kt) {
+    load_w(buf, kt);
+    load_a(buf, kt);
   };
   auto compute = [&](auto buf) {
     constexpr int B = decltype(buf)::value;
@@ -1495,17 +1517,14 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
   };
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
-  const int k0 = wave * kb / NW, k1 = (wave + 1) * kb / NW;
-  if (k0 < k1) {
-    load(B0{}, k0);
-    for (int kt = k0;;) {
-      load(B1{}, kt + 1 < k1 ? kt + 1 : kt);
-      compute(B0{});
-      if (++kt >= k1) break;
-      load(B0{}, kt + 1 < k1 ? kt + 1 : kt);
-      compute(B1{});
-      if (++kt >= k1) break;
-    }
+  load_a(B0{}, k0);
+  for (int kt = k0;;) {
+    load(B1{}, kt + 1 < k1 ? kt + 1 : kt);
+    compute(B0{});
+    if (++kt >= k1) break;
+    load(B0{}, kt + 1 < k1 ? kt + 1 : kt);
+    compute(B1{});
+    if (++kt >= k1) break;
   }
   __syncthreads();  // reduction buffer zeroed, slot routes written
 #pragma unroll
