@@ -202,8 +202,40 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
   char* meta_cur = lds + P::META_OFF;
   char* meta_nxt = lds + P::META_OFF + P::META;
 
-  // ---- prologue: the SiLU table and the first item, synchronously
+  // ---- prologue: the first item; the weight rows of its half-step 0 go
+  // out with its route list (they need only the schedule entry), and the
+  // SiLU table after the prologue (the first epilogue reads it).
+  ExpertItem cur{};
+  DmaHCore<T> c;
+  // Stage ring: st[0] holds the item's half-step 0, st[1] half-step 1 (NST
+  // == 3) or is free, st[NST - 1] is free.
+  char* st[3] = {lds, lds + P::STAGE, lds + (P::NST - 1) * P::STAGE};
+  __amdgpu_buffer_rsrc_t b_cur, b_cur2;
+  {
+    const int local = claim();
+    if (local >= mine) return;  // uniform: no item for this workgroup, nothing in flight
+    int e_v, r_v;
+    fetch_entry(local, e_v, r_v, cur.n0);
+    wait_vmcnt<0>();
+    cur.e = __builtin_amdgcn_readfirstlane(e_v);
+    cur.row0 = __builtin_amdgcn_readfirstlane(r_v);
+    const int cnt_v = fetch_lists(cur.e, cur.row0, cur.n0, meta_cur);
+    b_rsrcs(cur.e, cur.n0, b_cur, b_cur2);
+    c.issue_b(st[0], b_cur, b_cur2, kb, 0);
+    // the count, list and scales (issued before the weight rows) have landed
+    wait_vmcnt<T::B_INST>();
+    lds_barrier();
+    cur.count = (int)__builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(cnt_v));
+    cur.valid = true;
+  }
+  int voff_cur[T::A_INST];
+  fetch_rows(cur.row0, cur.count, meta_cur + P::M_ROUTES, meta_cur + P::M_AS, voff_cur);
+  c.issue_a(st[0], a_rsrc, voff_cur, 0, 0);
+  if (P::DIST == 2) c.issue(st[1], a_rsrc, voff_cur, 0, b_cur, b_cur2, kb, 1);
+  wait_vmcnt<(P::DIST - 1) * T::INST>();
+  lds_barrier();
   if constexpr (GU) {
+    // Landed by the end of half-step 0 (its wait covers every earlier load).
     const __amdgpu_buffer_rsrc_t lut_rsrc = make_rsrc(g_silu_lut, kSiluLutSize * 2);
 #pragma unroll
     for (int i = 0; i < kSiluLutSize * 2 / 1024 / T::NW; ++i) {
@@ -212,37 +244,6 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
                                                q * 1024, 0, 0);
     }
   }
-  wait_vmcnt<0>();
-  ExpertItem cur{};
-  {
-    const int local = claim();
-    if (local >= mine) {  // uniform: no item for this workgroup
-      wait_vmcnt<0>();
-      return;
-    }
-    int e_v, r_v;
-    fetch_entry(local, e_v, r_v, cur.n0);
-    wait_vmcnt<0>();
-    cur.e = __builtin_amdgcn_readfirstlane(e_v);
-    cur.row0 = __builtin_amdgcn_readfirstlane(r_v);
-    const int cnt_v = fetch_lists(cur.e, cur.row0, cur.n0, meta_cur);
-    wait_vmcnt<0>();
-    __syncthreads();
-    cur.count = (int)__builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(cnt_v));
-    cur.valid = true;
-  }
-  int voff_cur[T::A_INST];
-  fetch_rows(cur.row0, cur.count, meta_cur + P::M_ROUTES, meta_cur + P::M_AS, voff_cur);
-  __amdgpu_buffer_rsrc_t b_cur, b_cur2;
-  b_rsrcs(cur.e, cur.n0, b_cur, b_cur2);
-  DmaHCore<T> c;
-  // Stage ring: st[0] holds the item's half-step 0, st[1] half-step 1 (NST
-  // == 3) or is free, st[NST - 1] is free.
-  char* st[3] = {lds, lds + P::STAGE, lds + (P::NST - 1) * P::STAGE};
-  c.issue(st[0], a_rsrc, voff_cur, 0, b_cur, b_cur2, kb, 0);
-  if (P::DIST == 2) c.issue(st[1], a_rsrc, voff_cur, 0, b_cur, b_cur2, kb, 1);
-  wait_vmcnt<(P::DIST - 1) * T::INST>();
-  lds_barrier();
 
   v16i acc[T::TM][T::TN];
   const uint16_t* lut = reinterpret_cast<const uint16_t*>(lds + P::LUT_OFF);

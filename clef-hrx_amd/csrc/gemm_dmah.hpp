@@ -98,14 +98,25 @@ struct DmaHCore {
   __device__ __forceinline__ void issue(char* stage, __amdgpu_buffer_rsrc_t a_rsrc, const int (&voff_a)[T::A_INST],
                                         int a_q_stride, __amdgpu_buffer_rsrc_t b_rsrc,
                                         __amdgpu_buffer_rsrc_t b_rsrc2, int ksteps, int j) {
+    issue_a(stage, a_rsrc, voff_a, a_q_stride, j);
+    issue_b(stage, b_rsrc, b_rsrc2, ksteps, j);
+  }
+  // The activation rows (A_INST instructions) and the weight rows (B_INST)
+  // of half-step j separately.
+  __device__ __forceinline__ void issue_a(char* stage, __amdgpu_buffer_rsrc_t a_rsrc, const int (&voff_a)[T::A_INST],
+                                          int a_q_stride, int j) {
     const int kt = j >> 1, half = (j & 1) * 32;
-    char* sb = stage + T::A_BYTES;
 #pragma unroll
     for (int ql = 0; ql < T::A_INST; ++ql) {
       const int q = wave + T::NW * ql;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(stage + q * 1024), 16, voff_a[ql],
                                                16 * q * a_q_stride + kt * 128 + half, 0, 0);
     }
+  }
+  __device__ __forceinline__ void issue_b(char* stage, __amdgpu_buffer_rsrc_t b_rsrc, __amdgpu_buffer_rsrc_t b_rsrc2,
+                                          int ksteps, int j) {
+    const int kt = j >> 1, half = (j & 1) * 32;
+    char* sb = stage + T::A_BYTES;
 #pragma unroll
     for (int ql = 0; ql < T::B_INST; ++ql) {
       const int q = wave + T::NW * ql;
