@@ -252,6 +252,73 @@ __global__ __launch_bounds__(64) void group_scatter_kernel(const float* __restri
                                                            int bm, int32_t* __restrict__ schedule) {
   __shared__ unsigned long long masks[128];
   __shared__ int first[129];
+  if constexpr (KT > 0) {
+    // Every global load at once: the token's route ids, the block's 128
+    // list offsets (to LDS) and, for the tile schedule, the experts' counts.
+    // One round trip instead of ids -> offsets.
+    const int lane = threadIdx.x;
+    const int64_t t = (int64_t)blockIdx.x * kGroupBlock + lane;
+    const bool live = t < tokens;
+    float id[KT];
+#pragma unroll
+    for (int r = 0; r < KT; ++r) id[r] = live ? routes[t * 2 * KT + r] : -1.0f;
+    __shared__ int offs[128];
+    const int* offsets = block_offsets + (int64_t)blockIdx.x * 128;
+    const int o0 = offsets[lane], o1 = offsets[64 + lane];
+    int c0 = 0, c1 = 0;
+    if (schedule != nullptr) {
+      c0 = (int)groups[(int64_t)(2 * lane) * (tokens + 1)];
+      c1 = (int)groups[(int64_t)(2 * lane + 1) * (tokens + 1)];
+    }
+    masks[lane] = 0ull;
+    masks[64 + lane] = 0ull;
+    offs[lane] = o0;
+    offs[64 + lane] = o1;
+    if (schedule != nullptr) {
+      const int t0 = (c0 + bm - 1) / bm, t1 = (c1 + bm - 1) / bm;
+      int incl = t0 + t1;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += v;
+      }
+      first[2 * lane] = incl - t0 - t1;
+      first[2 * lane + 1] = incl - t1;
+      if (lane == 63) {
+        first[128] = incl;
+        if (blockIdx.x == 0) schedule[0] = incl;
+      }
+    }
+    __syncthreads();
+    int ex[KT];
+#pragma unroll
+    for (int r = 0; r < KT; ++r) {
+      ex[r] = route_expert(id[r]);
+      if (ex[r] >= 0) atomicOr(&masks[ex[r]], 1ull << lane);
+    }
+    __syncthreads();
+    if (schedule != nullptr)
+      tile_entries(first, bm, (int)(blockIdx.x * 64 + threadIdx.x), (int)(gridDim.x * 64), schedule);
+    if (!live) return;
+    const unsigned long long below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int r = 0; r < KT; ++r) {
+      const int e = ex[r];
+      bool last = e >= 0;
+#pragma unroll
+      for (int q = r + 1; q < KT; ++q) last = last && ex[q] != e;
+      if (!last) continue;
+      const int rank = offs[e] + __popcll(masks[e] & below);
+      groups[(int64_t)e * (tokens + 1) + 1 + rank] = (float)(t * KT + r);
+      if (order) {
+        int less = 0;
+#pragma unroll
+        for (int q = 0; q < KT; ++q) less += id[q] < (float)e ? 1 : 0;
+        order[t * KT + less] = (float)r;
+      }
+    }
+    return;
+  }
   if (schedule != nullptr) {
     const int l = threadIdx.x;
     const int t0 = ((int)groups[(int64_t)(2 * l) * (tokens + 1)] + bm - 1) / bm;
@@ -278,32 +345,6 @@ __global__ __launch_bounds__(64) void group_scatter_kernel(const float* __restri
   const float* rt = routes + t * 2 * topk;
   const unsigned long long below = (1ull << lane) - 1ull;
   const int* offsets = block_offsets + (int64_t)blockIdx.x * 128;
-  if constexpr (KT > 0) {
-    float id[KT];
-    int ex[KT];
-#pragma unroll
-    for (int r = 0; r < KT; ++r) {
-      id[r] = rt[r];
-      ex[r] = route_expert(id[r]);
-    }
-#pragma unroll
-    for (int r = 0; r < KT; ++r) {
-      const int e = ex[r];
-      bool last = e >= 0;
-#pragma unroll
-      for (int q = r + 1; q < KT; ++q) last = last && ex[q] != e;
-      if (!last) continue;
-      const int rank = offsets[e] + __popcll(masks[e] & below);
-      groups[(int64_t)e * (tokens + 1) + 1 + rank] = (float)(t * KT + r);
-      if (order) {
-        int less = 0;
-#pragma unroll
-        for (int q = 0; q < KT; ++q) less += id[q] < (float)e ? 1 : 0;
-        order[t * KT + less] = (float)r;
-      }
-    }
-    return;
-  }
   for (int r = 0; r < topk; ++r) {
     const int e = route_expert(rt[r]);
     if (e < 0 || !last_slot(rt, topk, r, e)) continue;
