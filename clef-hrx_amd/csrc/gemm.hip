@@ -1442,6 +1442,12 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
   const int NW = (int)blockDim.x >> 6;
   __shared__ int red[NA][16][64];  // [gate / up][accumulator register][lane]
   __shared__ int routes_s[32];
+  // Without GU, the epilogue's scales are DMA'd by wave 0 under the k-steps
+  // (lanes 32..63 read past their resources and land zeros in the upper
+  // halves), so the epilogue makes no global round trip. (With GU the two
+  // more addresses spill a register: 7.5 -> 8.2 us at 8 routed rows.)
+  __shared__ __align__(16) float ws_s[64];  // column scales c0 .. c0 + 31
+  __shared__ float as_s[64];                // row scales of the 32 slots
   // The item's schedule entry is read together with the tile count (every
   // launched item indexes inside the schedule buffer), so the exit test
   // costs no extra round trip.
@@ -1486,11 +1492,16 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
   // so waiting for the route leaves the weight loads in flight).
   const int k0 = wave * kb / NW, k1 = (wave + 1) * kb / NW;  // k0 < k1: NW <= kb
   load_w(std::integral_constant<int, 0>{}, k0);
+  if (!GU && wave == 0)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(ws + nrow, 32 * 4), (lds_ptr_t)&ws_s[0], 4, lane * 4, 0, 0, 0);
   const int my_route = row0 + lr < count ? (int)route_f : -1;
   if (threadIdx.x < 32) routes_s[threadIdx.x] = my_route;
   const int64_t xr = input_routed ? (int64_t)my_route : (int64_t)my_route / topk;
   const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a, a_bytes);
   const int a_voff = my_route >= 0 ? (int)(xr * a_words * 4) + 64 * h : (int)0x80000000u;
+  if (!GU && wave == 0)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(as, 0x7fffffff), (lds_ptr_t)&as_s[0], 4,
+                                             my_route >= 0 && h == 0 ? (int)(xr * 4) : (int)0x80000000u, 0, 0, 0);
   auto load_a = [&](auto buf, int kt) {
     constexpr int B = decltype(buf)::value;
 #pragma unroll
@@ -1526,7 +1537,8 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
     compute(B1{});
     if (++kt >= k1) break;
   }
-  __syncthreads();  // reduction buffer zeroed, slot routes written
+  wait_vmcnt<0>();  // this wave's scale DMA has landed
+  __syncthreads();  // reduction buffer zeroed, slot routes and scales written
 #pragma unroll
   for (int s = 0; s < NA; ++s)
 #pragma unroll
@@ -1540,8 +1552,9 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
     const int route = routes_s[ln & 31];
     if (route >= 0) {
       const int col = c0 + 8 * rq + 4 * (ln >> 5);
-      const float asv = as[input_routed ? (int64_t)route : (int64_t)route / topk];
-      const float4 wg4 = *reinterpret_cast<const float4*>(ws + (int64_t)e * n + col);
+      const float asv = GU ? as[input_routed ? (int64_t)route : (int64_t)route / topk] : as_s[ln & 31];
+      const float4 wg4 = GU ? *reinterpret_cast<const float4*>(ws + (int64_t)e * n + col)
+                            : *reinterpret_cast<const float4*>(&ws_s[col - c0]);
       const float wg[4] = {wg4.x, wg4.y, wg4.z, wg4.w};
       float y[4];
 #pragma unroll
