@@ -15,9 +15,14 @@ hipError_t launch_prepare(const uint16_t* x, int64_t rows, int width, int stride
 // launch_prepare) in one launch; only for widths the grid-stride quantizer
 // takes (route_prepare_fusable).
 bool route_prepare_fusable(int width);
+// With `groups` non-NULL (route_group_fusable) the routing workgroup also
+// writes the grouping tables and tile schedule (tiles of `bm` slots), as
+// launch_group_routes would.
+bool route_group_fusable(int64_t tokens, int topk);
 hipError_t launch_route_prepare(const void* logits, int dtype, int64_t tokens, int experts, int topk,
                                 float* routes, const uint16_t* x, int width, int stride, uint32_t* out,
-                                hipStream_t stream);
+                                hipStream_t stream, float* groups = nullptr, float* order = nullptr,
+                                int32_t* schedule = nullptr, int bm = 0);
 hipError_t launch_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t rows, int width,
                                  int stride, int bits, uint32_t* out, hipStream_t stream);
 hipError_t launch_prepare_attention_gate(const uint16_t* x, const uint16_t* q_gate, int64_t rows, int width,

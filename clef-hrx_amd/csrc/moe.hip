@@ -12,6 +12,7 @@
 // kernels/omni_combine.loom:50-77).
 #include "common.hpp"
 #include "kernels.hpp"
+#include "group.hpp"
 #include "route.hpp"
 
 namespace clef {
@@ -38,12 +39,6 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
 // workgroup runs all three passes (group_single_kernel).
 
 constexpr int kGroupBlock = 64;
-
-// Expert id of route slot r, or -1 when the slot names no expert in 0..127
-// (the oracle compares (int32_t)id against each expert).
-__device__ __forceinline__ int route_expert(float id) {
-  return (id > -1.0f && id < 128.0f) ? (int)id : -1;
-}
 
 // True when slot r is the last slot of this token naming its expert.
 __device__ __forceinline__ bool last_slot(const float* rt, int topk, int r, int e) {
@@ -90,60 +85,6 @@ __global__ __launch_bounds__(64) void group_count_kernel(const float* __restrict
   int* dst = block_counts + (int64_t)blockIdx.x * 128;
   dst[lane] = __popcll(masks[lane]);
   dst[64 + lane] = __popcll(masks[64 + lane]);
-}
-
-// The expert GEMM's tile list from the experts' counts: tiles of bm slots,
-// schedule = [total] then (expert, first slot) per tile, experts ascending.
-//
-// tile_prefix: `holder` threads (one per expert e) pass e's count; every
-// thread of the workgroup calls it. The tile counts' exclusive prefix is one
-// wave's scan, two experts per lane, between two barriers; afterwards
-// first[e] is expert e's first tile and first[128] the total.
-__device__ void tile_prefix(int count, bool holder, int e, int bm, int* first /* [129] */) {
-  if (holder) first[e] = (count + bm - 1) / bm;
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const int l = threadIdx.x;
-    const int t0 = first[2 * l], t1 = first[2 * l + 1];
-    int incl = t0 + t1;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int o = __shfl_up(incl, off, 64);
-      if (l >= off) incl += o;
-    }
-    first[2 * l] = incl - t0 - t1;
-    first[2 * l + 1] = incl - t1;
-    if (l == 63) first[128] = incl;
-  }
-  __syncthreads();
-}
-
-// Schedule entries t = t0, t0 + stride, ... below first[128]: tile t's
-// expert is the last one whose first tile is at or below t (experts without
-// tiles share the next one's first tile and are passed over).
-__device__ __forceinline__ void tile_entries(const int* first, int bm, int t0, int stride,
-                                             int32_t* __restrict__ schedule) {
-  const int total = first[128];
-  for (int t = t0; t < total; t += stride) {
-    int lo = 0, hi = 127;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (first[mid] <= t)
-        lo = mid;
-      else
-        hi = mid - 1;
-    }
-    schedule[1 + 2 * t] = lo;
-    schedule[2 + 2 * t] = (t - first[lo]) * bm;
-  }
-}
-
-// The whole schedule from one workgroup (few tiles: up to 4096 tokens).
-__device__ void write_tile_schedule(int count, bool holder, int e, int bm, int* first /* [129] */,
-                                    int32_t* __restrict__ schedule) {
-  tile_prefix(count, holder, e, bm, first);
-  if (threadIdx.x == 0) schedule[0] = first[128];
-  tile_entries(first, bm, threadIdx.x, blockDim.x, schedule);
 }
 
 // One workgroup of 1024 threads: 8 threads per expert, each summing a

@@ -23,6 +23,7 @@
 #include "common.hpp"
 #include "silu_table.hpp"
 #include "kernels.hpp"
+#include "group.hpp"
 #include "route.hpp"
 
 namespace clef {
@@ -528,12 +529,22 @@ __global__ __launch_bounds__(256) void prepare_loop_kernel(Src src, int64_t rows
 // route_blocks workgroups route the tokens (16 or 4 per workgroup), the others run the
 // grid-stride quantizer. Neither needs the other's output, so they share the
 // GPU instead of running one after the other.
+// With `groups` non-NULL (at most 16 tokens at top-8: one routing
+// workgroup) that workgroup also groups the routes it wrote (group_small).
 __global__ __launch_bounds__(256) void route_prepare_kernel(const void* __restrict__ logits, int dtype,
                                                             int64_t tokens, int experts, int topk,
                                                             float* __restrict__ routes, int64_t route_blocks,
                                                             PlainSource src, int width, int out_words,
-                                                            uint32_t* __restrict__ out) {
+                                                            uint32_t* __restrict__ out, float* groups, float* order,
+                                                            int32_t* schedule, int bm) {
   if ((int64_t)blockIdx.x < route_blocks) {
+    if (groups != nullptr) {  // topk 8, one routing workgroup: route_body16
+      __shared__ int ids[128];
+      route_impl::route_body16(logits, dtype, tokens, experts, topk, routes, 0, ids);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // ids written; the route stores may drain
+      group_small(ids, (int)tokens, groups, order, schedule, bm);
+      return;
+    }
     route_impl::route_block(logits, dtype, tokens, experts, topk, routes, blockIdx.x);
     return;
   }
@@ -643,17 +654,21 @@ hipError_t launch_prepare(const uint16_t* x, int64_t rows, int width, int stride
 
 bool route_prepare_fusable(int width) { return width % 256 == 0 && width / 256 <= 16; }
 
+bool route_group_fusable(int64_t tokens, int topk) { return topk == 8 && tokens >= 1 && tokens <= 16; }
+
 hipError_t launch_route_prepare(const void* logits, int dtype, int64_t tokens, int experts, int topk,
                                 float* routes, const uint16_t* x, int width, int stride, uint32_t* out,
-                                hipStream_t stream) {
+                                hipStream_t stream, float* groups, float* order, int32_t* schedule, int bm) {
   if (!route_prepare_fusable(width)) return hipErrorInvalidValue;
+  if (groups != nullptr && !route_group_fusable(tokens, topk)) return hipErrorInvalidValue;
   const int per_block = 16 / (width / 256);
   const int64_t blocks = (tokens + per_block - 1) / per_block;
   const int64_t prep = blocks < 2048 ? blocks : 2048;
   const int per = route_impl::route_tokens_per_block(topk);
   const int64_t route_blocks = (tokens + per - 1) / per;
   route_prepare_kernel<<<(unsigned)(route_blocks + prep), 256, 0, stream>>>(
-      logits, dtype, tokens, experts, topk, routes, route_blocks, PlainSource{x}, width, stride / 8, out);
+      logits, dtype, tokens, experts, topk, routes, route_blocks, PlainSource{x}, width, stride / 8, out, groups, order,
+      schedule, bm);
   return hipGetLastError();
 }
 

@@ -140,8 +140,11 @@ constexpr int kRouteTokens16 = 16;
 // of the instructions per token of the one-wave-per-token body, whose
 // reductions span 64 lanes for two slots each. Rank r is kept by lane r of
 // the row; the softmax sum runs in rank order over the row's lanes.
+// With `ids` non-NULL the ranks' expert ids also go to LDS: ids[8 * (token in
+// the block) + rank] (topk <= 8).
 __device__ __forceinline__ void route_body16(const void* __restrict__ logits, int dtype, int64_t tokens,
-                                             int experts, int topk, float* __restrict__ routes, int64_t block) {
+                                             int experts, int topk, float* __restrict__ routes, int64_t block,
+                                             int* ids = nullptr) {
   const int lane = threadIdx.x & 63, li = lane & 15;
   const int64_t t = block * kRouteTokens16 + (threadIdx.x >> 4);
   const bool live = t < tokens;  // every lane stays on for the row reductions
@@ -211,6 +214,7 @@ __device__ __forceinline__ void route_body16(const void* __restrict__ logits, in
     float* out = routes + t * 2 * topk;
     out[li] = (float)rid;
     out[topk + li] = bf16_round(p / sum);
+    if (ids != nullptr) ids[8 * (threadIdx.x >> 4) + li] = rid;
   }
 }
 

@@ -707,7 +707,8 @@ def test_combine_matches_oracle(ordered, topk, width):
     assert_same_u16(bf16_host(got), want, "combine")
 
 
-@pytest.mark.parametrize("tokens,hidden,inter", [(5, 512, 256), (96, 2048, 768), (300, 1024, 512),
+@pytest.mark.parametrize("tokens,hidden,inter", [(1, 2048, 768), (5, 512, 256), (16, 512, 256), (17, 512, 256),
+                                                 (96, 2048, 768), (300, 1024, 512),
                                                  (256, 512, 256), (257, 512, 256), (4160, 512, 256)])
 def test_moe_layer_matches_oracle(tokens, hidden, inter):
     """Whole Omni INT4 MoE block (src/omni.rs:762-857) bit-exact vs the oracle.
