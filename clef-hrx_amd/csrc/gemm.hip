@@ -1125,6 +1125,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint32_t* __
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int J = RW / 8;
   static_assert(RW % 8 == 0 && 128 % RW == 0 && MR * RW <= NW * 64, "decode tile");
+  // Every argument into SGPRs at once: one scalar round trip, where the
+  // compiler would otherwise fetch each under the branch that first needs it.
+  asm volatile("" ::"s"(a), "s"(as), "s"(w), "s"(ws), "s"(residual), "s"(out), "s"(M), "s"(a_words), "s"(N), "s"(kb));
   __shared__ int red[NW][MR][RW];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1263,6 +1266,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_ksplit_kernel(const uint32_t* __
   constexpr int CHUNKS = BM * NT * 4;        // 8-column row chunks of the tile
   constexpr int IPT = (CHUNKS + NW * 64 - 1) / (NW * 64);
   static_assert(NB * STAGE >= MT * NT * 4096, "a wave's accumulators fit its stages");
+  // Every argument into SGPRs at once (one scalar round trip).
+  asm volatile("" ::"s"(a), "s"(as), "s"(w), "s"(ws), "s"(residual), "s"(out), "s"(M), "s"(a_words), "s"(N), "s"(kb));
   __shared__ __align__(16) char lds[NW * NB * STAGE];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
