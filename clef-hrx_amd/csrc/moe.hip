@@ -479,7 +479,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int j = 0; j < KT; ++j) {
       p[j] = rt[KT + rank[j]];
-      v[j] = *reinterpret_cast<const uint4*>(values + ((t * KT + rank[j]) * width + c));
+      typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(values + ((t * KT + rank[j]) * width + c)));
+      v[j] = make_uint4(q.x, q.y, q.z, q.w);
     }
 #pragma unroll
     for (int j = 0; j < KT; ++j) {
