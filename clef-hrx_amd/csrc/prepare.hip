@@ -41,8 +41,11 @@ struct PlainSource {
     u4 a, b;
   };
   __device__ __forceinline__ Raw fetch(int64_t rowoff, int col) const {
-    const u4* p = reinterpret_cast<const u4*>(x + rowoff + col);
-    return Raw{p[0], p[1]};
+    // each input value is read once: non-temporal loads
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4* p = reinterpret_cast<const u32x4*>(x + rowoff + col);
+    const u32x4 a = __builtin_nontemporal_load(p), b = __builtin_nontemporal_load(p + 1);
+    return Raw{u4{a.x, a.y, a.z, a.w}, u4{b.x, b.y, b.z, b.w}};
   }
   __device__ __forceinline__ void convert(const Raw& r, float* v) const {
     uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
