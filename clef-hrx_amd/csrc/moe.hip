@@ -313,14 +313,20 @@ __global__ __launch_bounds__(64) void group_scatter_kernel(const float* __restri
 constexpr int kGroupSingleTokens = 512;
 constexpr int kGroupSingleWaves = 16;
 constexpr int kGroupSingleBlocks = kGroupSingleTokens / kGroupBlock;  // 8
-constexpr int kGroupSinglePer = (kGroupSingleBlocks + kGroupSingleWaves - 1) / kGroupSingleWaves;  // per wave
+constexpr int kGroupCountScanBlocks = 16;                               // 1024 tokens
 
+// NB: blocks of 64 tokens it takes (8: up to 512 tokens, all three passes;
+// 16: up to 1024 tokens without the scatter, the blocks' prefixes written to
+// `block_offsets` for group_scatter_kernel<8>: one launch for count and scan).
+template <int NB, bool SCATTER>
 __global__ __launch_bounds__(1024) void group_single_kernel(const float* __restrict__ routes, int64_t tokens,
                                                             float* __restrict__ groups, float* __restrict__ order,
-                                                            int32_t* __restrict__ schedule, int bm) {
+                                                            int32_t* __restrict__ schedule, int bm,
+                                                            int* __restrict__ block_offsets) {
   constexpr int KT = 8;
+  constexpr int kGroupSinglePer = (NB + kGroupSingleWaves - 1) / kGroupSingleWaves;  // blocks per wave
   __shared__ unsigned long long masks[kGroupSingleWaves][128];
-  __shared__ int offs[kGroupSingleBlocks][128];
+  __shared__ int offs[NB][128];
   __shared__ int part[8][128];
   __shared__ int tiles_scan[129];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -377,8 +383,11 @@ __global__ __launch_bounds__(1024) void group_single_kernel(const float* __restr
       run += c;
     }
     if (j == 7) groups[(int64_t)e * (tokens + 1)] = (float)run;
+    if (!SCATTER)
+      for (int b = b0; b < b1; ++b) block_offsets[b * 128 + e] = offs[b][e];
     if (schedule != nullptr) write_tile_schedule(run, j == 7, e, bm, tiles_scan, schedule);
   }
+  if (!SCATTER) return;
   __syncthreads();
   // scatter
   const unsigned long long below = (1ull << lane) - 1ull;
@@ -615,11 +624,19 @@ hipError_t launch_group_routes(const float* routes, int64_t tokens, int topk, fl
                                float* order, void* workspace, hipStream_t stream, int32_t* schedule,
                                int schedule_bm) {
   if (topk == 8 && tokens <= kGroupSingleTokens) {
-    group_single_kernel<<<1, 1024, 0, stream>>>(routes, tokens, groups, order, schedule, schedule_bm);
+    group_single_kernel<kGroupSingleBlocks, true><<<1, 1024, 0, stream>>>(routes, tokens, groups, order, schedule,
+                                                                          schedule_bm, nullptr);
     return hipGetLastError();
   }
   const int64_t blocks = (tokens + kGroupBlock - 1) / kGroupBlock;
   int* counts = static_cast<int*>(workspace);
+  if (topk == 8 && blocks <= kGroupCountScanBlocks) {
+    group_single_kernel<kGroupCountScanBlocks, false><<<1, 1024, 0, stream>>>(routes, tokens, groups, order,
+                                                                              schedule, schedule_bm, counts);
+    group_scatter_kernel<8><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts, groups, order,
+                                                                 schedule_bm, nullptr);
+    return hipGetLastError();
+  }
   if (topk == 8)
     group_count_kernel<8><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts);
   else
