@@ -66,9 +66,6 @@ SIGNATURES = {
                                                   _P, _SZ, _P]),
     "clef_moe_expert_i4": (ctypes.c_int, [_P, _I32, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P,
                                           _P, _SZ, _P]),
-    "clef_moe_expert_f6": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _SZ, _P]),
-    "clef_moe_expert_gate_up_f6": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _P, _SZ,
-                                                  _P]),
     "clef_moe_expert_ungrouped_workspace_bytes": (_SZ, [_I64, _I32]),
     "clef_moe_expert_i4_ungrouped": (ctypes.c_int, [_P, _I32, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P,
                                                     _P, _SZ, _P]),
@@ -666,33 +663,6 @@ def omni_gate_up(a: Prepared, gate: QuantizedWeight, up: QuantizedWeight, groups
     _check(lib().clef_moe_expert_gate_up_i4(_ptr(a.storage), a.stride, _ptr(a.scales), _ptr(gate.codes),
                                             _ptr(gate.scales), _ptr(up.codes), _ptr(up.scales), _ptr(groups),
                                             tokens, topk, gate.cols, n, _ptr(h), _ptr(ws), ws_bytes, _stream()))
-    return h
-
-
-def omni_expert_f6(a: PreparedF6, w: F6Weight, groups: torch.Tensor, tokens: int, topk: int,
-                   input_routed: bool) -> torch.Tensor:
-    """omni_expert on the bf6 form of the codes (a from prepare_f6, w from
-    f6_weight of the tiled expert weight): bit-equal to omni_expert."""
-    n = w.rows // 128
-    out = torch.zeros((tokens * topk, n), dtype=torch.bfloat16, device=groups.device)
-    ws_bytes = int(lib().clef_moe_expert_workspace_bytes(tokens, topk))
-    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=groups.device)
-    _check(lib().clef_moe_expert_f6(_ptr(a.codes), _ptr(a.scales), _ptr(w.codes), _ptr(w.scales), _ptr(groups),
-                                    tokens, topk, w.cols, n, int(input_routed), _ptr(out), _ptr(ws), ws_bytes,
-                                    _stream()))
-    return out
-
-
-def omni_gate_up_f6(a: PreparedF6, gate: F6Weight, up: F6Weight, groups: torch.Tensor, tokens: int,
-                    topk: int) -> torch.Tensor:
-    """omni_gate_up on the bf6 form of the codes: bit-equal to omni_gate_up."""
-    n = gate.rows // 128
-    h = torch.zeros((tokens * topk, n), dtype=torch.bfloat16, device=groups.device)
-    ws_bytes = int(lib().clef_moe_expert_workspace_bytes(tokens, topk))
-    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=groups.device)
-    _check(lib().clef_moe_expert_gate_up_f6(_ptr(a.codes), _ptr(a.scales), _ptr(gate.codes), _ptr(gate.scales),
-                                            _ptr(up.codes), _ptr(up.scales), _ptr(groups), tokens, topk, gate.cols,
-                                            n, _ptr(h), _ptr(ws), ws_bytes, _stream()))
     return h
 
 

@@ -1766,12 +1766,6 @@ hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int topk,
   return hipGetLastError();
 }
 
-hipError_t launch_expert_schedule_bm(const float* groups, int64_t tokens, int bm, int32_t* schedule,
-                                     hipStream_t stream) {
-  tile_list_kernel<int32_t><<<1, 128, 0, stream>>>(groups, tokens, bm, schedule);
-  return hipGetLastError();
-}
-
 hipError_t launch_expert_tasks(const float* groups, int64_t tokens, float* tasks, hipStream_t stream) {
   tile_list_kernel<float><<<1, 128, 0, stream>>>(groups, tokens, 16, tasks);
   return hipGetLastError();

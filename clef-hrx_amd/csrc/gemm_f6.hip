@@ -525,4 +525,3 @@ hipError_t launch_gemm_f6(const uint8_t* a, const float* as, const uint8_t* w, c
 }  // namespace clef
 
 // The grouped expert GEMM on bf6 operands (uses the helpers above).
-#include "expert_f6.hpp"

@@ -47,15 +47,6 @@ hipError_t launch_f6_rows(const uint32_t* a, int a_words, int64_t rows, int k, u
 hipError_t launch_f6_tiled(const uint32_t* w_tiled, int64_t n, int k, uint8_t* out, hipStream_t stream);
 hipError_t launch_gemm_f6(const uint8_t* a, const float* as, const uint8_t* w, const float* ws, int64_t m, int n,
                           int k, const uint16_t* residual, uint16_t* out, hipStream_t stream);
-// Grouped expert GEMM on bf6 operands (expert_f6.hpp): `a` bf6 activation
-// rows of k * 3/4 bytes (routed: one per route, else one per token), `w` (and
-// `w2`, GU: gate and up) the 128 experts' bf6 tiled weights [128 * n][k], on a
-// schedule of 128-slot tiles. GU writes h = S1(E1(gate), E1(up)).
-bool expert_f6_supported(bool gu, int k, int n, int64_t a_bytes, int64_t routes);
-hipError_t launch_expert_f6(bool gu, const uint8_t* a, int a_row_bytes, int64_t a_bytes, const float* as,
-                            const uint8_t* w, const float* ws, const uint8_t* w2, const float* ws2,
-                            const float* groups, const int32_t* schedule, int64_t list_stride, int topk, int k, int n,
-                            int input_routed, uint16_t* out, hipStream_t stream);
 // Records msg as clef_last_error() of this thread; returns CLEF_EINVAL.
 int set_last_error(const char* msg);
 // G1 tile configurations (clef_i4_gemm_config): 128x128 tiles, 256x256
@@ -95,9 +86,6 @@ int64_t expert_max_tiles(int64_t routes);
 size_t expert_schedule_bytes(int64_t routes);
 hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int topk, int32_t* schedule,
                                   hipStream_t stream);
-// The same schedule with tiles of `bm` slots (the bf6 expert GEMM: 128).
-hipError_t launch_expert_schedule_bm(const float* groups, int64_t tokens, int bm, int32_t* schedule,
-                                     hipStream_t stream);
 // `list_stride` is the row pitch of `groups` in floats: tokens + 1 for the
 // reference's table (0 selects it), more for a table that lists every route
 // slot (ungrouped, duplicates included).

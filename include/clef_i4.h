@@ -216,8 +216,10 @@ int clef_i4_gemm_configs(void);
  *   Preconditions as clef_i4_prepare (width % 256 == 0, 256 <= width <=
  *   32768, 1 <= rows <= 2^20 -> "unsupported rotated integer operand").
  * - clef_i4_gemm_f6: G1 on them, with clef_i4_gemm's epilogue and residual.
- *   Preconditions: m >= 1, n % 256 == 0, k % 256 == 0, k >= 256 ->
- *   "unsupported integer projection shape"; 16-byte aligned pointers. */
+ *   Preconditions: m >= 1, n % 256 == 0, k % 256 == 0, 256 <= k <= 32768
+ *   (the quantizer's widest row; the f32 sums of the bf6 products are exact
+ *   integers there) -> "unsupported integer projection shape"; 16-byte
+ *   aligned pointers. */
 int clef_i4_f6_activation(const uint32_t* a, int32_t k_stride, int64_t rows, int32_t k, uint8_t* out,
                           clef_stream_t stream);
 int clef_i4_f6_weight(const uint32_t* w_tiled, int64_t n, int32_t k, uint8_t* out, clef_stream_t stream);
@@ -257,7 +259,8 @@ int clef_i4_project_f6(const uint16_t* x, int64_t m, int32_t k, const uint8_t* w
  * probabilities rounded to bf16. logits_dtype 0 = bf16, 1 = f32.
  * Replaces Engine::omni_route (src/omni.rs:170-190), kernels/omni_route.loom.
  * Preconditions: 0 < topk <= experts <= 128 -> "invalid expert router shape";
- * tokens >= 1. */
+ * 1 <= tokens <= 2^24; logits 16-byte aligned (rows are read as 16-byte
+ * pieces where their length allows) -> the alignment message. */
 int clef_moe_route(const void* logits, int32_t logits_dtype, int64_t tokens, int32_t experts,
                    int32_t topk, float* routes, clef_stream_t stream);
 
@@ -347,25 +350,6 @@ int clef_moe_expert_gate_up_i4(const uint32_t* a, int32_t stride, const float* a
                                int32_t k, int32_t n, uint16_t* h, void* workspace,
                                size_t workspace_bytes, clef_stream_t stream);
 
-/* E1 and the fused gate/up on the bf6 form of the codes (no counterpart in
- * the reference: a gfx950 re-encoding of the same INT4 codes). `a` holds bf6
- * activation rows (clef_i4_prepare_f6 / clef_i4_f6_activation, k*3/4 bytes
- * per row), the weights are clef_i4_f6_weight of the tiled expert weights
- * (e * n rows). Every code is exact in bf6 and the f32 sums of integer dots
- * are exact for k < 2^18, so out / h equal clef_moe_expert_i4 /
- * clef_moe_expert_gate_up_i4 on the same codes bit for bit. Workspace: as
- * clef_moe_expert_i4. Preconditions: those of clef_moe_expert_i4 /
- * clef_moe_expert_gate_up_i4 (with the messages named there) and k >= 512;
- * the bf6 activation operand under 2 GiB and routes * n * 2 bytes of output
- * at most 2 GiB -> the shape message of each entry. */
-int clef_moe_expert_f6(const uint8_t* a, const float* a_scales, const uint8_t* w_f6, const float* w_scales,
-                       const float* groups, int64_t tokens, int32_t topk, int32_t k, int32_t n, int32_t input_routed,
-                       uint16_t* out, void* workspace, size_t workspace_bytes, clef_stream_t stream);
-int clef_moe_expert_gate_up_f6(const uint8_t* a, const float* a_scales, const uint8_t* gate_f6, const float* gate_s,
-                               const uint8_t* up_f6, const float* up_s, const float* groups, int64_t tokens,
-                               int32_t topk, int32_t k, int32_t n, uint16_t* h, void* workspace,
-                               size_t workspace_bytes, clef_stream_t stream);
-
 /* h = bf16(bf16(g/(1+exp(-g))) * u) elementwise over n values. Replaces
  * Engine::swiglu (src/ops.rs:9-29) and kernels/swiglu.loom. Precondition:
  * n >= 0 -> "SwiGLU shape/dtype mismatch". */
@@ -393,7 +377,8 @@ size_t clef_moe_layer_workspace_bytes(int64_t tokens, int32_t hidden, int32_t in
  * MoE half of omni::forward_layers_cached (src/omni.rs:760-857) without the
  * bf16 router-gate projection (logits are an input) and without the residual
  * add. Preconditions: experts == 128 -> "Omni MoE requires 128 experts";
- * hidden, inter % 256 == 0; then those of the stages, including the 2 GiB
+ * hidden, inter % 256 == 0; then those of the stages (logits 16-byte
+ * aligned, as clef_moe_route), including the 2 GiB
  * bound on the packed x (tokens rows) and packed h (tokens * topk rows): the
  * reference runs at most 2048 tokens per call (src/omni.rs:11), and callers
  * with more tokens than the bound allows split them into chunks. */

@@ -330,3 +330,30 @@ def test_moe_layer_static_rejects_beyond_scratch():
     rc, msg = call("clef_moe_layer_static", FAKE, FAKE, 0, 16, 2048, 768, 64, 8, FAKE, FAKE, FAKE, FAKE, FAKE,
                    FAKE, None, FAKE, None)
     assert rc == -1 and msg == "Omni MoE requires 128 experts"
+
+
+@pytest.mark.parametrize("k,ok", [(32768, True), (33024, False), (65536, False)])
+def test_gemm_f6_bounds_k_to_quantizer_width(k, ok):
+    """The bf6 GEMM's f32 sums equal the integer dots only while they stay
+    exact; k is capped at 32768, the widest row the quantizer packs. A shape
+    that passes reaches the alignment check (the fake pointer + 8 is not
+    16-byte aligned), one that fails stops at the shape check."""
+    rc, msg = call("clef_i4_gemm_f6", FAKE + 8, FAKE, FAKE, FAKE, 256, 256, k, None, FAKE, None)
+    assert rc == -1
+    assert msg == ("device pointer is NULL or not 16-byte aligned" if ok else "unsupported integer projection shape")
+
+
+@pytest.mark.parametrize("offset", [2, 4, 8])
+def test_router_rejects_logits_not_16_byte_aligned(offset):
+    """The router reads each token's logits as 16-byte pieces where the row
+    length allows, so the logits must start on a 16-byte boundary, in
+    clef_moe_route and in the MoE layer that runs it."""
+    align = "device pointer is NULL or not 16-byte aligned"
+    rc, msg = call("clef_moe_route", FAKE + offset, 0, 4, 128, 8, FAKE, None)
+    assert rc == -1 and msg == align
+    rc, msg = call("clef_moe_layer", FAKE, FAKE + offset, 0, 16, 2048, 768, 128, 8, FAKE, FAKE, FAKE, FAKE, FAKE,
+                   FAKE, None, FAKE, FAKE, 1 << 40, None)
+    assert rc == -1 and msg == align
+    rc, msg = call("clef_moe_layer_static", FAKE, FAKE + offset, 0, 16, 2048, 768, 128, 8, FAKE, FAKE, FAKE, FAKE,
+                   FAKE, FAKE, None, FAKE, None)
+    assert rc == -1 and msg == align

@@ -198,6 +198,85 @@ def test_gemm_acc_brute_force():
     assert np.array_equal(acc.astype(np.int64), a_vals @ w_vals.T)
 
 
+def random_codes8(rng, rows, width, stride):
+    """INT8 codes in [-127, 127], four per word (byte p of word q = column 4q + p)."""
+    vals = rng.integers(-127, 128, size=(rows, width))
+    words = np.zeros((rows, stride // 4), dtype=np.uint32)
+    byt = (vals & 0xFF).astype(np.uint32).reshape(rows, width // 4, 4)
+    words[:, : width // 4] = np.bitwise_or.reduce(byt << (np.arange(4, dtype=np.uint32) * 8), axis=2)
+    return vals, words
+
+
+def untile(tiled: np.ndarray, rows: int, words: int) -> np.ndarray:
+    """Inverse of the retile block formula (src/quantized.rs:1394-1397) for
+    `words` logical words per row, whatever the codes per word."""
+    n = np.arange(rows)[:, None]
+    q = np.arange(words)[None, :]
+    idx = ((n // 128) * (words // 32) + q // 32) * 4096 + (n % 128) * 32 + q % 32
+    return tiled[idx]
+
+
+def test_retile_block_formula_bits8():
+    """The same block formula with four codes per word: K = 512 gives 128
+    words per row, four 32-word blocks."""
+    rows, cols = 256, 512
+    words = cols // 4
+    codes = (np.arange(rows)[:, None] * 100000 + np.arange(words + 16)[None, :]).astype(np.uint32)
+    tiled = oracle.retile(codes, cols, bits=8)
+    assert tiled.shape == (rows * words,)
+    assert np.array_equal(untile(tiled, rows, words), codes[:, :words])
+
+
+@pytest.mark.parametrize("m,n,k", [(37, 256, 768), (5, 128, 256)])
+def test_gemm_acc_brute_force_bits8(m, n, k):
+    """G1 accumulators at bits 8 (h3_gemm_i8_256, kernels/gemm_integer.loom:454-485):
+    exact i32 sums of int8 products, the weight read back through the tiled
+    layout. Codes of +-127 in every slot bound |acc| by 127^2 * k."""
+    rng = np.random.default_rng(11)
+    a_vals, a_words = random_codes8(rng, m, k, k + 64)
+    w_vals, w_words = random_codes8(rng, n, k, k)
+    a_vals[0, :] = 127
+    w_vals[0, :] = -127
+    a_words[0, : k // 4] = np.uint32(0x7F7F7F7F)
+    w_words[0, : k // 4] = np.uint32(0x81818181)
+    tiled = oracle.retile(w_words, k, bits=8)
+    acc = oracle.gemm_acc(a_words, tiled, n, k, bits=8)
+    assert np.array_equal(acc.astype(np.int64), a_vals @ w_vals.T)
+    assert acc[0, 0] == -127 * 127 * k
+
+
+def test_pack_weight_bits8_is_quantizer_then_block_formula():
+    """Q2 at bits 8 (Engine::load_quantized_weight, src/quantized.rs:147-234):
+    each row's codes, read back through the block formula, are the reference
+    test quantizer's (src/quantized.rs:1092-1113) of that row, and the scales
+    are its scales."""
+    rows, cols = 256, 1024
+    w = BF(np.array([[((i * 37 + 11 * r) % 257 - 128) / 91.0 for i in range(cols)] for r in range(rows)],
+                    dtype=np.float32))
+    tiled, scales = oracle.pack_weight(w, bits=8)
+    words = untile(tiled, rows, cols // 4)
+    got = decode_codes(words, cols, 8)
+    for r in range(rows):
+        want_codes, want_scale = reference_test_quantize(F(w[r]), 8)
+        assert np.array_equal(got[r], want_codes), r
+        assert np.float32(scales[r]) == np.float32(want_scale), r
+
+
+def test_gemm_epilogue_power_of_two_scales_bits8():
+    """The G1 epilogue on bits-8 accumulators: with power-of-two scales every
+    step before the bf16 rounding is exact."""
+    rng = np.random.default_rng(12)
+    m, n, k = 16, 128, 512
+    a_vals, a_words = random_codes8(rng, m, k, k + 64)
+    w_vals, w_words = random_codes8(rng, n, k, k)
+    tiled = oracle.retile(w_words, k, bits=8)
+    a_s = (2.0 ** rng.integers(-12, 0, size=m)).astype(np.float32)
+    w_s = (2.0 ** rng.integers(-12, 0, size=n)).astype(np.float32)
+    out = oracle.gemm(a_words, a_s, tiled, w_s, n, k, bits=8)
+    exact = (a_vals @ w_vals.T).astype(np.float64) * w_s[None, :].astype(np.float64) * a_s[:, None]
+    assert np.array_equal(out, BF(exact.astype(np.float32)))
+
+
 def test_gemm_epilogue_power_of_two_scales():
     rng = np.random.default_rng(4)
     m, n, k = 16, 128, 256
