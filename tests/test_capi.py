@@ -357,3 +357,13 @@ def test_router_rejects_logits_not_16_byte_aligned(offset):
     rc, msg = call("clef_moe_layer_static", FAKE, FAKE + offset, 0, 16, 2048, 768, 128, 8, FAKE, FAKE, FAKE, FAKE,
                    FAKE, FAKE, None, FAKE, None)
     assert rc == -1 and msg == align
+
+
+def test_static_layer_rejects_700_tokens():
+    """Just past the static scratch: 700 tokens at the Omni shape need more
+    than its 32 MiB, and the entry point says so before touching the device."""
+    need = clef_i4.lib().clef_moe_layer_workspace_bytes(700, 2048, 768, 8)
+    assert need > 32 << 20
+    rc, msg = call("clef_moe_layer_static", FAKE, FAKE, 0, 700, 2048, 768, 128, 8, FAKE, FAKE, FAKE, FAKE, FAKE,
+                   FAKE, None, FAKE, None)
+    assert rc == -1 and msg.startswith(f"MoE layer needs {need} bytes of scratch")

@@ -93,6 +93,10 @@ def test_headline_gemm_full_shape():
     for cfg in range(clef_i4.gemm_configs()):
         other = clef_i4.project_prepared(a, qw, config=cfg)
         assert torch.equal(other.view(torch.int16), out.view(torch.int16)), f"config {cfg}"
+    # the bf6 form of the same codes (the benchmark kernel: 48 column tiles,
+    # several tiles per workgroup), whole output bit for bit
+    f6 = clef_i4.project_f6(clef_i4.prepare_f6(x), clef_i4.f6_weight(qw))
+    assert torch.equal(f6.view(torch.int16), out.view(torch.int16)), "bf6 GEMM 4096x4096x12288"
 
 
 @pytest.mark.parametrize("n", [4096, 1024])
@@ -110,6 +114,8 @@ def test_attention_projection_full_shape(n):
     codes, scales, _ = oracle.prepare(u16(x[idx]), a.stride)
     want = oracle.gemm(codes, scales, *host_weight(qw), n, k, residual=u16(res[idx]))
     assert_rows(u16(out[idx]), want, rows, f"projection 16384x4096x{n} + residual")
+    f6 = clef_i4.project_f6(clef_i4.prepare_f6(x), clef_i4.f6_weight(qw), residual=res)
+    assert torch.equal(f6.view(torch.int16), out.view(torch.int16)), f"bf6 projection 16384x4096x{n} + residual"
 
 
 def test_dense_mlp_full_shape():
@@ -135,6 +141,15 @@ def test_dense_mlp_full_shape():
     h_codes, h_scales, _ = oracle.prepare_swiglu(g_want, u_want, h.stride)
     y_want = oracle.gemm(h_codes, h_scales, *host_weight(wd), d, f)
     assert_rows(u16(y[idx]), y_want, rows, "mlp down")
+    # the same block on the bf6 form of the codes (as the benchmark runs it),
+    # every stage's whole output bit for bit
+    af = clef_i4.prepare_f6(x)
+    g6 = clef_i4.project_f6(af, clef_i4.f6_weight(wg))
+    u6 = clef_i4.project_f6(af, clef_i4.f6_weight(wu))
+    assert torch.equal(g6.view(torch.int16), gate.view(torch.int16)), "bf6 mlp gate"
+    assert torch.equal(u6.view(torch.int16), up.view(torch.int16)), "bf6 mlp up"
+    y6 = clef_i4.project_f6(clef_i4.prepare_swiglu_f6(g6, u6), clef_i4.f6_weight(wd))
+    assert torch.equal(y6.view(torch.int16), y.view(torch.int16)), "bf6 mlp down"
 
 
 def skewed_logits(tokens: int, seed: int) -> torch.Tensor:

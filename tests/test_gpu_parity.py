@@ -482,6 +482,23 @@ def test_group_routes_matches_oracle(tokens):
     assert np.array_equal(tasks[: 1 + 2 * total], want_t[: 1 + 2 * total]), "tasks"
 
 
+@pytest.mark.parametrize("tokens,topk", [(1, 1), (17, 4), (300, 6), (513, 2), (4100, 4), (2000, 16), (700, 24)])
+def test_group_routes_other_topk(tokens, topk):
+    """Grouping at topk other than 8 (the generic count and scatter kernels:
+    the one-workgroup and register paths take top-8 only): lists, counts and
+    the ascending-expert order of each token's topk ranks."""
+    rng = np.random.default_rng(tokens * 3 + topk)
+    routes = random_routes(rng, tokens, topk=topk, skew=1.0 if tokens > 100 else 0.0)
+    want_g, want_o = oracle.group_routes(routes, topk=topk)
+    g, o = clef_i4.omni_group_routes(to_dev_f32(routes))
+    g = g.cpu().numpy()
+    for e in range(128):
+        c = int(want_g[e, 0])
+        assert g[e, 0] == want_g[e, 0], f"count e={e}"
+        assert np.array_equal(g[e, 1:1 + c], want_g[e, 1:1 + c]), f"list e={e}"
+    assert np.array_equal(o.cpu().numpy(), want_o), "order"
+
+
 def test_group_routes_empty_and_full_experts():
     """Empty experts and one expert taking every token (src/omni.rs:920-938)."""
     tokens = 600
@@ -730,6 +747,31 @@ def test_moe_layer_matches_oracle(tokens, hidden, inter):
     assert_same_u16(bf16_host(got), want, f"moe layer tokens={tokens}")
     again = layer(to_dev_bf16(x), to_dev_bf16(logits))
     assert_same_u16(bf16_host(again), want, "moe layer replay")
+
+
+@pytest.mark.parametrize("tokens,hidden,inter,topk", [
+    (12, 512, 256, 4), (300, 512, 256, 6), (700, 512, 256, 2), (40, 512, 256, 16), (20, 512, 256, 24),
+    (64, 5120, 256, 8), (300, 4352, 256, 8), (9, 6144, 256, 4)])
+def test_moe_layer_other_topk_and_wide_hidden(tokens, hidden, inter, topk):
+    """The MoE block off the Omni shape, bit-exact against the oracle.
+    topk other than 8 runs the generic grouping and combine kernels (the
+    routing workgroup groups only top-8 routes); topk above 16 takes the
+    wave-per-token router. hidden above 4096 (16 groups of 256) runs the
+    router, the grouping and the quantizer of x as three launches instead of
+    the router beside the quantizer."""
+    rng = np.random.default_rng(tokens * 31 + hidden + topk)
+    x = randn_bf16(rng, (tokens, hidden))
+    logits = BF(rng.standard_normal((tokens, 128)).astype(np.float32))
+    gate = packed_experts(rng, inter, hidden)
+    up = packed_experts(rng, inter, hidden)
+    down = packed_experts(rng, hidden, inter)
+    want, want_routes = oracle.moe_layer(x, logits, gate, up, down, topk=topk)
+    layer = clef_i4.MoeLayer(dev_weight(*gate, 128 * inter, hidden), dev_weight(*up, 128 * inter, hidden),
+                             dev_weight(*down, 128 * hidden, inter), topk=topk)
+    routes = torch.empty((tokens, 2 * topk), dtype=torch.float32, device=DEV)
+    got = layer(to_dev_bf16(x), to_dev_bf16(logits), routes_out=routes)
+    assert np.array_equal(routes.cpu().numpy().view(np.uint32), want_routes.view(np.uint32)), "routes"
+    assert_same_u16(bf16_host(got), want, f"moe layer tokens={tokens} hidden={hidden} topk={topk}")
 
 
 def test_moe_layer_closed_form():
