@@ -22,9 +22,13 @@
 //    an item starts on data already in LDS;
 //  * items are (schedule tile, column block) pairs in expert-major order,
 //    split into 8 contiguous per-XCD ranges (workgroup b runs on XCD b % 8);
-//    the k-th workgroup of an XCD takes items k, k + W, k + 2W, ... of its
-//    range (W workgroups per XCD), so the column blocks of one tile run side
-//    by side and share its activation rows in the XCD's L2;
+//    the k-th workgroup of an XCD starts with item k of its range and then
+//    claims the next unclaimed item from the XCD's counter, so the column
+//    blocks of one tile run side by side and share its activation rows in the
+//    XCD's L2. Claiming balances the two workgroups of a CU: the one
+//    dispatched first wins instruction issue by age and runs its items about
+//    twice as fast as the other while both compute, so equal static shares
+//    left every CU with a tail of the slower workgroup running alone;
 //  * the epilogue (E1, for GU then S1 with the SiLU table in LDS) goes out
 //    in blocks of 32 output columns: each wave stages its 64 rows of a block
 //    in the stage the item's last half-step read (free until the next item
@@ -55,7 +59,7 @@ namespace clef {
 template <bool GU, int NW_>
 struct ExpertPersist {
   static constexpr int NW = NW_;
-  using T = DmaHTile<64, 128, 2, NW / 2, kSchedFree, GU>;
+  using T = DmaHTile<64, 128, 2, NW / 2, kSchedPin, GU>;
   static_assert((NW == 4 || NW == 8) && T::BM == 128, "128-slot items on 4 or 8 waves");
   static constexpr int COLS = GU ? T::BN / 2 : T::BN;  // output columns per item
   static constexpr int STAGE = T::STAGE_BYTES;
@@ -73,12 +77,13 @@ struct ExpertPersist {
   static constexpr int LUT_OFF = NST * STAGE;
   static constexpr int LUT_BYTES = GU ? kSiluLutSize * 2 : 0;
   static constexpr int META_OFF = LUT_OFF + LUT_BYTES;
-  static constexpr int LDS = META_OFF + 2 * META;
+  static constexpr int CLAIM_OFF = META_OFF + 2 * META;  // the next item's index (16 bytes)
+  static constexpr int LDS = CLAIM_OFF + 16;
   static_assert(LDS * PER_CU <= 160 * 1024, "workgroups per CU");
   static_assert(NW * T::WM * 64 <= STAGE, "epilogue staging: 4 KiB per wave in one stage");
   static constexpr int THREADS = T::THREADS;
-  // Half-steps the pipeline needs: the next item is fetched during half-steps
-  // 0..3 (K >= 512).
+  // Half-steps the pipeline needs: the next item is claimed and fetched
+  // during half-steps 0..3 (K >= 512).
   static constexpr int MIN_HALF_STEPS = 4;
 };
 
@@ -104,7 +109,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
     const uint32_t* __restrict__ w, const float* __restrict__ ws, const uint32_t* __restrict__ w2,
     const float* __restrict__ ws2, const float* __restrict__ groups, const int32_t* __restrict__ schedule,
     int64_t list_stride, int topk, int kb, int n, int input_routed,
-    uint16_t* __restrict__ out, int tiles_n) {
+    uint16_t* __restrict__ out, int tiles_n, int32_t* __restrict__ claims) {
 #if defined(__HIP_DEVICE_COMPILE__)
   using P = ExpertPersist<GU, NW>;
   using T = typename P::T;
@@ -131,22 +136,30 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
 
   // ---- fetch steps of an item; each is issued before a half-step's stage
   // DMA and its results are used one half-step later.
-  // Step 0: the workgroup's next item in its XCD's range (static round
-  // robin: the k-th item of workgroup b is b / 8 + k * gridDim / 8).
-  const int64_t per_xcd = gridDim.x / 8;
-  int64_t claim_next = blockIdx.x / 8;
-  auto claim = [&]() -> int {
-    const int v = (int)claim_next;
-    claim_next += per_xcd;
-    return v;
+  // Step 0: the workgroup's next item in its XCD's range. Workgroup b starts
+  // with item b / 8; later items come from the XCD's counter (zeroed with the
+  // schedule), offset by the W = gridDim / 8 items handed out at the start.
+  // Lane 0 of wave 0 issues the atomic during half-step 0 (a vector atomic,
+  // covered by that half-step's vmcnt wait like the stage DMA issued after
+  // it) and publishes the index in LDS before the half-step's barrier; every
+  // wave reads it at half-step 1.
+  const int per_xcd = gridDim.x / 8;
+  int* claim_slot = reinterpret_cast<int*>(lds + P::CLAIM_OFF);
+  int claimed = 0;
+  auto claim_issue = [&]() {
+    if (threadIdx.x == 0)
+      claimed = per_xcd + __hip_atomic_fetch_add(claims + xcd, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  auto claim_publish = [&]() {
+    if (threadIdx.x == 0) *claim_slot = claimed;
   };
   // Step 1: the schedule entry of item `local`.
   auto fetch_entry = [&](int local, int& e_v, int& r_v, int& n0) {
     const int64_t it = first + local;
     const int tile = (int)(it / tiles_n);
     n0 = (int)(it - (int64_t)tile * tiles_n) * P::COLS;
-    e_v = __builtin_amdgcn_raw_buffer_load_b32(sched_rsrc, 0, (1 + 2 * tile) * 4, 0);
-    r_v = __builtin_amdgcn_raw_buffer_load_b32(sched_rsrc, 0, (2 + 2 * tile) * 4, 0);
+    e_v = __builtin_amdgcn_raw_buffer_load_b32(sched_rsrc, 0, (kSchedEntries + 2 * tile) * 4, 0);
+    r_v = __builtin_amdgcn_raw_buffer_load_b32(sched_rsrc, 0, (kSchedEntries + 1 + 2 * tile) * 4, 0);
   };
   // Step 2: the expert's count (vector load), its route list from slot row0
   // (waves 0, 1: 64 routes each, 4 bytes per lane, zero past the list's
@@ -212,7 +225,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
   char* st[3] = {lds, lds + P::STAGE, lds + (P::NST - 1) * P::STAGE};
   __amdgpu_buffer_rsrc_t b_cur, b_cur2;
   {
-    const int local = claim();
+    const int local = blockIdx.x / 8;
     if (local >= mine) return;  // uniform: no item for this workgroup, nothing in flight
     int e_v, r_v;
     fetch_entry(local, e_v, r_v, cur.n0);
@@ -267,8 +280,9 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
     auto main_loop = [&](char* __restrict__ r0, char* __restrict__ r1, char* __restrict__ r2,
                          char* __restrict__ mn) {
       auto half_step = [&](const char* rd, char* dma, int j) {
+        if (j == 0) claim_issue();
         if (j == 1) {
-          const int local = claim();
+          const int local = __builtin_amdgcn_readfirstlane(*claim_slot);
           nxt.valid = local < mine;
           if (nxt.valid) fetch_entry(local, e_v, r_v, nxt.n0);
         }
@@ -300,6 +314,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
           wait_vmcnt<(P::DIST - 1) * P::INST>();
         else
           wait_vmcnt<0>();
+        if (j == 0) claim_publish();
         lds_barrier();
       };
       if constexpr (P::NST == 3) {

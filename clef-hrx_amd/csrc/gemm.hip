@@ -618,14 +618,16 @@ using Dma256x256W8Pin = DmaTile<128, 64, 2, 4, kSchedPin>;
 
 constexpr int kExpertBM = 128;
 
-// Per-expert tile list: schedule[0] = tiles, then (expert, first slot) pairs
-// for experts ascending and tiles of kExpertBM slots each. With bm = 16 and
-// float output the same walk is the reference task list R3
-// (kernels/omni_expert_tasks.loom:30-62).
-template <class OutT>
+// Per-expert tile list: list[0] = tiles, then from list[HEAD] (expert, first
+// slot) pairs for experts ascending and tiles of bm slots each. The expert
+// GEMM schedule (int32, HEAD = kSchedEntries) also gets its work counters
+// zeroed. With bm = 16, float output and HEAD = 1 the same walk is the
+// reference task list R3 (kernels/omni_expert_tasks.loom:30-62).
+template <class OutT, int HEAD>
 __global__ __launch_bounds__(128) void tile_list_kernel(const float* __restrict__ groups,
                                                         int64_t tokens, int bm, OutT* __restrict__ list) {
   __shared__ int scan[128];
+  if (HEAD > 1 && threadIdx.x < HEAD - 1) list[1 + threadIdx.x] = (OutT)0;
   const int e = threadIdx.x;
   const int count = (int)groups[(int64_t)e * (tokens + 1)];
   const int tiles = (count + bm - 1) / bm;
@@ -652,8 +654,8 @@ __global__ __launch_bounds__(128) void tile_list_kernel(const float* __restrict_
         lo = mid + 1;
     }
     const int first = lo > 0 ? scan[lo - 1] : 0;
-    list[1 + 2 * t] = (OutT)lo;
-    list[2 + 2 * t] = (OutT)((t - first) * bm);
+    list[HEAD + 2 * t] = (OutT)lo;
+    list[HEAD + 1 + 2 * t] = (OutT)((t - first) * bm);
   }
   if (e == 127) list[0] = (OutT)total;
 }
@@ -705,8 +707,8 @@ __global__ __launch_bounds__(T::THREADS, 2) void expert_dmah_kernel(
   if (item >= items) return;
   const int tile = (int)(item / tiles_n);
   const int tn = (int)(item - (int64_t)tile * tiles_n);
-  const int e = schedule[1 + 2 * tile];
-  const int row0 = schedule[2 + 2 * tile];
+  const int e = schedule[kSchedEntries + 2 * tile];
+  const int row0 = schedule[kSchedEntries + 1 + 2 * tile];
   const float* list = groups + (int64_t)e * list_stride;
   const int count = (int)list[0];
   constexpr int COLS = GU ? T::BN / 2 : T::BN;  // output columns per tile
@@ -1460,8 +1462,8 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
   const int tile = (int)(item / slices);
   const int c0 = (int)(item - (int64_t)tile * slices) * 32;  // first output column within the expert
   const int tiles = schedule[0];
-  const int e = schedule[1 + 2 * tile];
-  const int row0 = schedule[2 + 2 * tile];
+  const int e = schedule[kSchedEntries + 2 * tile];
+  const int row0 = schedule[kSchedEntries + 1 + 2 * tile];
   if (item >= (int64_t)tiles * slices || e < 0) return;  // e >= 0 in every listed tile
   const float* list = groups + (int64_t)e * list_stride;
   const int lane = threadIdx.x & 63;
@@ -1721,9 +1723,12 @@ hipError_t launch_expert_persist(const uint32_t* a, int a_words, int64_t a_bytes
   if (hipError_t e = current_device(dev)) return e;
   if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) return e;
   const int grid = cus * P::PER_CU >= 8 ? cus * P::PER_CU / 8 * 8 : 8;
+  // Work counters: the schedule's first eight for the fused gate/up kernel,
+  // the second eight for the other (each used by one launch per schedule).
+  int32_t* claims = const_cast<int32_t*>(schedule) + kSchedClaims + (GU ? 0 : 8);
   expert_persist_kernel<GU, NW><<<(unsigned)grid, P::THREADS, P::LDS, stream>>>(
       a, a_words, (uint32_t)a_bytes, as, w, ws, w2, ws2, groups, schedule, list_stride, topk, k / 256, n,
-      input_routed, out, n / P::COLS);
+      input_routed, out, n / P::COLS, claims);
   return hipGetLastError();
 }
 
@@ -1757,17 +1762,18 @@ hipError_t launch_expert_gate_up(const uint32_t* a, int a_words, const float* as
 }
 
 size_t expert_schedule_bytes(int64_t routes) {
-  return (size_t)(1 + 2 * expert_max_tiles(routes)) * sizeof(int32_t);
+  return (size_t)(kSchedEntries + 2 * expert_max_tiles(routes)) * sizeof(int32_t);
 }
 
 hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int topk, int32_t* schedule,
                                   hipStream_t stream) {
-  tile_list_kernel<int32_t><<<1, 128, 0, stream>>>(groups, tokens, expert_tile_rows(tokens * topk), schedule);
+  tile_list_kernel<int32_t, kSchedEntries><<<1, 128, 0, stream>>>(groups, tokens, expert_tile_rows(tokens * topk),
+                                                                  schedule);
   return hipGetLastError();
 }
 
 hipError_t launch_expert_tasks(const float* groups, int64_t tokens, float* tasks, hipStream_t stream) {
-  tile_list_kernel<float><<<1, 128, 0, stream>>>(groups, tokens, 16, tasks);
+  tile_list_kernel<float, 1><<<1, 128, 0, stream>>>(groups, tokens, 16, tasks);
   return hipGetLastError();
 }
 

@@ -7,6 +7,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "kernels.hpp"
 
 namespace clef {
 
@@ -57,8 +58,8 @@ __device__ __forceinline__ void tile_entries(const int* first, int bm, int t0, i
       else
         hi = mid - 1;
     }
-    schedule[1 + 2 * t] = lo;
-    schedule[2 + 2 * t] = (t - first[lo]) * bm;
+    schedule[kSchedEntries + 2 * t] = lo;
+    schedule[kSchedEntries + 1 + 2 * t] = (t - first[lo]) * bm;
   }
 }
 
@@ -67,6 +68,7 @@ __device__ inline void write_tile_schedule(int count, bool holder, int e, int bm
                                     int32_t* __restrict__ schedule) {
   tile_prefix(count, holder, e, bm, first);
   if (threadIdx.x == 0) schedule[0] = first[128];
+  if (threadIdx.x < kSchedEntries - kSchedClaims) schedule[kSchedClaims + threadIdx.x] = 0;
   tile_entries(first, bm, threadIdx.x, blockDim.x, schedule);
 }
 

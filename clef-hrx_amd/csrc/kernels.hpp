@@ -76,11 +76,17 @@ hipError_t launch_group_routes(const float* routes, int64_t tokens, int topk, fl
 hipError_t launch_expert_tasks(const float* groups, int64_t tokens, float* tasks,
                                hipStream_t stream);
 
-// Tile schedule of the grouped expert GEMM: int32 [1 + 2 * max_tiles], tiles
-// of expert_tile_rows(routes) slots for `routes` routed rows (tokens * topk):
-// 32-slot tiles for few routed rows, 128-slot tiles otherwise. The expert
-// GEMM launches pick their kernel by the same rule, so a schedule must be
-// built for the routes count the GEMMs are launched with.
+// Tile schedule of the grouped expert GEMM: int32 [kSchedEntries + 2 *
+// max_tiles], tiles of expert_tile_rows(routes) slots for `routes` routed rows
+// (tokens * topk): 32-slot tiles for few routed rows, 128-slot tiles
+// otherwise. The expert GEMM launches pick their kernel by the same rule, so a
+// schedule must be built for the routes count the GEMMs are launched with.
+// Layout: [0] the tile count; [kSchedClaims, +16) the work counters of the
+// persistent expert kernels (eight per launch, one per XCD: the fused gate/up
+// kernel uses the first eight, the other the second eight), zeroed by every
+// writer of [0]; tile t's expert and first slot at [kSchedEntries + 2t] and
+// [kSchedEntries + 2t + 1].
+constexpr int kSchedClaims = 1, kSchedEntries = 17;
 int expert_tile_rows(int64_t routes);
 int64_t expert_max_tiles(int64_t routes);
 size_t expert_schedule_bytes(int64_t routes);

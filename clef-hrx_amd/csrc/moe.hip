@@ -229,6 +229,7 @@ __global__ __launch_bounds__(64) void group_scatter_kernel(const float* __restri
         first[128] = incl;
         if (blockIdx.x == 0) schedule[0] = incl;
       }
+      if (blockIdx.x == 0 && lane < kSchedEntries - kSchedClaims) schedule[kSchedClaims + lane] = 0;
     }
     __syncthreads();
     int ex[KT];
@@ -276,6 +277,7 @@ __global__ __launch_bounds__(64) void group_scatter_kernel(const float* __restri
       first[128] = incl;
       if (blockIdx.x == 0) schedule[0] = incl;
     }
+    if (blockIdx.x == 0 && l < kSchedEntries - kSchedClaims) schedule[kSchedClaims + l] = 0;
   }
   build_masks<KT>(routes, tokens, topk, masks);  // its barriers also order `first`
   if (schedule != nullptr)
