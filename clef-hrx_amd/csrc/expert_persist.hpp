@@ -384,11 +384,20 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
       // below 2^24, so the f32 list entries convert exactly to int.
       constexpr int RB = T::WM / 16;
       uint32_t dst[RB];
+      // All RB route reads go out together and are pinned in registers before
+      // the selects below (left to itself the compiler moves each read under
+      // its row's condition: one LDS round trip per row).
+      float route_f[RB];
+#pragma unroll
+      for (int s = 0; s < RB; ++s) {
+        route_f[s] = routes[wm * T::WM + 16 * s + (lane >> 2)];
+        pin_vgpr(route_f[s]);
+      }
 #pragma unroll
       for (int s = 0; s < RB; ++s) {
         const int r = wm * T::WM + 16 * s + (lane >> 2);
-        const int route = (int)routes[r];  // read unconditionally: no branch per row
-        dst[s] = cur.row0 + r < cur.count ? (uint32_t)(((int64_t)route * n + cur.n0) * 2) : 0x80000000u;
+        // route * n + n0 < 2^30 (the launcher bounds routes * n * 2 by 2^31)
+        dst[s] = cur.row0 + r < cur.count ? (uint32_t)(((int)route_f[s] * n + cur.n0) * 2) : 0x80000000u;
       }
       // f32(acc) is 256 * dot exactly. For GU, when every row and column
       // scale of the wave is at least 2^-59, RN(asr * 2^-8) * w is exact and
@@ -527,13 +536,23 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
             flush(wn * 64 + 32 * j);
           }
         } else {
+          // The column scales of block j + 1 are read while block j is
+          // converted and stored, so each block waits for LDS once (its
+          // staged rows) instead of once per scale read.
+          float4 w4[2][4];
+          auto load_scales = [&](int j, float4 (&dst4)[4]) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              dst4[q] = *reinterpret_cast<const float4*>(wsl + wn * T::WN + 32 * j + 8 * q + 4 * h);
+          };
+          load_scales(0, w4[0]);
 #pragma unroll
           for (int j = 0; j < T::TN; ++j) {
+            if (j + 1 < T::TN) load_scales(j + 1, w4[(j + 1) & 1]);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              const int col = wn * T::WN + 32 * j + 8 * q + 4 * h;
-              const float4 w4 = *reinterpret_cast<const float4*>(wsl + col);
-              const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+              const float4 c4 = w4[j & 1][q];
+              const float wv[4] = {c4.x, c4.y, c4.z, c4.w};
 #pragma unroll
               for (int i = 0; i < T::TM; ++i)
                 put(i, q, pack_bf16x2(scaled(i, j, 4 * q, wv[0]), scaled(i, j, 4 * q + 1, wv[1])),
