@@ -10,6 +10,10 @@ M=4096 on one MI355X.
                the fp6 MFMA; the output equals the INT4-operand GEMM's bit for
                bit (checked in the run), which is reported beside it
                (int4_operand_gemm).
+  rotating_weights  the same projection in both forms with the weight cycled
+               through copies that exceed the 256 MB last-level cache (INT4 14
+               x 25 MB, bf6 10 x 38 MB), each with its own output, so every
+               call streams its weight from HBM.
   moe_*        Omni INT4 MoE layer, 4096 tokens, hidden 2048, 128 experts,
                top-8, expert intermediate 768: route -> group -> expert GEMMs
                -> SwiGLU -> combine, timed over --steps layer calls.
@@ -27,6 +31,10 @@ M=4096 on one MI355X.
                on a prepared activation (bf6 form, checked against INT4).
   moe_skewed_t65536  the MoE layer at 65536 tokens with skewed routing (a few
                experts take most rows, eight none).
+  moe_small_t  the MoE layer at 1, 16 and 256 tokens: GPU time per layer by
+               graph replay (weights from HBM, and cache-resident), and the
+               HBM rate of the skinny expert GEMMs over the routed experts'
+               codes.
   roofline     the GEMM kernel against the peak of the MFMA it runs on (fp6
                dense, 10.1 POP/s); pct_int8_peak is the metric's own ratio.
   cpu_baseline the CPU oracle (quantize + i32 matmul + epilogue; MoE layer) on
@@ -72,11 +80,33 @@ def parse():
     p.add_argument("--moe-tokens", type=int, default=4096,
                    help="tokens of the MoE leg (4096 is the benchmark workload; small counts show the "
                         "decode-sized path)")
-    p.add_argument("--only", choices=["gemm", "moe", "moe65536", "mlp", "attn", "i8", "smallm", "copy", "peaks"],
+    p.add_argument("--only", choices=["gemm", "moe", "moe65536", "moesmall", "mlp", "attn", "i8", "smallm", "copy",
+                                      "peaks"],
                    default=None,
                    help="run one leg; 'copy' is a plain 512 MiB device copy, the known-size "
                         "kernel that scales HBM byte counters")
     return p.parse_args()
+
+
+def device_warmup(seconds=0.25):
+    """Brings the board to its sustained clock before the first leg: an idle
+    MI355X needs ~0.1 s of MFMA load before its power management settles (the
+    first ~100 GEMM launches run up to 25 % slower), which a leg's own few
+    warmup calls do not cover. Runs the library's INT4 GEMM, untimed; every
+    leg still does its --warmup calls and times exactly --steps calls."""
+    import torch
+
+    import clef_i4
+
+    x = bf16_randn((4096, 4096), 1.0, 7)
+    w = clef_i4.load_quantized_weight(bf16_randn((4096, 4096), 0.02, 8))
+    a = clef_i4.prepare(x)
+    out = torch.empty((4096, 4096), dtype=torch.bfloat16, device="cuda")
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            clef_i4.project_prepared(a, w, out=out)
+        torch.cuda.synchronize()
 
 
 def timed(fn, steps, warmup):
@@ -134,9 +164,52 @@ def gemm_leg(args):
     # operands read once (codes + f32 scales) and the bf16 output written once
     nbytes = m * k * 3 // 4 + 4 * m + n * k * 3 // 4 + 4 * n + 2 * m * n
     i4_bytes = m * k // 2 + 4 * m + n * k // 2 + 4 * n + 2 * m * n
+    rot = rotating_gemm(args, a, af, qw, fw, out_i4, out)
     return {"m": m, "n": n, "k": k, "ms": ms, "tops": ops / ms / 1e9, "prepare_ms": prep_ms,
-            "ops": ops, "bytes": nbytes,
+            "ops": ops, "bytes": nbytes, "rotating": rot,
             "int4": {"ms": i4_ms, "tops": ops / i4_ms / 1e9, "prepare_ms": i4_prep_ms, "bytes": i4_bytes}}
+
+
+def rotating_gemm(args, a, af, qw, fw, out_i4, out_f6):
+    """The headline projection with its weight cycled through copies that
+    together exceed the 256 MB last-level cache (as the reference's paired
+    integer benchmark keeps rotating weight copies, src/benchmarking.rs:318-381),
+    each copy with its own output: every call then streams its weight from
+    HBM instead of the cache that holds a repeated one. Both weight forms, each
+    copy's output checked against the resident run's."""
+    import torch
+
+    import clef_i4
+
+    ops = 2.0 * a.rows * qw.rows * qw.cols
+    res = {}
+    for form, copies, make, run, want in (
+            ("int4", 14, lambda: clef_i4.QuantizedWeight(qw.codes.clone(), qw.scales.clone(), qw.rows, qw.cols,
+                                                         qw.stride, qw.bits),
+             lambda w, o: clef_i4.project_prepared(a, w, out=o), out_i4),
+            ("bf6", 10, lambda: clef_i4.F6Weight(fw.codes.clone(), fw.scales.clone(), fw.rows, fw.cols),
+             lambda w, o: clef_i4.project_f6(af, w, out=o), out_f6)):
+        ws = [make() for _ in range(copies)]
+        outs = [torch.empty_like(want) for _ in range(copies)]
+        turn = [0]
+
+        def call():
+            i = turn[0] = (turn[0] + 1) % copies
+            run(ws[i], outs[i])
+
+        # whole rounds of the copies, at least as many calls as the resident timing
+        steps = max(copies, (args.steps + copies - 1) // copies * copies)
+        ms = timed(call, steps, max(copies, args.warmup // copies * copies))
+        torch.cuda.synchronize()
+        for o in outs:
+            if not torch.equal(o.view(torch.int16), want.view(torch.int16)):
+                raise SystemExit(f"rotating {form} GEMM output differs from the resident run's")
+        res[form] = {"ms": ms, "tops": ops / ms / 1e9, "copies": copies,
+                     "weight_mb_cycled": round(copies * (ws[0].codes.numel() * ws[0].codes.element_size()
+                                                         + 4 * qw.rows) / 1e6, 1)}
+        del ws, outs
+        torch.cuda.empty_cache()
+    return res
 
 
 def graph_timed(fn, calls=50, replays=8):
@@ -351,6 +424,83 @@ def moe_leg(args):
             "bytes": nbytes}
 
 
+def moe_small_leg(args):
+    """The Omni MoE layer at decode-sized token counts (1, 16 and 256 tokens;
+    hidden 2048, 128 experts, top-8, intermediate 768): GPU time per layer by
+    HIP graph replay, and the HBM rate of the two expert GEMMs alone (the
+    skinny 32-slot kernels; each call also runs its small tile-schedule
+    kernel), over the codes and scales of the experts the tokens route to.
+    `us` and the GEMM figures cycle through 14 copies of the layer's packed
+    weights, so each call reads its experts from HBM as a multi-layer decode
+    does; `us_cached` repeats one copy (the touched experts stay in the
+    last-level cache)."""
+    import ctypes
+
+    import torch
+
+    import clef_i4
+
+    d, inter, copies = 2048, 768, 14
+    base = [clef_i4.load_quantized_weight(bf16_randn((128 * inter, d), 0.02, 1004 * 16 + 2)),
+            clef_i4.load_quantized_weight(bf16_randn((128 * inter, d), 0.02, 1004 * 16 + 3)),
+            clef_i4.load_quantized_weight(bf16_randn((128 * d, inter), 0.02, 1004 * 16 + 4))]
+    layers = [[clef_i4.QuantizedWeight(w.codes.clone(), w.scales.clone(), w.rows, w.cols, w.stride, w.bits)
+               for w in base] for _ in range(copies)]
+    lib = clef_i4.lib()
+    P = ctypes.c_void_p
+    res = {}
+    for t in (1, 16, 256):
+        x = bf16_randn((t, d), 1.0, 1004 * 16 + 0)
+        logits = bf16_randn((t, 128), 1.0, 1004 * 16 + 1)
+        out = torch.empty((t, d), dtype=torch.bfloat16, device="cuda")
+        mods = [clef_i4.MoeLayer(*ws) for ws in layers]
+        turn = [0]
+
+        def layer_rotating():
+            i = turn[0] = (turn[0] + 1) % copies
+            mods[i](x, logits, out=out)
+
+        us = graph_timed(layer_rotating, calls=56) * 1e3
+        us_cached = graph_timed(lambda: mods[0](x, logits, out=out)) * 1e3
+
+        # the expert GEMMs alone on this call's routing, through the C ABI
+        routes = clef_i4.omni_route(logits, 8)
+        groups, _ = clef_i4.omni_group_routes(routes)
+        active = int((groups[:, 0] > 0).sum().item())
+        ax = clef_i4.prepare(x)
+        h = clef_i4.omni_gate_up(ax, base[0], base[1], groups, t, 8)
+        ah = clef_i4.prepare(h)
+        v = torch.empty((t * 8, d), dtype=torch.bfloat16, device="cuda")
+        wsb = int(lib.clef_moe_expert_workspace_bytes(t, 8))
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+
+        def gate_up():
+            i = turn[0] = (turn[0] + 1) % copies
+            g, u = layers[i][0], layers[i][1]
+            clef_i4._check(lib.clef_moe_expert_gate_up_i4(
+                P(ax.storage.data_ptr()), ax.stride, P(ax.scales.data_ptr()), P(g.codes.data_ptr()),
+                P(g.scales.data_ptr()), P(u.codes.data_ptr()), P(u.scales.data_ptr()), P(groups.data_ptr()), t, 8, d,
+                inter, P(h.data_ptr()), P(ws.data_ptr()), wsb, P(torch.cuda.current_stream().cuda_stream)))
+
+        def down():
+            i = turn[0] = (turn[0] + 1) % copies
+            w = layers[i][2]
+            clef_i4._check(lib.clef_moe_expert_i4(
+                P(ah.storage.data_ptr()), ah.stride, P(ah.scales.data_ptr()), P(w.codes.data_ptr()),
+                P(w.scales.data_ptr()), P(groups.data_ptr()), t, 8, inter, d, 1, P(v.data_ptr()), P(ws.data_ptr()),
+                wsb, P(torch.cuda.current_stream().cuda_stream)))
+
+        gu_us = graph_timed(gate_up, calls=56) * 1e3
+        dn_us = graph_timed(down, calls=56) * 1e3
+        gu_bytes = active * (2 * inter * d // 2 + 2 * 4 * inter)  # gate and up codes + scales
+        dn_bytes = active * (d * inter // 2 + 4 * d)
+        res[t] = {"us": us, "us_cached": us_cached, "tokens_per_s": t / us * 1e6, "active_experts": active,
+                  "gate_up_us": gu_us, "gate_up_hbm_gbs": gu_bytes / gu_us / 1e3,
+                  "down_us": dn_us, "down_hbm_gbs": dn_bytes / dn_us / 1e3}
+        del mods
+    return res
+
+
 def copy_leg(args):
     """Plain device-to-device copy of 512 MiB: read and written bytes are known
     exactly, so a counter run over it gives the factor between the FETCH_SIZE /
@@ -434,9 +584,9 @@ def main():
 
     clef_i4.lib()
     torch.cuda.init()
+    if args.only not in ("copy", "peaks"):
+        device_warmup()
     res = {}
-    if args.only in (None, "moe"):
-        res["moe"] = moe_leg(args)
     if args.only in (None, "mlp"):
         res["mlp"] = mlp_leg(args)
     if args.only in (None, "i8"):
@@ -448,9 +598,14 @@ def main():
         res["attn"] = attention_leg(args)
     if args.only in (None, "moe65536"):
         res["moe65536"] = moe_skewed_leg(args)
-    # The headline GEMM runs last: the other legs keep the device busy for
-    # seconds before it, so its timed launches see the sustained clock of a
-    # loaded device rather than the ramp of an idle one.
+    if args.only in (None, "moesmall"):
+        res["moesmall"] = moe_small_leg(args)
+    # The MoE layer and the headline GEMM run last: the other legs keep the
+    # device busy before them, so their timed calls see the sustained clock of
+    # a loaded device rather than the ramp of an idle one (the first ~100
+    # calls on an idle board run up to 25 % slower).
+    if args.only in (None, "moe"):
+        res["moe"] = moe_leg(args)
     if args.only in (None, "gemm"):
         res["gemm"] = gemm_leg(args)
     if args.only == "peaks":
@@ -497,6 +652,10 @@ def main():
         line["int4_operand_gemm"] = {"ms": round(i4["ms"], 4), "tops": round(i4["tops"], 1),
                                      "pct_int8_peak": round(100.0 * i4["tops"] / INT8_PEAK_TOPS, 2),
                                      "prepare_ms": round(i4["prepare_ms"], 4)}
+        line["rotating_weights"] = {f: {"ms": round(v["ms"], 4), "tops": round(v["tops"], 1),
+                                        "pct_int8_peak": round(100.0 * v["tops"] / INT8_PEAK_TOPS, 2),
+                                        "copies": v["copies"], "weight_mb_cycled": v["weight_mb_cycled"]}
+                                    for f, v in g["rotating"].items()}
     if "moe" in res:
         if res["moe"]["tokens"] != 4096:
             line["moe_tokens"] = res["moe"]["tokens"]
@@ -529,6 +688,15 @@ def main():
     if "attn" in res:
         line["attn_proj_m16384_ms"] = round(res["attn"]["ms"], 4)
         line["attn_proj_tops"] = round(res["attn"]["tops"], 1)
+    if "moesmall" in res:
+        line["moe_small_t"] = {f"t{t}": {"us": round(v["us"], 2), "us_cached": round(v["us_cached"], 2),
+                                         "tokens_per_s": round(v["tokens_per_s"], 1),
+                                         "active_experts": v["active_experts"],
+                                         "gate_up_us": round(v["gate_up_us"], 2),
+                                         "gate_up_hbm_gbs": round(v["gate_up_hbm_gbs"], 1),
+                                         "down_us": round(v["down_us"], 2),
+                                         "down_hbm_gbs": round(v["down_hbm_gbs"], 1)}
+                               for t, v in res["moesmall"].items()}
     if "smallm" in res:
         line["small_m_k4096_n12288"] = {f"m{m}": {"us": round(v["us"], 2), "hbm_gbs": round(v["gbs"], 1),
                                                   "us_cached": round(v["us_cached"], 2)}
