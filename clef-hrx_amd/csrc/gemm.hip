@@ -160,9 +160,8 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dma_kernel(
     const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
 #if defined(__HIP_DEVICE_COMPILE__)  // buffer-resource builtins exist only in the device pass
   extern __shared__ __align__(16) char lds[];
-  int64_t tm;
-  int tn;
-  tile_of_block(blockIdx.x, (int64_t)gridDim.x, tiles_m, tiles_n, tm, tn);
+  int tm, tn;
+  tile_of_block((int)blockIdx.x, (int)gridDim.x, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = tm * T::BM;
   const int n0 = tn * T::BN;
   const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
@@ -190,9 +189,8 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dma8_kernel(
     const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
 #if defined(__HIP_DEVICE_COMPILE__)
   extern __shared__ __align__(16) char lds[];
-  int64_t tm;
-  int tn;
-  tile_of_block(blockIdx.x, (int64_t)gridDim.x, tiles_m, tiles_n, tm, tn);
+  int tm, tn;
+  tile_of_block((int)blockIdx.x, (int)gridDim.x, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = tm * T::BM;
   const int n0 = tn * T::BN;
   const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
@@ -339,6 +337,14 @@ __device__ __forceinline__ void staged_epilogue_store(const v16i (&acc)[T::TM][T
   const __amdgpu_buffer_rsrc_t out_rsrc = make_rsrc(out + m0 * N, (uint32_t)(rows_here * N * 2));
   const __amdgpu_buffer_rsrc_t res_rsrc =
       make_rsrc(RESID ? residual + m0 * N : out, RESID ? (uint32_t)(rows_here * N * 2) : 0u);
+  // The lane's part of every store offset (the blocks' rows go in the scalar
+  // part). Opaque to the compiler: otherwise it keeps one precomputed sum per
+  // store across the persistent loop, runs out of registers and reloads them
+  // from scratch in this epilogue, each reload followed by a wait for all
+  // outstanding memory operations (the next tile's DMA included).
+  const int lrow = lane / kLanesPerRow, lchunk = lane % kLanesPerRow;
+  int voff = ((wm * T::WM + lrow) * N + n0 + wn * T::WN + 8 * lchunk) * 2;
+  asm volatile("" : "+v"(voff));
 #pragma unroll
   for (int i = 0; i < T::TM; ++i) {
     const float asv = e.asr[i];
@@ -367,10 +373,8 @@ __device__ __forceinline__ void staged_epilogue_store(const v16i (&acc)[T::TM][T
       }
 #pragma unroll
     for (int r = 0; r < kReads; ++r) {
-      const int lrow = lane / kLanesPerRow, row = kRowsPerRead * r + lrow, chunk = lane % kLanesPerRow;
+      const int row = kRowsPerRead * r + lrow, chunk = lchunk;
       v4u v = *reinterpret_cast<const v4u*>(wlds + row * kRowBytes + ((chunk ^ (row & 7)) << 4));
-      // lane part in the VGPR offset, the block's rows in the scalar offset
-      const int voff = ((wm * T::WM + lrow) * N + n0 + wn * T::WN + 8 * chunk) * 2;
       const int soff = (32 * i + kRowsPerRead * r) * N * 2;
       if (RESID) {
         const v4i rv = __builtin_amdgcn_raw_buffer_load_b128(res_rsrc, voff, soff, 0);
@@ -476,20 +480,19 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dma_persist_kernel(
     const uint16_t* __restrict__ residual, uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
 #if defined(__HIP_DEVICE_COMPILE__)
   extern __shared__ __align__(16) char lds[];
-  const int64_t total = (int64_t)tiles_m * tiles_n;
-  int64_t t = blockIdx.x;
+  const int total = tiles_m * tiles_n;  // below 2^31 (launch_dma_persist)
+  int t = blockIdx.x;
   if (t >= total) return;
   struct Tile {
     __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
     int64_t m0;
     int n0;
   };
-  auto tile = [&](int64_t b) {
-    int64_t tm;
-    int tn;
+  auto tile = [&](int b) {
+    int tm, tn;
     tile_of_block(b, total, tiles_m, tiles_n, tm, tn);
     Tile x;
-    x.m0 = tm * T::BM;
+    x.m0 = (int64_t)tm * T::BM;
     x.n0 = tn * T::BN;
     const int64_t rows_here = M - x.m0 < T::BM ? M - x.m0 : T::BM;
     x.a_rsrc = make_rsrc(a + x.m0 * a_words, (uint32_t)(rows_here * a_words * 4));
@@ -517,7 +520,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_dma_persist_kernel(
   zero();
   dma_kstep_first<T>(c, acc, stage(0), stage(1), cur.a_rsrc, voff_a, a_q_stride, cur.b_rsrc, kb);
   while (true) {
-    const int64_t tn_next = t + gridDim.x;
+    const int tn_next = t + (int)gridDim.x;
     const bool has_next = tn_next < total;
     for (int kt = 1; kt + 1 < kb; ++kt)
       dma_kstep_next<T>(c, acc, stage(g + kt), stage(g + kt + 1), cur.a_rsrc, voff_a, a_q_stride, cur.b_rsrc, kb,
@@ -548,6 +551,7 @@ hipError_t launch_dma_persist(const uint32_t* a, int a_words, const float* as, c
   const int tiles_n = n / T::BN;
   const int64_t tiles_m = (m + T::BM - 1) / T::BM;
   const int64_t total = tiles_m * tiles_n;
+  if (total > kMaxTiles) return hipErrorInvalidValue;  // the kernel's 32-bit tile indices
   int64_t grid = (int64_t)cus * per_cu / 8 * 8;
   if (grid < 8) grid = 8;
   if (grid > total) grid = total;

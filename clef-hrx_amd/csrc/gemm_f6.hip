@@ -387,15 +387,14 @@ __global__ __launch_bounds__(F6Tile::THREADS) void gemm_f6_kernel(
 #if defined(__HIP_DEVICE_COMPILE__)
   using T = F6Tile;
   extern __shared__ __align__(16) char lds[];
-  const int64_t total = (int64_t)tiles_m * tiles_n;
-  int64_t t = blockIdx.x;
+  const int total = tiles_m * tiles_n;  // below 2^31 (launch_gemm_f6_impl)
+  int t = blockIdx.x;
   if (t >= total) return;
-  auto tile = [&](int64_t b) {
-    int64_t tm;
-    int tn;
+  auto tile = [&](int b) {
+    int tm, tn;
     tile_of_block(b, total, tiles_m, tiles_n, tm, tn);
     F6Tiles x;
-    x.m0 = tm * T::BM;
+    x.m0 = (int64_t)tm * T::BM;
     x.n0 = tn * T::BN;
     const int64_t rows_here = M - x.m0 < T::BM ? M - x.m0 : T::BM;
     x.a_rsrc = make_rsrc(a + x.m0 * a_row_bytes, (uint32_t)(rows_here * a_row_bytes));
@@ -423,7 +422,7 @@ __global__ __launch_bounds__(F6Tile::THREADS) void gemm_f6_kernel(
   int rot = 0;  // ring position of the tile's k-step 0
   v16f acc[T::TM][T::TN];
   while (true) {
-    const int64_t t_next = t + gridDim.x;
+    const int t_next = t + (int)gridDim.x;
     const bool has_next = t_next < total;
     const F6Tiles nxt = tile(has_next ? t_next : t);  // the last tile re-reads its own
     scales.row0 = cur.m0 + wm * T::WM;
@@ -492,6 +491,7 @@ hipError_t launch_gemm_f6_impl(const uint8_t* a, const float* as, const uint8_t*
   const int tiles_n = n / T::BN;
   const int64_t tiles_m = (m + T::BM - 1) / T::BM;
   const int64_t total = tiles_m * tiles_n;
+  if (total > kMaxTiles) return hipErrorInvalidValue;  // the kernel's 32-bit tile indices
   int64_t grid = (int64_t)cus * per_cu / 8 * 8;
   if (grid < 8) grid = 8;
   if (grid > total) grid = total;

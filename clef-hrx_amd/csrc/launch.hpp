@@ -55,17 +55,19 @@ hipError_t resident_per_cu(LaunchCache& c, const void* kern, int threads, int ld
 // XCDs (block b runs on XCD b % 8), so block b is renumbered to make each
 // XCD's blocks consecutive, then the renumbered order walks 8-tile-tall
 // column bands: 32 co-resident blocks of one XCD cover an 8 x 4 patch and
-// share its A and B panels in that XCD's L2.
-__device__ __forceinline__ void tile_of_block(int64_t b, int64_t blocks, int tiles_m, int tiles_n,
-                                              int64_t& tm, int& tn) {
-  const int64_t per = blocks / 8;
-  const int64_t r = b < 8 * per ? (b % 8) * per + b / 8 : b;
-  const int64_t band = 8 * (int64_t)tiles_n;
-  const int64_t group = r / band, within = r - group * band;
-  const int64_t first = group * 8;
-  const int64_t height = tiles_m - first < 8 ? tiles_m - first : 8;
+// share its A and B panels in that XCD's L2. 32-bit arithmetic: the
+// launchers keep tiles_m * tiles_n below 2^31 (kMaxTiles), and 64-bit
+// divisions here cost the persistent kernels registers they spill.
+constexpr int64_t kMaxTiles = (int64_t)1 << 30;
+__device__ __forceinline__ void tile_of_block(int b, int blocks, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int per = blocks / 8;
+  const int r = b < 8 * per ? (b % 8) * per + b / 8 : b;
+  const int band = 8 * tiles_n;
+  const int group = r / band, within = r - group * band;
+  const int first = group * 8;
+  const int height = tiles_m - first < 8 ? tiles_m - first : 8;
   tm = first + within % height;
-  tn = (int)(within / height);
+  tn = within / height;
 }
 
 }  // namespace
