@@ -122,10 +122,12 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
 
   // This workgroup's XCD range of items.
   const int xcd = blockIdx.x & 7;
-  const int64_t total = (int64_t)schedule[0] * tiles_n;
-  const int64_t chunk = (total + 7) / 8;
-  const int64_t first = xcd * chunk;
-  const int64_t mine = total - first < chunk ? (total - first > 0 ? total - first : 0) : chunk;
+  // Item counts are below 2^31 (the launcher bounds tiles * tiles_n): 32-bit
+  // arithmetic, which keeps the per-item index math off 64-bit division.
+  const int total = schedule[0] * tiles_n;
+  const int chunk = (total + 7) / 8;
+  const int first = xcd * chunk;
+  const int mine = total - first < chunk ? (total - first > 0 ? total - first : 0) : chunk;
 
   const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a, a_bytes);
   const uint32_t b_bytes = (uint32_t)((P::COLS / 128) * kb * 16384);
@@ -155,9 +157,9 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
   };
   // Step 1: the schedule entry of item `local`.
   auto fetch_entry = [&](int local, int& e_v, int& r_v, int& n0) {
-    const int64_t it = first + local;
-    const int tile = (int)(it / tiles_n);
-    n0 = (int)(it - (int64_t)tile * tiles_n) * P::COLS;
+    const int it = first + local;
+    const int tile = it / tiles_n;
+    n0 = (it - tile * tiles_n) * P::COLS;
     e_v = __builtin_amdgcn_raw_buffer_load_b32(sched_rsrc, 0, (kSchedEntries + 2 * tile) * 4, 0);
     r_v = __builtin_amdgcn_raw_buffer_load_b32(sched_rsrc, 0, (kSchedEntries + 1 + 2 * tile) * 4, 0);
   };
@@ -193,14 +195,15 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
 #pragma unroll
     for (int ql = 0; ql < T::A_INST; ++ql) {
       const int r = 16 * (wave + NW * ql) + (lane >> 2);
-      const int64_t route = row0 + r < count ? (int64_t)routes[r] : 0;
-      const int64_t xr = input_routed ? route : route / topk;
-      voff[ql] = row0 + r < count ? (int)(xr * a_words * 4) + dmah_chunk16(lane) : (int)0x80000000u;
+      // ordinals are below 2^24 and the operand below 2 GiB: 32-bit math
+      const int route = row0 + r < count ? (int)routes[r] : 0;
+      const int xr = input_routed ? route : route / topk;
+      voff[ql] = row0 + r < count ? xr * a_words * 4 + dmah_chunk16(lane) : (int)0x80000000u;
     }
     if (wave < 2) {
       const int rs = 64 * wave + lane;
-      const int64_t rt = row0 + rs < count ? (int64_t)routes[rs] : 0;
-      const int64_t xs = input_routed ? rt : rt / topk;
+      const int rt = row0 + rs < count ? (int)routes[rs] : 0;
+      const int xs = input_routed ? rt : rt / topk;
       const __amdgpu_buffer_rsrc_t s_rsrc = make_rsrc(as, 0x7fffffff);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rsrc, (lds_ptr_t)(as_out + 256 * wave), 4,
                                                row0 + rs < count ? (int)(xs * 4) : (int)0x80000000u, 0, 0, 0);

@@ -1743,7 +1743,8 @@ template <bool GU>
 bool use_expert_persist(int k, int n, int64_t routes) {
   using P = ExpertPersist<GU, kExpertWaves>;
   return k / 256 * 2 >= P::MIN_HALF_STEPS && n % P::COLS == 0 &&
-         routes * n * 2 <= ((int64_t)1 << 31);  // 32-bit store offsets
+         routes * n * 2 <= ((int64_t)1 << 31) &&  // 32-bit store offsets
+         expert_max_tiles(routes) * (n / P::COLS) < ((int64_t)1 << 31);  // 32-bit item indices
 }
 }  // namespace
 
