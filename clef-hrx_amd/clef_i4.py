@@ -248,24 +248,36 @@ class QuantizedProjections:
     Mirrors QuantizedProjections::{for_precision, precision, resident_bytes,
     is_bf16, is_full_int4} (src/quantized.rs:41-62, 104-127) with Precision
     from src/model.rs:22-29 given as "bf16", "int4_mlp" or "int4".
+
+    `forms` (this library's addition) names the packed forms each 4-bit
+    weight keeps resident: "int4" is the reference's tiled codes (N*K/2
+    bytes), "bf6" the same codes as e3m2 for the bf6 GEMM (N*K*3/4 bytes,
+    clef_i4_f6_weight); both share the N f32 row scales. The default keeps the
+    reference's form only; ("int4", "bf6") keeps both (2.5x the reference's
+    code bytes), ("bf6",) the bf6 form alone (1.5x), which serves every
+    projection through project_f6 with the same output bits.
     """
 
     PRECISIONS = ("bf16", "int4_mlp", "int4")
+    FORMS = ("int4", "bf6")
 
     def __init__(self, bits: int | None = None, backbone_bits: int | None = None,
-                 projections=("up", "gate", "down"), share_packing: bool = False):
+                 projections=("up", "gate", "down"), share_packing: bool = False, forms=("int4",)):
         self.bits = bits
         self.backbone_bits = backbone_bits
         self.projections = list(projections)
         self.share_packing = share_packing
+        if not forms or any(f not in self.FORMS for f in forms):
+            raise ValueError(f"unknown resident weight forms {forms!r}")
+        self.forms = tuple(forms)
 
     @classmethod
-    def for_precision(cls, precision: str) -> "QuantizedProjections":
+    def for_precision(cls, precision: str, forms=("int4",)) -> "QuantizedProjections":
         if precision not in cls.PRECISIONS:
             raise ValueError(f"unknown precision {precision!r}")
         return cls(bits=4 if precision == "int4_mlp" else None,
                    backbone_bits=4 if precision == "int4" else None,
-                   share_packing=precision != "bf16")
+                   share_packing=precision != "bf16", forms=forms)
 
     def is_bf16(self) -> bool:
         return self.bits is None and self.backbone_bits is None
@@ -289,8 +301,32 @@ class QuantizedProjections:
         bits = self.precision(name, rows, cols)
         if bits is None:
             return rows * cols * 2
-        # retiled codes carry no stride padding; one f32 scale per row
-        return rows * cols * bits // 8 + rows * 4
+        # retiled codes carry no stride padding; one f32 scale per row, shared
+        # by the forms of a 4-bit weight
+        if bits != 4:
+            return rows * cols * bits // 8 + rows * 4
+        code_bytes = {"int4": rows * cols // 2, "bf6": rows * cols * 3 // 4}
+        return sum(code_bytes[f] for f in self.forms) + rows * 4
+
+    def pack(self, w: torch.Tensor, name: str, tiled_checkpoint: bool = False):
+        """The resident forms of checkpoint weight `name` (bf16 [rows][cols]):
+        a dict with "int4" (QuantizedWeight) and/or "bf6" (F6Weight) as
+        `forms` asks, or {"bf16": w} when the weight stays bf16. The bf6 form
+        is made from the packed codes, whose buffer is dropped when "int4" is
+        not kept; resident_bytes counts exactly what is returned."""
+        rows, cols = w.shape
+        bits = self.precision(name, rows, cols)
+        if bits is None:
+            return {"bf16": w}
+        qw = load_quantized_weight(w, bits=bits, tiled_checkpoint=tiled_checkpoint)
+        if bits != 4:
+            return {"int" + str(bits): qw}
+        out = {}
+        if "bf6" in self.forms:
+            out["bf6"] = f6_weight(qw)
+        if "int4" in self.forms:
+            out["int4"] = qw
+        return out
 
 
 class _PackKey(ctypes.Structure):

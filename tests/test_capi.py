@@ -367,3 +367,21 @@ def test_static_layer_rejects_700_tokens():
     rc, msg = call("clef_moe_layer_static", FAKE, FAKE, 0, 700, 2048, 768, 128, 8, FAKE, FAKE, FAKE, FAKE, FAKE,
                    FAKE, None, FAKE, None)
     assert rc == -1 and msg.startswith(f"MoE layer needs {need} bytes of scratch")
+
+
+def test_resident_bytes_count_the_kept_weight_forms():
+    """A 4-bit projection kept in the bf6 form costs N*K*3/4 code bytes, both
+    forms N*K*5/4; the f32 row scales are shared. bf16 weights are unaffected."""
+    name = "model.language_model.layers.0.mlp.up_proj.weight"
+    n, k = 17408, 5120
+    ref = clef_i4.QuantizedProjections.for_precision("int4_mlp")
+    both = clef_i4.QuantizedProjections.for_precision("int4_mlp", forms=("int4", "bf6"))
+    f6 = clef_i4.QuantizedProjections.for_precision("int4_mlp", forms=("bf6",))
+    assert ref.resident_bytes(name, n, k) == n * k // 2 + 4 * n
+    assert both.resident_bytes(name, n, k) == n * k // 2 + n * k * 3 // 4 + 4 * n
+    assert f6.resident_bytes(name, n, k) == n * k * 3 // 4 + 4 * n
+    assert f6.resident_bytes("model.visual.blocks.0.mlp.up_proj.weight", 4096, 4096) == 4096 * 4096 * 2
+    with pytest.raises(ValueError):
+        clef_i4.QuantizedProjections(bits=4, forms=("int4", "fp8"))
+    with pytest.raises(ValueError):
+        clef_i4.QuantizedProjections(bits=4, forms=())

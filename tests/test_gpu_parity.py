@@ -1114,3 +1114,28 @@ def test_project_quantized_f6_matches_project_quantized(m, n, k, resid):
     want = bf16_host(clef_i4.project_quantized(x, qw, residual=res))
     got = bf16_host(clef_i4.project_quantized_f6(x, clef_i4.f6_weight(qw), residual=res))
     assert_same_u16(got, want, f"project_quantized_f6 m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("forms", [("int4",), ("bf6",), ("int4", "bf6")])
+def test_projection_forms_resident_bytes_and_output(forms):
+    """QuantizedProjections.pack keeps exactly the forms asked for, their
+    buffers add up to resident_bytes, and a projection through either form
+    gives the reference-format GEMM's output bit for bit."""
+    name = "model.language_model.layers.0.mlp.gate_proj.weight"
+    n, k, m = 512, 1024, 40
+    rng = np.random.default_rng(77)
+    w = to_dev_bf16(randn_bf16(rng, (n, k), std=0.02))
+    x = to_dev_bf16(randn_bf16(rng, (m, k)))
+    policy = clef_i4.QuantizedProjections.for_precision("int4_mlp", forms=forms)
+    packed = policy.pack(w, name)
+    assert set(packed) == set(forms)
+    held = sum(t.numel() * t.element_size() for p in packed.values() for t in (p.codes,))
+    held += n * 4  # the shared row scales
+    assert held == policy.resident_bytes(name, n, k)
+    want = clef_i4.project_prepared(clef_i4.prepare(x), clef_i4.load_quantized_weight(w))
+    if "int4" in packed:
+        got = clef_i4.project_prepared(clef_i4.prepare(x), packed["int4"])
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    if "bf6" in packed:
+        got = clef_i4.project_f6(clef_i4.prepare_f6(x), packed["bf6"])
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
