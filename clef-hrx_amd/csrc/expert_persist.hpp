@@ -337,7 +337,13 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void expert_persist_kerne
         c.template substep<false>(acc, 1, 0, 0, 0);
       }
     };
+    // The contraction at raised issue priority: the other workgroup's
+    // epilogue on the same SIMDs then takes the issue slots the MFMA stream
+    // leaves free instead of taking turns with it (measured 7 % faster for the
+    // fused gate/up kernel at 4096 tokens, 3 % for the down projection).
+    __builtin_amdgcn_s_setprio(2);
     main_loop(st[0], st[1], st[2], meta_nxt);
+    __builtin_amdgcn_s_setprio(0);
 
     // The next item's stages: its half-step 0 goes where this item's
     // half-step H would (stage H % NST), and so on around the ring.
