@@ -18,8 +18,9 @@ M=4096 on one MI355X.
                top-8, expert intermediate 768: route -> group -> expert GEMMs
                -> SwiGLU -> combine, timed over --steps layer calls.
   mlp_*        INT4-MLP dense block, 4096 x 4096 input, gate|up 24576 x 4096,
-               down 4096 x 12288: quantize -> GEMM -> SwiGLU+quantize -> GEMM
-               (bf6 form of the codes, checked against the INT4 block).
+               down 4096 x 12288: quantize -> gate|up GEMM with SwiGLU in its
+               epilogue -> quantize -> GEMM (bf6 form of the codes, checked
+               against the INT4 block).
   int8_gemm_*  the INT8 x INT8 projection at the GEMM's shape.
   small_m_*    M = 1, 16, 64 on the GEMM's weight (K4096 N12288): GPU time per
                call (HIP graph replay) and HBM GB/s of the bytes the call moves,
@@ -367,9 +368,10 @@ def i8_leg(args):
 
 def mlp_leg(args):
     """The INT4-MLP block M4096 D4096 F12288 on the bf6 form of the codes:
-    Q1(x) -> gate and up projections -> SwiGLU-fused Q1(h) -> down
-    projection, each quantizer writing bf6, the weights re-encoded once. The
-    output is checked bit for bit against the same block on INT4 operands."""
+    Q1(x) -> gate and up projections with SwiGLU in one GEMM (h written once)
+    -> Q1(h) -> down projection, each quantizer writing bf6, the weights
+    re-encoded once. The output is checked bit for bit against the same block
+    on INT4 operands (separate gate, up and SwiGLU-fused Q1)."""
     import torch
 
     import clef_i4
@@ -380,17 +382,15 @@ def mlp_leg(args):
     wu = clef_i4.load_quantized_weight(bf16_randn((f, d), 0.02, 1002 * 16 + 3))
     wd = clef_i4.load_quantized_weight(bf16_randn((d, f), 0.02, 1002 * 16 + 4))
     fg, fu, fd = clef_i4.f6_weight(wg), clef_i4.f6_weight(wu), clef_i4.f6_weight(wd)
-    gate = torch.empty((m, f), dtype=torch.bfloat16, device="cuda")
-    up = torch.empty((m, f), dtype=torch.bfloat16, device="cuda")
+    hb = torch.empty((m, f), dtype=torch.bfloat16, device="cuda")
     y = torch.empty((m, d), dtype=torch.bfloat16, device="cuda")
     a = clef_i4.prepare_f6(x)
-    h = clef_i4.prepare_swiglu_f6(gate, up)
+    h = clef_i4.prepare_f6(hb)
 
     def block():
         clef_i4.prepare_f6(x, out=a.storage)
-        clef_i4.project_f6(a, fg, out=gate)
-        clef_i4.project_f6(a, fu, out=up)
-        clef_i4.prepare_swiglu_f6(gate, up, out=h.storage)
+        clef_i4.project_gate_up_f6(a, fg, fu, out=hb)
+        clef_i4.prepare_f6(hb, out=h.storage)
         clef_i4.project_f6(h, fd, out=y)
 
     ms = timed(block, args.steps, max(1, args.warmup // 2))

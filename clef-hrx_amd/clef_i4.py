@@ -49,6 +49,7 @@ SIGNATURES = {
     "clef_i4_f6_activation": (ctypes.c_int, [_P, _I32, _I64, _I32, _P, _P]),
     "clef_i4_f6_weight": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
     "clef_i4_gemm_f6": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P]),
+    "clef_i4_gemm_f6_gate_up": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P, _P]),
     "clef_i4_f6_prepared_bytes": (ctypes.c_int64, [_I64, _I32]),
     "clef_i4_prepare_f6": (ctypes.c_int, [_P, _I64, _I32, _P, _P]),
     "clef_i4_prepare_swiglu_f6": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _P]),
@@ -565,6 +566,22 @@ def project_f6(a: PreparedF6, w: F6Weight, residual: torch.Tensor | None = None,
     if a.width != w.cols:
         raise ClefError(-1, "unsupported integer projection shape")
     return gemm_f6(a.codes, a.scales, w, residual, out)
+
+
+def project_gate_up_f6(a: PreparedF6, gate: F6Weight, up: F6Weight, out: torch.Tensor | None = None
+                       ) -> torch.Tensor:
+    """The dense MLP's gate and up projections with SwiGLU in one bf6 GEMM
+    (clef_i4_gemm_f6_gate_up): h = swiglu(project_f6(a, gate), project_f6(a,
+    up)) bit for bit, for the reference's dense MLP (src/quantized.rs:399-401,
+    406-439), without writing gate and up."""
+    if a.width != gate.cols or gate.cols != up.cols or gate.rows != up.rows:
+        raise ClefError(-1, "unsupported integer projection shape")
+    if out is None:
+        out = _empty((a.rows, gate.rows), torch.bfloat16, a.storage.device)
+    _check(lib().clef_i4_gemm_f6_gate_up(_ptr(a.codes), _ptr(a.scales), _ptr(gate.codes), _ptr(gate.scales),
+                                         _ptr(up.codes), _ptr(up.scales), a.rows, gate.rows, gate.cols, _ptr(out),
+                                         _stream()))
+    return out
 
 
 def project_quantized_f6(x: torch.Tensor, w: F6Weight, residual: torch.Tensor | None = None,

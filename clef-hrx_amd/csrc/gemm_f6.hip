@@ -38,6 +38,7 @@
 #include "gemm_dma.hpp"
 #include "kernels.hpp"
 #include "launch.hpp"
+#include "silu_table.hpp"
 
 namespace clef {
 
@@ -126,6 +127,9 @@ struct F6Tile {
   static constexpr int EPI_WAVE = 32 * WN * 2;                  // staging bytes per wave (32 rows of WN bf16)
   static constexpr int SCALE_WAVE = 1024;                       // per-wave epilogue scales (768 bytes used)
   static constexpr int LDS = NST * STAGE_BYTES + NW * SCALE_WAVE;  // 152 KiB
+  // fused gate/up: the SiLU window after the scales (exactly 160 KiB)
+  static constexpr int LUT_OFF = LDS;
+  static constexpr int LDS_GU = LUT_OFF + kSiluWinBytes;
   static_assert(NW * EPI_WAVE <= STAGE_BYTES, "the epilogue stages its output in one free stage");
   static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "whole DMA instructions per wave");
   static_assert(BN % 128 == 0 && B_BYTES / 1024 % (BN / 128) == 0, "12 DMA instructions per 128-row panel");
@@ -160,9 +164,10 @@ __device__ __forceinline__ v16f mfma_f6(v8i w, v8i a, v16f c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 3, 3, 0, 127, 0, 127);
 }
 
-// DMA addressing of one workgroup tile.
+// DMA addressing of one workgroup tile (fused gate/up: B rows 0..127 from
+// the gate panel b_rsrc, 128..255 from the up panel b_rsrc2).
 struct F6Tiles {
-  __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
+  __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc, b_rsrc2;
   int64_t m0;
   int n0;
 };
@@ -190,21 +195,32 @@ struct F6Scales {
   int64_t row0;  // first row of the wave's rows
   int col0;      // first column of the wave's columns
 };
-__device__ __forceinline__ void f6_issue_scales(char* __restrict__ sc, const F6Scales& s) {
+// Fused gate/up (GU): the wave's WN / 2 gate column scales at byte 512 and
+// its WN / 2 up column scales at byte 768 (ws2), from column col0.
+template <bool GU = false>
+__device__ __forceinline__ void f6_issue_scales(char* __restrict__ sc, const F6Scales& s, const float* ws2 = nullptr) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int r = 0; r < F6Tile::WM / 64; ++r)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(s.as_rsrc, (lds_ptr_t)(sc + 256 * r), 4, lane * 4,
                                              (int)((s.row0 + 64 * r) * 4), 0, 0);
-  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(s.ws + s.col0, F6Tile::WN * 4);
+  if constexpr (GU) {
+    const __amdgpu_buffer_rsrc_t g_rsrc = make_rsrc(s.ws + s.col0, F6Tile::WN / 2 * 4);
+    const __amdgpu_buffer_rsrc_t u_rsrc = make_rsrc(ws2 + s.col0, F6Tile::WN / 2 * 4);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(g_rsrc, (lds_ptr_t)(sc + 512), 4, lane * 4, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(u_rsrc, (lds_ptr_t)(sc + 768), 4, lane * 4, 0, 0, 0);
+  } else {
+    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(s.ws + s.col0, F6Tile::WN * 4);
 #pragma unroll
-  for (int c = 0; c < F6Tile::WN / 64; ++c)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(sc + 512 + 256 * c), 4, lane * 4, 256 * c, 0, 0);
+    for (int c = 0; c < F6Tile::WN / 64; ++c)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(sc + 512 + 256 * c), 4, lane * 4, 256 * c, 0, 0);
+  }
 }
 
 // DMA instruction `slot` of this wave's share of k-step kt of tile `x` into
 // `stage` (slots 0 .. A_INST - 1 move A rows, the rest B rows; together the
-// slots are f6_issue).
+// slots are f6_issue). GU: the second 128-row panel comes from b_rsrc2.
+template <bool GU = false>
 __device__ __forceinline__ void f6_issue_slot(char* stage, const F6Tiles& x, const int (&voff_a)[F6Tile::A_INST],
                                               int kb, int kt, int slot) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -214,16 +230,22 @@ __device__ __forceinline__ void f6_issue_slot(char* stage, const F6Tiles& x, con
   } else {
     const int q = wave + F6Tile::NW * (slot - F6Tile::A_INST);
     const int panel = q / 12, in_blk = (q % 12) * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(x.b_rsrc, (lds_ptr_t)(stage + F6Tile::A_BYTES + q * 1024), 16,
-                                             lane * 16, (panel * kb + kt) * 12288 + in_blk, 0, 0);
+    if constexpr (GU)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(panel == 0 ? x.b_rsrc : x.b_rsrc2,
+                                               (lds_ptr_t)(stage + F6Tile::A_BYTES + q * 1024), 16, lane * 16,
+                                               kt * 12288 + in_blk, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(x.b_rsrc, (lds_ptr_t)(stage + F6Tile::A_BYTES + q * 1024), 16,
+                                               lane * 16, (panel * kb + kt) * 12288 + in_blk, 0, 0);
   }
 }
 
 // DMA of k-step kt of tile `x` into `stage` (all of this wave's slots).
+template <bool GU = false>
 __device__ __forceinline__ void f6_issue(char* stage, const F6Tiles& x, const int (&voff_a)[F6Tile::A_INST], int kb,
                                          int kt) {
 #pragma unroll
-  for (int slot = 0; slot < F6Tile::INST; ++slot) f6_issue_slot(stage, x, voff_a, kb, kt, slot);
+  for (int slot = 0; slot < F6Tile::INST; ++slot) f6_issue_slot<GU>(stage, x, voff_a, kb, kt, slot);
 }
 
 // The two MFMA rounds of one k-step on stage `rd`, with the DMA of k-step
@@ -233,9 +255,13 @@ __device__ __forceinline__ void f6_issue(char* stage, const F6Tiles& x, const in
 // under the MFMAs already issued, and the loads start earlier in the k-step
 // than when all of them follow the MFMAs (measured 4 % faster over the
 // M4096 K4096 N12288 projection).
+// GU: weight fragment j of the wave starts at B row b_base + j * b_step (its
+// gate and up fragments); otherwise b_step = 32 * ROW.
+template <bool GU = false>
 __device__ __forceinline__ void f6_compute(v16f (&acc)[F6Tile::TM][F6Tile::TN], const char* __restrict__ rd,
                                            const F6Offsets& o, int a_base, int b_base, char* __restrict__ nx,
-                                           const F6Tiles& x, const int (&voff_a)[F6Tile::A_INST], int kb, int ks) {
+                                           const F6Tiles& x, const int (&voff_a)[F6Tile::A_INST], int kb, int ks,
+                                           int b_step = 32 * F6Tile::ROW) {
   using T = F6Tile;
   int slot = 0, idx = 0;
 #pragma unroll
@@ -244,7 +270,7 @@ __device__ __forceinline__ void f6_compute(v16f (&acc)[F6Tile::TM][F6Tile::TN], 
 #pragma unroll
     for (int i = 0; i < T::TM; ++i) fa[i] = o.operand(rd + a_base + i * 32 * T::ROW, mf);
 #pragma unroll
-    for (int j = 0; j < T::TN; ++j) fb[j] = o.operand(rd + T::A_BYTES + b_base + j * 32 * T::ROW, mf);
+    for (int j = 0; j < T::TN; ++j) fb[j] = o.operand(rd + T::A_BYTES + b_base + j * b_step, mf);
 #pragma unroll
     for (int i = 0; i < T::TM; ++i)
 #pragma unroll
@@ -252,7 +278,7 @@ __device__ __forceinline__ void f6_compute(v16f (&acc)[F6Tile::TM][F6Tile::TN], 
         acc[i][j] = mfma_f6(fb[j], fa[i], acc[i][j]);
         if ((idx & 1) && idx >= 3 && slot < T::INST) {
           __builtin_amdgcn_sched_barrier(0);
-          f6_issue_slot(nx, x, voff_a, kb, ks, slot);
+          f6_issue_slot<GU>(nx, x, voff_a, kb, ks, slot);
           ++slot;
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -260,7 +286,7 @@ __device__ __forceinline__ void f6_compute(v16f (&acc)[F6Tile::TM][F6Tile::TN], 
       }
   }
 #pragma unroll
-  for (; slot < T::INST; ++slot) f6_issue_slot(nx, x, voff_a, kb, ks, slot);
+  for (; slot < T::INST; ++slot) f6_issue_slot<GU>(nx, x, voff_a, kb, ks, slot);
 }
 
 // Workgroup barrier that waits for this wave's LDS operations only (a
@@ -372,6 +398,137 @@ __device__ __forceinline__ void f6_epilogue(const v16f (&acc)[F6Tile::TM][F6Tile
   }
 }
 
+// Epilogue of the fused gate/up projection: h = S1(G1(gate), G1(up)) =
+// bf16(silu_bf16(g) * u) for the wave's WN / 2 output columns, where the
+// wave's weight fragment 0 holds gate rows and fragment 1 the up rows of the
+// same columns (kernels/swiglu.loom:43-51 on the two G1 outputs, each rounded
+// to bf16 first, as the separate gate, up and SwiGLU steps do). Staged per
+// wave 32 rows at a time (64-byte rows, chunk q of row r at q ^ (r & 3)) and
+// stored as 16-byte row pieces. The SiLU comes from the table window in LDS
+// (silu_window_pair); values outside it take silu_bf16 on a wave-uniform
+// branch.
+__device__ __forceinline__ void f6_epilogue_gu(const v16f (&acc)[F6Tile::TM][F6Tile::TN], int K, int64_t M, int N,
+                                               int64_t m0, int n0, uint16_t* __restrict__ out,
+                                               char* __restrict__ wlds, const char* __restrict__ sc,
+                                               const char* __restrict__ lut) {
+  using T = F6Tile;
+  constexpr int WC = T::WN / 2;  // output columns per wave
+  constexpr int kRowBytes = WC * 2, kLanesPerRow = WC / 8, kRowsPerRead = 64 / kLanesPerRow;
+  constexpr int kReads = 32 / kRowsPerRead;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+  const int h = lane >> 5, lr = lane & 31;
+  const float inf = __builtin_huge_valf();
+  float asr[T::TM];
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) asr[i] = *reinterpret_cast<const float*>(sc + (32 * i + lr) * 4);
+  // fast path as in f6_epilogue, over the wave's rows and both column sets
+  // (the clamp cannot fire: every G1 value is RN(RN(dot * ws) * as) + 0)
+  bool ok = true;
+  float amax = 0.0f, wmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < T::TM; ++i) {
+    if (m0 + wm * T::WM + 32 * i + lr < M) {
+      ok = ok & (asr[i] > 0.0f) & (asr[i] < inf);
+      amax = __builtin_fmaxf(amax, asr[i]);
+    }
+  }
+  {
+    // lane lr holds gate and up scale lr of the wave's 32 columns; the bound
+    // takes the wave's largest column and row scales (a lane's values mix
+    // rows and columns that other lanes checked)
+    const float wgl = *reinterpret_cast<const float*>(sc + 512 + lr * 4);
+    const float wul = *reinterpret_cast<const float*>(sc + 768 + lr * 4);
+    ok = ok & (wgl > 0.0f) & (wgl < inf) & (wul > 0.0f) & (wul < inf);
+    wmax = __builtin_fmaxf(wgl, wul);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      wmax = __builtin_fmaxf(wmax, __shfl_xor(wmax, off));
+      amax = __builtin_fmaxf(amax, __shfl_xor(amax, off));
+    }
+  }
+  ok = ok & (wmax * amax * (64.0f * (float)K) < kBf16Max);
+  const bool fast = __all(ok);
+  const int64_t rows_here = M - m0 < T::BM ? M - m0 : T::BM;
+  const __amdgpu_buffer_rsrc_t out_rsrc = make_rsrc(out + m0 * N, (uint32_t)(rows_here * N * 2));
+  // this lane's 16 gate and 16 up column scales (columns 8q + 4h .. + 3)
+  float4 wg[4], wu[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    wg[q] = *reinterpret_cast<const float4*>(sc + 512 + (8 * q + 4 * h) * 4);
+    wu[q] = *reinterpret_cast<const float4*>(sc + 768 + (8 * q + 4 * h) * 4);
+  }
+  // one copy of the loop per path (a wave-uniform flag tested inside would be
+  // re-tested per value, a scheduling barrier between the table reads)
+  auto values = [&](auto fast_tag) {
+    constexpr bool FAST = decltype(fast_tag)::value;
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i) {
+      const float asv = asr[i];
+      // the fragment's 16 gate and up pairs first, their 32 table reads in
+      // flight together, then one wave-uniform check for values the window
+      // does not cover
+      uint32_t gp[4][2], upv[4][2], act[4][2];
+      uint32_t outside = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float g4[4] = {wg[q].x, wg[q].y, wg[q].z, wg[q].w};
+        const float u4[4] = {wu[q].x, wu[q].y, wu[q].z, wu[q].w};
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          if constexpr (FAST) {
+            gp[q][p] = pack_bf16x2(acc[i][0][4 * q + 2 * p] * g4[2 * p] * asv + 0.0f,
+                                   acc[i][0][4 * q + 2 * p + 1] * g4[2 * p + 1] * asv + 0.0f);
+            upv[q][p] = pack_bf16x2(acc[i][1][4 * q + 2 * p] * u4[2 * p] * asv + 0.0f,
+                                    acc[i][1][4 * q + 2 * p + 1] * u4[2 * p + 1] * asv + 0.0f);
+          } else {
+            gp[q][p] = g1_f6(acc[i][0][4 * q + 2 * p], g4[2 * p], asv) |
+                       (g1_f6(acc[i][0][4 * q + 2 * p + 1], g4[2 * p + 1], asv) << 16);
+            upv[q][p] = g1_f6(acc[i][1][4 * q + 2 * p], u4[2 * p], asv) |
+                        (g1_f6(acc[i][1][4 * q + 2 * p + 1], u4[2 * p + 1], asv) << 16);
+          }
+          act[q][p] = silu_window_pair<true>(gp[q][p], lut, outside);
+        }
+      }
+      if (__any(outside != 0)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            uint32_t fix = 0;
+            silu_window_pair<true>(gp[q][p], lut, fix);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+              if ((fix >> (16 * t)) & 0x8000u) {
+                const uint32_t gb = (gp[q][p] >> (16 * t)) & 0xFFFFu;
+                const uint32_t sb = f32_to_bf16(silu_bf16(bf16_to_f32(gb)));
+                act[q][p] = (act[q][p] & (0xFFFF0000u >> (16 * t))) | (sb << (16 * t));
+              }
+          }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t h0 =
+            pack_bf16x2(bf16_lo(act[q][0]) * bf16_lo(upv[q][0]), bf16_hi(act[q][0]) * bf16_hi(upv[q][0]));
+        const uint32_t h1 =
+            pack_bf16x2(bf16_lo(act[q][1]) * bf16_lo(upv[q][1]), bf16_hi(act[q][1]) * bf16_hi(upv[q][1]));
+        *reinterpret_cast<f6_v2u*>(wlds + lr * kRowBytes + ((q ^ (lr & 3)) << 4) + 8 * h) = f6_v2u{h0, h1};
+      }
+#pragma unroll
+      for (int r = 0; r < kReads; ++r) {
+        const int lrow = lane / kLanesPerRow, row = kRowsPerRead * r + lrow, chunk = lane % kLanesPerRow;
+        const f6_v4u v = *reinterpret_cast<const f6_v4u*>(wlds + row * kRowBytes + ((chunk ^ (row & 3)) << 4));
+        const int voff = ((wm * T::WM + 32 * i + row) * N + n0 + wn * WC + 8 * chunk) * 2;
+        store_b128(out_rsrc, voff, v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]});
+      }
+    }
+  };
+  if (fast)
+    values(std::true_type{});
+  else
+    values(std::false_type{});
+}
+
 // Persistent bf6 G1: workgroup b walks tiles b, b + grid, ... (grid a
 // multiple of 8: all on its XCD, in the XCD-aware order of tile_of_block).
 // Three LDS stages in a ring: k-step kt reads stage kt % 3 while the DMA of
@@ -379,13 +536,21 @@ __device__ __forceinline__ void f6_epilogue(const v16f (&acc)[F6Tile::TM][F6Tile
 // the next tile's first two, and k-step 0 the tile's scales (into the wave's
 // own block). The epilogue stages its output in the stage the last k-step
 // read, and its stores drain under the next tile's first k-step.
-template <bool RESID>
+//
+// GU (fused gate/up, benches/kernels/omni_gate_up_i4.loom's dense form): a
+// tile is 256 rows x 128 output columns of h; its B stage holds the 128 gate
+// rows (w) and the same 128 up rows (w2) of those columns, wave (wm, wn)
+// multiplies gate rows 32 wn .. and up rows 128 + 32 wn .., and the epilogue
+// writes h = S1(G1(gate), G1(up)) (f6_epilogue_gu); N is the width of h.
+template <bool RESID, bool GU = false>
 __global__ __launch_bounds__(F6Tile::THREADS) void gemm_f6_kernel(
     const uint8_t* __restrict__ a, int a_row_bytes, const float* __restrict__ as, const uint8_t* __restrict__ w,
     const float* __restrict__ ws, int64_t M, int N, int kb, const uint16_t* __restrict__ residual,
-    uint16_t* __restrict__ out, int tiles_m, int tiles_n) {
+    uint16_t* __restrict__ out, int tiles_m, int tiles_n, const uint8_t* __restrict__ w2 = nullptr,
+    const float* __restrict__ ws2 = nullptr) {
 #if defined(__HIP_DEVICE_COMPILE__)
   using T = F6Tile;
+  constexpr int TILE_N = GU ? T::BN / 2 : T::BN;  // output columns per tile
   extern __shared__ __align__(16) char lds[];
   const int total = tiles_m * tiles_n;  // below 2^31 (launch_gemm_f6_impl)
   int t = blockIdx.x;
@@ -395,10 +560,11 @@ __global__ __launch_bounds__(F6Tile::THREADS) void gemm_f6_kernel(
     tile_of_block(b, total, tiles_m, tiles_n, tm, tn);
     F6Tiles x;
     x.m0 = (int64_t)tm * T::BM;
-    x.n0 = tn * T::BN;
+    x.n0 = tn * TILE_N;
     const int64_t rows_here = M - x.m0 < T::BM ? M - x.m0 : T::BM;
     x.a_rsrc = make_rsrc(a + x.m0 * a_row_bytes, (uint32_t)(rows_here * a_row_bytes));
-    x.b_rsrc = make_rsrc(w + (int64_t)(x.n0 / 128) * kb * 12288, (uint32_t)((T::BN / 128) * kb * 12288));
+    x.b_rsrc = make_rsrc(w + (int64_t)(x.n0 / 128) * kb * 12288, (uint32_t)((TILE_N / 128) * kb * 12288));
+    x.b_rsrc2 = GU ? make_rsrc(w2 + (int64_t)(x.n0 / 128) * kb * 12288, (uint32_t)(kb * 12288)) : x.b_rsrc;
     return x;
   };
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -407,7 +573,9 @@ __global__ __launch_bounds__(F6Tile::THREADS) void gemm_f6_kernel(
   int voff_a[T::A_INST];
   f6_a_offsets(a_row_bytes, voff_a);
   const F6Offsets o;
-  const int a_base = (wm * T::WM + lr) * T::ROW, b_base = (wn * T::WN + lr) * T::ROW;
+  const int a_base = (wm * T::WM + lr) * T::ROW;
+  const int b_base = ((GU ? wn * (T::WN / 2) : wn * T::WN) + lr) * T::ROW;
+  const int b_step = (GU ? T::BN / 2 : 32) * T::ROW;  // weight fragment 1: the up rows (GU)
   auto st = [&](int i) { return lds + i * T::STAGE_BYTES; };
   char* sc = lds + T::NST * T::STAGE_BYTES + wave * T::SCALE_WAVE;
   F6Scales scales;
@@ -415,8 +583,16 @@ __global__ __launch_bounds__(F6Tile::THREADS) void gemm_f6_kernel(
   scales.ws = ws;
 
   F6Tiles cur = tile(t);
-  f6_issue(st(0), cur, voff_a, kb, 0);
-  f6_issue(st(1), cur, voff_a, kb, 1);
+  const char* lut = lds + T::LUT_OFF;
+  if constexpr (GU) {
+    // the SiLU window: one KiB per wave (sign half wave / 4, KiB wave % 4)
+    const __amdgpu_buffer_rsrc_t lut_rsrc = make_rsrc(g_silu_lut, kSiluLutSize * 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        lut_rsrc, (lds_ptr_t)(lds + T::LUT_OFF + wave * 1024), 16, lane * 16,
+        (wave >> 2) * (kSiluLutSize / 2) * 2 + kSiluWinSrc + (wave & 3) * 1024, 0, 0);
+  }
+  f6_issue<GU>(st(0), cur, voff_a, kb, 0);
+  f6_issue<GU>(st(1), cur, voff_a, kb, 1);
   wait_vmcnt<0>();
   f6_lds_barrier();
   int rot = 0;  // ring position of the tile's k-step 0
@@ -426,7 +602,7 @@ __global__ __launch_bounds__(F6Tile::THREADS) void gemm_f6_kernel(
     const bool has_next = t_next < total;
     const F6Tiles nxt = tile(has_next ? t_next : t);  // the last tile re-reads its own
     scales.row0 = cur.m0 + wm * T::WM;
-    scales.col0 = cur.n0 + wn * T::WN;
+    scales.col0 = cur.n0 + wn * (GU ? T::WN / 2 : T::WN);
 #pragma unroll
     for (int i = 0; i < T::TM; ++i)
 #pragma unroll
@@ -443,10 +619,16 @@ __global__ __launch_bounds__(F6Tile::THREADS) void gemm_f6_kernel(
       auto step = [&](const char* rd, char* nx, int kt, auto scales_tag) {
         // The scales (k-step 0) before the stage DMA, so that the DMA group
         // is the last one issued (the wait below counts on it).
-        if constexpr (decltype(scales_tag)::value) f6_issue_scales(scl, scales);
+        if constexpr (decltype(scales_tag)::value) f6_issue_scales<GU>(scl, scales, ws2);
         __builtin_amdgcn_sched_barrier(0);
         const bool own = kt + 2 < kb;
-        f6_compute(acc, rd, o, a_base, b_base, nx, own ? cur : nxt, voff_a, kb, own ? kt + 2 : kt + 2 - kb);
+        // the DMA's tile, selected field by field (scalar selects; a select
+        // of the whole struct would go through scratch memory)
+        F6Tiles src;
+        src.a_rsrc = own ? cur.a_rsrc : nxt.a_rsrc;
+        src.b_rsrc = own ? cur.b_rsrc : nxt.b_rsrc;
+        src.b_rsrc2 = own ? cur.b_rsrc2 : nxt.b_rsrc2;
+        f6_compute<GU>(acc, rd, o, a_base, b_base, nx, src, voff_a, kb, own ? kt + 2 : kt + 2 - kb, b_step);
         __builtin_amdgcn_sched_barrier(0);
         // k-step kt + 1 has landed once at most the DMA issued here is
         // outstanding (vector memory operations complete in issue order; at
@@ -465,7 +647,10 @@ __global__ __launch_bounds__(F6Tile::THREADS) void gemm_f6_kernel(
     // the next tile's k-steps 0 and 1 and this tile's scales have landed
     wait_vmcnt<0>();
     char* staging = st((rot + kb - 1) % 3) + wave * T::EPI_WAVE;
-    f6_epilogue<RESID>(acc, kb * 128, M, N, cur.m0, cur.n0, residual, out, staging, sc);
+    if constexpr (GU)
+      f6_epilogue_gu(acc, kb * 128, M, N, cur.m0, cur.n0, out, staging, sc, lut);
+    else
+      f6_epilogue<RESID>(acc, kb * 128, M, N, cur.m0, cur.n0, residual, out, staging, sc);
     if (!has_next) break;
     // every wave is done with the staging stage before k-step 0 of the next
     // tile loads k-step 2 into it
@@ -478,25 +663,29 @@ __global__ __launch_bounds__(F6Tile::THREADS) void gemm_f6_kernel(
 #endif
 }
 
-template <bool RESID>
+// GU: w / ws the gate weight, w2 / ws2 the up weight, n the width of h
+// (n % 128 == 0), out = h.
+template <bool RESID, bool GU = false>
 hipError_t launch_gemm_f6_impl(const uint8_t* a, const float* as, const uint8_t* w, const float* ws, int64_t m, int n,
-                               int k, const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+                               int k, const uint16_t* residual, uint16_t* out, hipStream_t stream,
+                               const uint8_t* w2 = nullptr, const float* ws2 = nullptr) {
   using T = F6Tile;
-  static_assert(T::LDS <= 160 * 1024, "LDS per workgroup");
+  constexpr int lds = GU ? T::LDS_GU : T::LDS;
+  static_assert(lds <= 160 * 1024, "LDS per workgroup");
   static LaunchCache cache;
-  const void* kern = reinterpret_cast<const void*>(&gemm_f6_kernel<RESID>);
-  if (hipError_t e = ensure_dynamic_lds(cache, kern, T::LDS)) return e;
+  const void* kern = reinterpret_cast<const void*>(&gemm_f6_kernel<RESID, GU>);
+  if (hipError_t e = ensure_dynamic_lds(cache, kern, lds)) return e;
   int per_cu = 0, cus = 0;
-  if (hipError_t e = resident_per_cu(cache, kern, T::THREADS, T::LDS, per_cu, cus)) return e;
-  const int tiles_n = n / T::BN;
+  if (hipError_t e = resident_per_cu(cache, kern, T::THREADS, lds, per_cu, cus)) return e;
+  const int tiles_n = n / (GU ? T::BN / 2 : T::BN);
   const int64_t tiles_m = (m + T::BM - 1) / T::BM;
   const int64_t total = tiles_m * tiles_n;
   if (total > kMaxTiles) return hipErrorInvalidValue;  // the kernel's 32-bit tile indices
   int64_t grid = (int64_t)cus * per_cu / 8 * 8;
   if (grid < 8) grid = 8;
   if (grid > total) grid = total;
-  gemm_f6_kernel<RESID><<<(unsigned)grid, T::THREADS, T::LDS, stream>>>(a, k * 3 / 4, as, w, ws, m, n, k / 128,
-                                                                        residual, out, (int)tiles_m, tiles_n);
+  gemm_f6_kernel<RESID, GU><<<(unsigned)grid, T::THREADS, lds, stream>>>(
+      a, k * 3 / 4, as, w, ws, m, n, k / 128, residual, out, (int)tiles_m, tiles_n, w2, ws2);
   return hipGetLastError();
 }
 
@@ -522,6 +711,10 @@ hipError_t launch_gemm_f6(const uint8_t* a, const float* as, const uint8_t* w, c
   return launch_gemm_f6_impl<false>(a, as, w, ws, m, n, k, residual, out, stream);
 }
 
-}  // namespace clef
+hipError_t launch_gemm_f6_gate_up(const uint8_t* a, const float* as, const uint8_t* gate_w, const float* gate_s,
+                                  const uint8_t* up_w, const float* up_s, int64_t m, int n, int k, uint16_t* h,
+                                  hipStream_t stream) {
+  return launch_gemm_f6_impl<false, true>(a, as, gate_w, gate_s, m, n, k, nullptr, h, stream, up_w, up_s);
+}
 
-// The grouped expert GEMM on bf6 operands (uses the helpers above).
+}  // namespace clef

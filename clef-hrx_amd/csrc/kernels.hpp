@@ -47,6 +47,10 @@ hipError_t launch_f6_rows(const uint32_t* a, int a_words, int64_t rows, int k, u
 hipError_t launch_f6_tiled(const uint32_t* w_tiled, int64_t n, int k, uint8_t* out, hipStream_t stream);
 hipError_t launch_gemm_f6(const uint8_t* a, const float* as, const uint8_t* w, const float* ws, int64_t m, int n,
                           int k, const uint16_t* residual, uint16_t* out, hipStream_t stream);
+// Gate and up projections with SwiGLU on the bf6 forms: h [m][n] (n % 128 == 0).
+hipError_t launch_gemm_f6_gate_up(const uint8_t* a, const float* as, const uint8_t* gate_w, const float* gate_s,
+                                  const uint8_t* up_w, const float* up_s, int64_t m, int n, int k, uint16_t* h,
+                                  hipStream_t stream);
 // Records msg as clef_last_error() of this thread; returns CLEF_EINVAL.
 int set_last_error(const char* msg);
 // G1 tile configurations (clef_i4_gemm_config): 128x128 tiles, 256x256

@@ -231,6 +231,22 @@ int clef_i4_gemm_f6(const uint8_t* a_f6, const float* a_scales, const uint8_t* w
                     int64_t m, int32_t n, int32_t k, const uint16_t* residual, uint16_t* out,
                     clef_stream_t stream);
 
+/* The dense MLP's gate and up projections with SwiGLU in one GEMM on the bf6
+ * forms: h[m][n] = S1(G1(a, gate), G1(a, up)) = bf16(silu_bf16(g) * u), g
+ * and u each G1's bf16 output. Replaces the two project_prepared calls and
+ * the SwiGLU step of the reference's dense MLP (src/quantized.rs:399-401
+ * then project_swiglu :406-439, whose fused quantizer rounds the same h to
+ * bf16 before quantizing; kernels/swiglu.loom:43-51): h equals
+ * clef_swiglu(clef_i4_gemm_f6(a, gate), clef_i4_gemm_f6(a, up)) bit for
+ * bit, and clef_i4_prepare_f6(h) equals clef_i4_prepare_swiglu_f6 of those
+ * two outputs. Reads the activation tile once for both projections and
+ * writes h instead of gate and up. Preconditions: those of clef_i4_gemm_f6
+ * with n % 128 == 0 (gate and up weights both [n][k], bf6 tiled) ->
+ * "unsupported integer projection shape"; 16-byte aligned pointers. */
+int clef_i4_gemm_f6_gate_up(const uint8_t* a_f6, const float* a_scales, const uint8_t* gate_f6,
+                            const float* gate_scales, const uint8_t* up_f6, const float* up_scales, int64_t m,
+                            int32_t n, int32_t k, uint16_t* h, clef_stream_t stream);
+
 /* Bytes of scratch clef_i4_project needs (the packed activation). */
 size_t clef_i4_project_workspace_bytes(int64_t m, int32_t k);
 

@@ -150,6 +150,12 @@ def test_dense_mlp_full_shape():
     assert torch.equal(u6.view(torch.int16), up.view(torch.int16)), "bf6 mlp up"
     y6 = clef_i4.project_f6(clef_i4.prepare_swiglu_f6(g6, u6), clef_i4.f6_weight(wd))
     assert torch.equal(y6.view(torch.int16), y.view(torch.int16)), "bf6 mlp down"
+    # the fused gate/up + SwiGLU GEMM (the benchmark's block): h bit for bit
+    # the SwiGLU of the separate projections, and the block output unchanged
+    hf = clef_i4.project_gate_up_f6(af, clef_i4.f6_weight(wg), clef_i4.f6_weight(wu))
+    assert torch.equal(hf.view(torch.int16), clef_i4.swiglu(gate, up).view(torch.int16)), "fused gate/up h"
+    yf = clef_i4.project_f6(clef_i4.prepare_f6(hf), clef_i4.f6_weight(wd))
+    assert torch.equal(yf.view(torch.int16), y.view(torch.int16)), "fused mlp down"
 
 
 def skewed_logits(tokens: int, seed: int) -> torch.Tensor:

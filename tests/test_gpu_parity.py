@@ -1028,6 +1028,83 @@ def test_project_f6_matches_oracle(m, n, k, resid):
     assert_same_u16(bf16_host(got), want, f"project_f6 m={m} n={n} k={k} resid={resid}")
 
 
+# ---------------------------------------------------------------- fused gate/up (bf6)
+
+def _gate_up_operands(rng, m, n, k, gate_row_scale=None):
+    x = randn_bf16(rng, (m, k))
+    wg = randn_bf16(rng, (n, k), std=0.02)
+    wu = randn_bf16(rng, (n, k), std=0.02)
+    if gate_row_scale is not None:  # per-row multipliers of the gate weight
+        wg = oracle.f32_to_bf16(oracle.bf16_to_f32(wg) * gate_row_scale[:, None].astype(np.float32))
+    return x, wg, wu
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 128, 256), (300, 384, 512), (257, 256, 2048), (512, 1152, 4096),
+                                   (96, 768, 1024)])
+def test_gemm_f6_gate_up_matches_oracle(m, n, k):
+    """h = S1(G1(gate), G1(up)) in one bf6 GEMM against the oracle's two
+    projections and S1, and, where the separate bf6 GEMM takes the width
+    (n % 256 == 0), bit-equal to the unfused library path (two bf6 GEMMs, then
+    clef_swiglu); ragged m and h widths of 1, 2, 3, 6 and 9 panels."""
+    rng = np.random.default_rng(31 * m + n + k)
+    x, wg, wu = _gate_up_operands(rng, m, n, k)
+    stride = oracle.activation_stride(k)
+    a_codes, a_scales, _ = oracle.prepare(x, stride)
+    g_tiled, g_scales = oracle.pack_weight(wg)
+    u_tiled, u_scales = oracle.pack_weight(wu)
+    want = oracle.swiglu(oracle.gemm(a_codes, a_scales, g_tiled, g_scales, n, k),
+                         oracle.gemm(a_codes, a_scales, u_tiled, u_scales, n, k))
+    fg = clef_i4.f6_weight(dev_weight(g_tiled, g_scales, n, k))
+    fu = clef_i4.f6_weight(dev_weight(u_tiled, u_scales, n, k))
+    a = clef_i4.prepare_f6(to_dev_bf16(x))
+    got = clef_i4.project_gate_up_f6(a, fg, fu)
+    assert_same_u16(bf16_host(got), want, f"gate_up m={m} n={n} k={k}")
+    if n % 256 == 0:
+        unfused = clef_i4.swiglu(clef_i4.project_f6(a, fg), clef_i4.project_f6(a, fu))
+        assert_same_u16(bf16_host(got), bf16_host(unfused), f"gate_up vs unfused m={m} n={n} k={k}")
+
+
+def test_gemm_f6_gate_up_silu_window_edges():
+    """Gate rows scaled so that g falls below the SiLU table window (|g| <
+    2^-10: the g/2 form), far above it (|g| >= 64: the exact silu), and a NaN
+    and an infinite activation row (the slow epilogue and the exact silu on
+    non-finite g), all bit-equal to the unfused path and to the oracle."""
+    m, n, k = 200, 256, 1024
+    rng = np.random.default_rng(7)
+    row_scale = np.ones(n, dtype=np.float32)
+    row_scale[0:48] = 1e-4      # |g| ~ 1e-4
+    row_scale[48:64] = 1e-6     # |g| ~ 1e-6
+    row_scale[64:96] = 300.0    # |g| ~ 300
+    row_scale[96:100] = 0.0     # g = 0 exactly
+    x, wg, wu = _gate_up_operands(rng, m, n, k, gate_row_scale=row_scale)
+    x[5, :] = 0x7FC0            # NaN row
+    x[9, 3] = 0x7F80            # an infinite value
+    x[11, :] = 0x8000           # -0 row
+    stride = oracle.activation_stride(k)
+    a_codes, a_scales, _ = oracle.prepare(x, stride)
+    g_tiled, g_scales = oracle.pack_weight(wg)
+    u_tiled, u_scales = oracle.pack_weight(wu)
+    gate = oracle.gemm(a_codes, a_scales, g_tiled, g_scales, n, k)
+    gf = np.abs(oracle.bf16_to_f32(gate[np.isfinite(oracle.bf16_to_f32(gate))]))
+    assert (gf[gf > 0] < 2.0 ** -10).any() and (gf >= 64).any(), "the case must reach both sides of the window"
+    want = oracle.swiglu(gate, oracle.gemm(a_codes, a_scales, u_tiled, u_scales, n, k))
+    fg = clef_i4.f6_weight(dev_weight(g_tiled, g_scales, n, k))
+    fu = clef_i4.f6_weight(dev_weight(u_tiled, u_scales, n, k))
+    a = clef_i4.prepare_f6(to_dev_bf16(x))
+    got = clef_i4.project_gate_up_f6(a, fg, fu)
+    unfused = clef_i4.swiglu(clef_i4.project_f6(a, fg), clef_i4.project_f6(a, fu))
+    assert_same_u16(bf16_host(got), bf16_host(unfused), "gate_up window edges vs unfused")
+    assert_same_u16(bf16_host(got), want, "gate_up window edges vs oracle")
+
+
+def test_gemm_f6_gate_up_rejects():
+    fw = clef_i4.F6Weight(torch.zeros(192 * 256 * 3 // 4, dtype=torch.uint8, device="cuda"),
+                          torch.ones(192, device="cuda"), 192, 256)
+    a = clef_i4.prepare_f6(torch.zeros((4, 256), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(clef_i4.ClefError, match="unsupported integer projection shape"):
+        clef_i4.project_gate_up_f6(a, fw, fw)  # 192 columns: not whole 128-column panels
+
+
 # ---------------------------------------------------------------- decode-sized G1
 # Configuration 4: v_dot8_i32_i4 on the packed codes for m <= 8.
 

@@ -872,3 +872,26 @@ def test_moe_layer_closed_form():
     want, gates = moe_closed_form(c, routes, wg, wu, wd, d, inter, topk)
     assert np.all(gates >= 17.0)
     assert np.array_equal(F(got), want)
+
+
+def test_silu_is_half_below_the_table_window():
+    """For every bf16 g with exponent field 2..116 (2^-125 <= |g| < 2^-10),
+    both signs, S1 with u = 1 gives g / 2 exactly (g's exponent field minus
+    one), and +-0 gives +-0: the closed form the fused gate/up epilogue uses
+    below its SiLU table window. Also pins where it stops holding: exponent
+    field 119 has values where it fails, so the window's lower edge (117)
+    keeps a margin."""
+    e = np.arange(2, 117, dtype=np.uint32)
+    mant = np.arange(128, dtype=np.uint32)
+    mag = ((e[:, None] << 7) | mant[None, :]).ravel()
+    g = np.concatenate([mag, mag | 0x8000, np.array([0, 0x8000], dtype=np.uint32)]).astype(np.uint16)
+    ones = np.full(g.shape, 0x3F80, dtype=np.uint16)
+    got = oracle.swiglu(g.reshape(1, -1), ones.reshape(1, -1)).ravel()
+    want = g.copy()
+    nz = (g & 0x7FFF) != 0
+    want[nz] = g[nz] - 0x80
+    assert np.array_equal(got, want)
+    e119 = ((np.uint32(119) << 7) | mant).astype(np.uint16)
+    half119 = e119 - np.uint16(0x80)
+    assert not np.array_equal(oracle.swiglu(e119.reshape(1, -1), np.full((1, 128), 0x3F80, np.uint16)).ravel(),
+                              half119)
