@@ -99,34 +99,43 @@ __device__ __forceinline__ void dense_epilogue(const v16i (&acc)[T::TM][T::TN], 
     const int blk = (col >> 2) ^ (row & 15);
     *reinterpret_cast<uint2*>(tile + row * RP + blk * 8) = make_uint2(p0, p1);
   };
+  // one copy of the loops per path (a wave-uniform flag tested inside them
+  // is re-tested per value, a scheduling barrier each time)
+  auto values = [&](auto fast_tag) {
+    constexpr bool FAST = decltype(fast_tag)::value;
 #pragma unroll
-  for (int i = 0; i < T::TM; ++i) {
-    const float asv = asr[i];
+    for (int i = 0; i < T::TM; ++i) {
+      const float asv = asr[i];
 #pragma unroll
-    for (int j = 0; j < T::TN; ++j)
+      for (int j = 0; j < T::TN; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int row = 32 * i + lr, col = 32 * j + 8 * q + 4 * h;
-        const float4 wsv = wsr[j][q];
-        uint32_t p0, p1;
-        if (fast) {
-          const float w4[4] = {wsv.x, wsv.y, wsv.z, wsv.w};
-          float y[4];
+        for (int q = 0; q < 4; ++q) {
+          const int row = 32 * i + lr, col = 32 * j + 8 * q + 4 * h;
+          const float4 wsv = wsr[j][q];
+          uint32_t p0, p1;
+          if constexpr (FAST) {
+            const float w4[4] = {wsv.x, wsv.y, wsv.z, wsv.w};
+            float y[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            y[e] = (float)acc[i][j][4 * q + e] * (w4[e] * kUnshift);
-            y[e] = y[e] * asv;
-            y[e] = y[e] + 0.0f;
+            for (int e = 0; e < 4; ++e) {
+              y[e] = (float)acc[i][j][4 * q + e] * (w4[e] * kUnshift);
+              y[e] = y[e] * asv;
+              y[e] = y[e] + 0.0f;
+            }
+            p0 = pack_bf16x2(y[0], y[1]);
+            p1 = pack_bf16x2(y[2], y[3]);
+          } else {
+            p0 = g1_value<SHIFT>(acc[i][j][4 * q + 0], wsv.x, asv) | (g1_value<SHIFT>(acc[i][j][4 * q + 1], wsv.y, asv) << 16);
+            p1 = g1_value<SHIFT>(acc[i][j][4 * q + 2], wsv.z, asv) | (g1_value<SHIFT>(acc[i][j][4 * q + 3], wsv.w, asv) << 16);
           }
-          p0 = pack_bf16x2(y[0], y[1]);
-          p1 = pack_bf16x2(y[2], y[3]);
-        } else {
-          p0 = g1_value<SHIFT>(acc[i][j][4 * q + 0], wsv.x, asv) | (g1_value<SHIFT>(acc[i][j][4 * q + 1], wsv.y, asv) << 16);
-          p1 = g1_value<SHIFT>(acc[i][j][4 * q + 2], wsv.z, asv) | (g1_value<SHIFT>(acc[i][j][4 * q + 3], wsv.w, asv) << 16);
+          stage(row, col, p0, p1);
         }
-        stage(row, col, p0, p1);
-      }
-  }
+    }
+  };
+  if (fast)
+    values(std::true_type{});
+  else
+    values(std::false_type{});
   // Each wave reads back only its own region; the LDS ops of a wave complete
   // in order, so no barrier is needed between the two phases.
   const int c = lane % LPR;
@@ -345,48 +354,57 @@ __device__ __forceinline__ void staged_epilogue_store(const v16i (&acc)[T::TM][T
   const int lrow = lane / kLanesPerRow, lchunk = lane % kLanesPerRow;
   int voff = ((wm * T::WM + lrow) * N + n0 + wn * T::WN + 8 * lchunk) * 2;
   asm volatile("" : "+v"(voff));
+  // one copy of the loops per path: a wave-uniform flag tested inside them
+  // is re-tested per value, and each test is a scheduling barrier
+  auto values = [&](auto fast_tag) {
+    constexpr bool FAST = decltype(fast_tag)::value;
 #pragma unroll
-  for (int i = 0; i < T::TM; ++i) {
-    const float asv = e.asr[i];
+    for (int i = 0; i < T::TM; ++i) {
+      const float asv = e.asr[i];
 #pragma unroll
-    for (int j = 0; j < T::TN; ++j)
+      for (int j = 0; j < T::TN; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 wsv = e.wsr[j][q];
-        uint32_t p0, p1;
-        if (e.fast) {
-          const float w4[4] = {wsv.x, wsv.y, wsv.z, wsv.w};
-          float y[4];
+        for (int q = 0; q < 4; ++q) {
+          const float4 wsv = e.wsr[j][q];
+          uint32_t p0, p1;
+          if constexpr (FAST) {
+            const float w4[4] = {wsv.x, wsv.y, wsv.z, wsv.w};
+            float y[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              y[t] = (float)acc[i][j][4 * q + t] * w4[t];
+              y[t] = y[t] * asv;
+            }
+            p0 = pack_bf16x2(y[0], y[1]);
+            p1 = pack_bf16x2(y[2], y[3]);
+          } else {
+            p0 = g1_value(acc[i][j][4 * q + 0], wsv.x, asv) | (g1_value(acc[i][j][4 * q + 1], wsv.y, asv) << 16);
+            p1 = g1_value(acc[i][j][4 * q + 2], wsv.z, asv) | (g1_value(acc[i][j][4 * q + 3], wsv.w, asv) << 16);
+          }
+          const int chunk = 4 * j + q;  // 16-byte chunk of the row: columns 8 * chunk .. + 7
+          *reinterpret_cast<v2u*>(wlds + lr * kRowBytes + ((chunk ^ (lr & 7)) << 4) + 8 * h) = v2u{p0, p1};
+        }
+#pragma unroll
+      for (int r = 0; r < kReads; ++r) {
+        const int row = kRowsPerRead * r + lrow, chunk = lchunk;
+        v4u v = *reinterpret_cast<const v4u*>(wlds + row * kRowBytes + ((chunk ^ (row & 7)) << 4));
+        const int soff = (32 * i + kRowsPerRead * r) * N * 2;
+        if (RESID) {
+          const v4i rv = __builtin_amdgcn_raw_buffer_load_b128(res_rsrc, voff, soff, 0);
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            y[t] = (float)acc[i][j][4 * q + t] * w4[t];
-            y[t] = y[t] * asv;
+            const uint32_t p = v[t], rr = (uint32_t)rv[t];
+            v[t] = pack_bf16x2(bf16_lo(rr) + bf16_lo(p), bf16_hi(rr) + bf16_hi(p));
           }
-          p0 = pack_bf16x2(y[0], y[1]);
-          p1 = pack_bf16x2(y[2], y[3]);
-        } else {
-          p0 = g1_value(acc[i][j][4 * q + 0], wsv.x, asv) | (g1_value(acc[i][j][4 * q + 1], wsv.y, asv) << 16);
-          p1 = g1_value(acc[i][j][4 * q + 2], wsv.z, asv) | (g1_value(acc[i][j][4 * q + 3], wsv.w, asv) << 16);
         }
-        const int chunk = 4 * j + q;  // 16-byte chunk of the row: columns 8 * chunk .. + 7
-        *reinterpret_cast<v2u*>(wlds + lr * kRowBytes + ((chunk ^ (lr & 7)) << 4) + 8 * h) = v2u{p0, p1};
+        store_b128(out_rsrc, voff + soff, v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]});
       }
-#pragma unroll
-    for (int r = 0; r < kReads; ++r) {
-      const int row = kRowsPerRead * r + lrow, chunk = lchunk;
-      v4u v = *reinterpret_cast<const v4u*>(wlds + row * kRowBytes + ((chunk ^ (row & 7)) << 4));
-      const int soff = (32 * i + kRowsPerRead * r) * N * 2;
-      if (RESID) {
-        const v4i rv = __builtin_amdgcn_raw_buffer_load_b128(res_rsrc, voff, soff, 0);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const uint32_t p = v[t], rr = (uint32_t)rv[t];
-          v[t] = pack_bf16x2(bf16_lo(rr) + bf16_lo(p), bf16_hi(rr) + bf16_hi(p));
-        }
-      }
-      store_b128(out_rsrc, voff + soff, v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]});
     }
-  }
+  };
+  if (e.fast)
+    values(std::true_type{});
+  else
+    values(std::false_type{});
 }
 
 // Last k-step of one tile and first k-step of the next, in one inlined body
