@@ -670,8 +670,14 @@ def main():
                                 "roofline_us": round(max(m["ops"] / INT8_PEAK_TOPS / 1e6,
                                                          m["bytes"] / HBM_PEAK_GBS / 1e3), 1),
                                 "hbm_gbs": round(m["bytes"] / m["ms"] / 1e6, 1),
-                                "algorithmic_bytes": m["bytes"], "traffic": MOE_TRAFFIC_BYTES,
-                                "traffic_source": "profiles/omni_int4_moe_t4096.txt (FETCH_SIZE, WRITE_SIZE)"}
+                                "algorithmic_bytes": m["bytes"]}
+        # The counter readings were taken at 4096 tokens; other token counts
+        # carry no traffic figure here.
+        if m["tokens"] == 4096:
+            line["moe_roofline"].update({"traffic": MOE_TRAFFIC_BYTES,
+                                         "traffic_source": "profiles/omni_int4_moe_t4096.txt (FETCH_SIZE, WRITE_SIZE)"})
+        else:
+            line["moe_roofline"]["traffic"] = None
     if "mlp" in res:
         line["mlp_block_ms"] = round(res["mlp"]["ms"], 4)
         line["mlp_tops"] = round(res["mlp"]["tops"], 1)
