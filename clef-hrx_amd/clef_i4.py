@@ -494,20 +494,33 @@ def f6_weight(w: QuantizedWeight) -> F6Weight:
     return F6Weight(codes, w.scales, w.rows, w.cols)
 
 
+def f6_codes_bytes(rows: int, width: int) -> int:
+    """Bytes of bf6 activation codes (clef_i4_f6_activation's layout): 128-row
+    blocks, the last one padded."""
+    return (rows + 127) // 128 * 128 * width * 3 // 4
+
+
 def f6_activation(a: Prepared, out: torch.Tensor | None = None) -> torch.Tensor:
-    """bf6 rows [rows][width * 3/4] of a 4-bit prepared activation."""
+    """The bf6 activation codes (uint8 [f6_codes_bytes(rows, width)], blocks
+    of 128 rows x 128 k) of a 4-bit prepared activation."""
     if a.bits != 4:
         raise ClefError(-1, "unsupported integer projection shape")
+    nbytes = f6_codes_bytes(a.rows, a.width)
     if out is None:
-        out = torch.empty((a.rows, a.width * 3 // 4), dtype=torch.uint8, device=a.storage.device)
+        out = torch.empty(nbytes, dtype=torch.uint8, device=a.storage.device)
+    elif out.dtype != torch.uint8 or out.numel() < nbytes:
+        raise ClefError(-1, "bf6 activation buffer too small")
     _check(lib().clef_i4_f6_activation(_ptr(a.storage), a.stride, a.rows, a.width, _ptr(out), _stream()))
     return out
 
 
 def gemm_f6(a_f6: torch.Tensor, a_scales: torch.Tensor, w: F6Weight, residual: torch.Tensor | None = None,
             out: torch.Tensor | None = None) -> torch.Tensor:
-    """G1 on bf6 operands: equal to project_prepared on the operands they came from."""
-    rows = a_f6.shape[0]
+    """G1 on bf6 operands: equal to project_prepared on the operands they came
+    from. The rows are those of a_scales (one f32 scale per row)."""
+    rows = a_scales.numel()
+    if a_f6.numel() < f6_codes_bytes(rows, w.cols):
+        raise ClefError(-1, "bf6 activation buffer too small")
     if out is None:
         out = _empty((rows, w.rows), torch.bfloat16, a_f6.device)
     _check(lib().clef_i4_gemm_f6(_ptr(a_f6), _ptr(a_scales), _ptr(w.codes), _ptr(w.scales), rows, w.rows, w.cols,
@@ -518,18 +531,19 @@ def gemm_f6(a_f6: torch.Tensor, a_scales: torch.Tensor, w: F6Weight, residual: t
 @dataclass
 class PreparedF6:
     """Q1 output in bf6 form (clef_i4_prepare_f6): one uint8 buffer holding
-    rows x width*3/4 bytes of e3m2 codes, then rows f32 scales."""
-    storage: torch.Tensor  # uint8 [rows * (width * 3/4 + 4)]
+    the e3m2 codes in the bf6 activation layout (f6_codes_bytes), then rows
+    f32 scales."""
+    storage: torch.Tensor  # uint8 [f6_codes_bytes(rows, width) + 4 * rows]
     rows: int
     width: int
 
     @property
     def codes(self) -> torch.Tensor:
-        return self.storage[: self.rows * self.width * 3 // 4].view(self.rows, self.width * 3 // 4)
+        return self.storage[: f6_codes_bytes(self.rows, self.width)]
 
     @property
     def scales(self) -> torch.Tensor:
-        start = self.rows * self.width * 3 // 4
+        start = f6_codes_bytes(self.rows, self.width)
         return self.storage[start: start + 4 * self.rows].view(torch.float32)
 
 

@@ -9,6 +9,18 @@
 
 namespace clef {
 
+// bf6 activation layout (this library's own, the bf6 weight's block shape
+// without its swizzle): blocks of 128 rows x 128 k, each 12 KiB of 96-byte
+// rows (value k of a row at bits 6k of its 96 bytes, little-endian), block
+// (r / 128, k / 128) at byte ((r / 128) * (K / 128) + k / 128) * 12288, row
+// r % 128 of a block at (r % 128) * 96. Rows of the last block past `rows`
+// are padding that no kernel writes and the GEMMs never store. The f32 row
+// scales of a prepared buffer follow the codes.
+constexpr int64_t f6_codes_bytes(int64_t rows, int64_t width) { return (rows + 127) / 128 * 128 * width * 3 / 4; }
+constexpr int64_t f6_offset(int64_t row, int64_t col, int64_t width) {
+  return ((row >> 7) * (width >> 7) + (col >> 7)) * 12288 + (row & 127) * 96 + (col & 127) * 3 / 4;
+}
+
 hipError_t launch_prepare(const uint16_t* x, int64_t rows, int width, int stride, int bits,
                           uint32_t* out, hipStream_t stream);
 // The router and the INT4 quantizer of `x` ([tokens][width], stride as

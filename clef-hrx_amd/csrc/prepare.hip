@@ -255,8 +255,7 @@ __device__ __forceinline__ void pack_codes_f6(const float* v, float inv, bool va
 }
 
 // Codes of the 16 values at column col of a row whose output starts at
-// row_out: BITS 4 and 8 pack two's complement fields (32 / BITS per word),
-// BITS 6 writes bf6 (12 bytes at byte col * 3/4).
+// row_out: BITS 4 and 8 pack two's complement fields (32 / BITS per word).
 template <int BITS>
 __device__ __forceinline__ void store_codes(uint32_t* row_out, int col, const float* nat, float inv, bool valid) {
   if constexpr (BITS == 4) {
@@ -267,14 +266,38 @@ __device__ __forceinline__ void store_codes(uint32_t* row_out, int col, const fl
         make_uint4(pack_codes<8>(nat, inv, valid), pack_codes<8>(nat + 4, inv, valid),
                    pack_codes<8>(nat + 8, inv, valid), pack_codes<8>(nat + 12, inv, valid));
   } else {
-    static_assert(BITS == 6, "codes of 4 or 8 bits, or bf6");
-    uint32_t o[3];
-    pack_codes_f6(nat, inv, valid, o);
-    uint32_t* dst = row_out + col * 3 / 16;
-    dst[0] = o[0];
-    dst[1] = o[1];
-    dst[2] = o[2];
+    static_assert(BITS == 8, "codes of 4 or 8 bits (bf6: store_codes_f6)");
   }
+}
+
+// bf6 codes of the 16 values at column col of row `row`: 12 bytes in the
+// tiled bf6 activation layout (f6_offset).
+__device__ __forceinline__ void store_codes_f6(uint32_t* out, int64_t row, int col, int width, const float* nat,
+                                               float inv, bool valid) {
+  uint32_t o[3];
+  pack_codes_f6(nat, inv, valid, o);
+  uint32_t* dst = out + f6_offset(row, col, width) / 4;
+  dst[0] = o[0];
+  dst[1] = o[1];
+  dst[2] = o[2];
+}
+
+// Codes of one 16-value group, in the output layout of BITS (out_row: the
+// row's first word for BITS 4 and 8; out: the whole buffer for bf6).
+template <int BITS>
+__device__ __forceinline__ void store_group(uint32_t* out, uint32_t* out_row, int64_t row, int col, int width,
+                                            const float* nat, float inv, bool valid) {
+  if constexpr (BITS == 6)
+    store_codes_f6(out, row, col, width, nat, inv, valid);
+  else
+    store_codes<BITS>(out_row, col, nat, inv, valid);
+}
+
+// Where a prepared buffer's f32 row scales start.
+template <int BITS>
+__device__ __forceinline__ float* scales_of(uint32_t* out, int64_t rows, int width, int out_words) {
+  if constexpr (BITS == 6) return reinterpret_cast<float*>(reinterpret_cast<char*>(out) + f6_codes_bytes(rows, width));
+  return reinterpret_cast<float*>(out + rows * out_words);
 }
 
 template <int P, int BITS, class Src>
@@ -407,12 +430,9 @@ __global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int
       nat[4 * c + 3] = t.w;
     }
     __syncthreads();
-    if (on) store_codes<BITS>(out + row * out_words, grp * 256 + 16 * L, nat, inv, valid);
+    if (on) store_group<BITS>(out, out + row * out_words, row, grp * 256 + 16 * L, width, nat, inv, valid);
   }
-  if (active && grp0 == 0 && L == 0) {
-    float* scales = reinterpret_cast<float*>(out + rows * out_words);
-    scales[row] = scale;
-  }
+  if (active && grp0 == 0 && L == 0) scales_of<BITS>(out, rows, width, out_words)[row] = scale;
 }
 
 // Rows of G <= 16 groups, as prepare_kernel<1> but persistent: a workgroup
@@ -516,8 +536,8 @@ __device__ __forceinline__ void prepare_loop_body(Src src, int64_t rows, int wid
     }
     __syncthreads();
     if (on) {
-      store_codes<BITS>(out + out_off, col, nat, inv, valid);
-      if (grp == 0 && L == 0) reinterpret_cast<float*>(out + rows * out_words)[row] = scale;
+      store_group<BITS>(out, out + out_off, row, col, width, nat, inv, valid);
+      if (grp == 0 && L == 0) scales_of<BITS>(out, rows, width, out_words)[row] = scale;
     }
   }
 }
@@ -587,8 +607,8 @@ hipError_t launch_prepare_bits(const Src& src, int64_t rows, int width, int out_
   return hipGetLastError();
 }
 
-// bits 4 or 8: packed codes of `stride` columns per row; bits 6: bf6 rows of
-// width * 3/4 bytes (stride == width).
+// bits 4 or 8: packed codes of `stride` columns per row; bits 6: the tiled
+// bf6 activation layout (f6_offset; stride == width).
 template <class Src>
 hipError_t launch_prepare_src(const Src& src, int64_t rows, int width, int stride, int bits,
                               uint32_t* out, hipStream_t stream) {

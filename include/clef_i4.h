@@ -199,20 +199,24 @@ int clef_i4_gemm_configs(void);
  * clef_i4_gemm returns for the operands they were made from, with no
  * unpacking in the GEMM and twice the int8 MFMA's k per instruction.
  * - clef_i4_f6_activation: packed activation codes (as clef_i4_gemm's `a`,
- *   row pitch k_stride/8 words) -> bf6 rows: value k of a row at bits 6k of
- *   the row's k*3/4 bytes. Preconditions: rows >= 1, k % 128 == 0,
- *   k_stride >= k, k_stride % 32 == 0 -> "unsupported integer projection
- *   shape"; 16-byte aligned pointers.
+ *   row pitch k_stride/8 words) -> the bf6 activation layout: blocks of 128
+ *   rows x 128 k (12 KiB of 96-byte rows; value k of a row at bits 6k of
+ *   its 96 bytes) at ((row/128)*(k/128) + k/128)*12288, row r % 128 of a
+ *   block at (r % 128)*96; rows past `rows` in the last block are padding
+ *   (not written): ceil(rows/128)*128*k*3/4 bytes. Preconditions: rows >= 1,
+ *   k % 128 == 0, k_stride >= k, k_stride % 32 == 0 -> "unsupported integer
+ *   projection shape"; 16-byte aligned pointers.
  * - clef_i4_f6_weight: tiled weight codes (clef_i4_retile, bits 4, [n][k])
  *   -> bf6 tiled weight: 128-row x 128-k blocks of 96-byte rows (12 KiB) at
  *   ((row/128)*(k/128) + k/128)*12288, the 16-byte chunk c of block row r
  *   stored at chunk c ^ ((r >> 3) & 1); n*k*3/4 bytes. Preconditions:
  *   n % 128 == 0, k % 256 == 0 -> "unsupported integer projection shape".
  * - clef_i4_prepare_f6 / clef_i4_prepare_swiglu_f6: Q1 (as clef_i4_prepare /
- *   clef_i4_prepare_swiglu with bits 4) writing the codes as bf6 rows
- *   directly: rows * width*3/4 bytes of codes, then rows f32 scales (at byte
- *   rows * width*3/4); clef_i4_f6_prepared_bytes gives the size. Same codes
- *   and scales as clef_i4_prepare then clef_i4_f6_activation, in one pass.
+ *   clef_i4_prepare_swiglu with bits 4) writing the codes in the bf6
+ *   activation layout directly: ceil(rows/128)*128*width*3/4 bytes of codes,
+ *   then rows f32 scales (at that byte); clef_i4_f6_prepared_bytes gives the
+ *   size. Same codes and scales as clef_i4_prepare then
+ *   clef_i4_f6_activation, in one pass.
  *   Preconditions as clef_i4_prepare (width % 256 == 0, 256 <= width <=
  *   32768, 1 <= rows <= 2^20 -> "unsupported rotated integer operand").
  * - clef_i4_gemm_f6: G1 on them, with clef_i4_gemm's epilogue and residual.

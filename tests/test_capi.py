@@ -343,6 +343,17 @@ def test_gemm_f6_bounds_k_to_quantizer_width(k, ok):
     assert msg == ("device pointer is NULL or not 16-byte aligned" if ok else "unsupported integer projection shape")
 
 
+@pytest.mark.parametrize("rows,width", [(1, 256), (127, 768), (128, 4096), (129, 4096), (4096, 12288)])
+def test_f6_prepared_bytes_pad_rows_to_whole_blocks(rows, width):
+    """A bf6-prepared activation holds its codes in 128-row blocks (the last
+    one padded), then one f32 scale per row; the C ABI's size, the Python
+    helper and the project workspace agree on it."""
+    codes = (rows + 127) // 128 * 128 * width * 3 // 4
+    assert clef_i4.f6_codes_bytes(rows, width) == codes
+    assert clef_i4.lib().clef_i4_f6_prepared_bytes(rows, width) == codes + 4 * rows
+    assert clef_i4.lib().clef_i4_project_f6_workspace_bytes(rows, width) >= codes + 4 * rows
+
+
 @pytest.mark.parametrize("offset", [2, 4, 8])
 def test_router_rejects_logits_not_16_byte_aligned(offset):
     """The router reads each token's logits as 16-byte pieces where the row

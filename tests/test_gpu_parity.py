@@ -852,9 +852,34 @@ def f6_rows_numpy(codes_u32: np.ndarray, k: int) -> np.ndarray:
     return words.reshape(rows, -1).view(np.uint8).reshape(rows, k * 3 // 4)
 
 
+def f6_untile_numpy(buf: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """bf6 rows [rows][k*3/4] of the bf6 activation layout: blocks of 128 rows
+    x 128 k (96-byte rows, 12 KiB) at ((r // 128) * (k // 128) + k // 128) *
+    12288, row r % 128 of a block at (r % 128) * 96; padding rows dropped."""
+    rb = (rows + 127) // 128
+    assert buf.size >= rb * 128 * k * 3 // 4
+    blocks = buf[: rb * 128 * k * 3 // 4].reshape(rb, k // 128, 128, 96)
+    return blocks.transpose(0, 2, 1, 3).reshape(rb * 128, k * 3 // 4)[:rows]
+
+
+def test_f6_untile_numpy_places_blocks():
+    """The layout helper on a buffer whose bytes name their own position:
+    byte j of row r's 96-byte piece of k-block b sits at ((r // 128) * kb + b)
+    * 12288 + (r % 128) * 96 + j."""
+    rows, k = 300, 384
+    kb = k // 128
+    buf = np.arange(3 * 128 * k * 3 // 4, dtype=np.int64)
+    got = f6_untile_numpy(buf, rows, k)
+    for r in (0, 1, 127, 128, 255, 299):
+        for b in range(kb):
+            want = ((r // 128) * kb + b) * 12288 + (r % 128) * 96 + np.arange(96)
+            assert np.array_equal(got[r, 96 * b: 96 * b + 96], want)
+
+
 def test_f6_converters_match_numpy_layout():
-    """Activation rows plainly packed; tiled weight in 12 KiB blocks of 96-byte
-    rows with chunk c of block row r at c ^ ((r >> 3) & 1)."""
+    """Activation in 128-row x 128-k blocks of plainly packed 96-byte rows;
+    tiled weight in the same blocks with chunk c of block row r at
+    c ^ ((r >> 3) & 1)."""
     rng = np.random.default_rng(61)
     m, n, k = 37, 256, 768
     x, w, stride, a_codes, a_scales, w_tiled, w_scales = make_operands(rng, m, n, k)
@@ -863,7 +888,8 @@ def test_f6_converters_match_numpy_layout():
     storage = np.concatenate([a_codes.reshape(-1), a_scales.view(np.uint32)])
     a = clef_i4.Prepared(to_dev_u32(storage), m, k, stride, 4)
     got = clef_i4.f6_activation(a).cpu().numpy()
-    assert np.array_equal(got, f6_rows_numpy(a_codes, k))
+    assert got.size == clef_i4.f6_codes_bytes(m, k) == 128 * k * 3 // 4
+    assert np.array_equal(f6_untile_numpy(got, m, k), f6_rows_numpy(a_codes, k))
     # weight: untile the reference layout to rows, pack, then block + swizzle
     kb4 = k // 256
     rows_u32 = w_tiled.reshape(n // 128, kb4, 128, 32).transpose(0, 2, 1, 3).reshape(n, k // 8)
@@ -969,11 +995,18 @@ def test_gemm_f6_zero_rows_give_positive_zero():
     assert_same_u16(bf16_host(got), want, "gemm_f6 zero rows")
 
 
-def f6_prepared_numpy(codes_u32: np.ndarray, scales: np.ndarray, width: int) -> np.ndarray:
-    """clef_i4_prepare_f6's buffer from the oracle's INT4 codes and scales:
-    bf6 rows, then the f32 scales."""
-    return np.concatenate([f6_rows_numpy(codes_u32, width).reshape(-1),
-                           np.ascontiguousarray(scales, dtype=np.float32).view(np.uint8)])
+def assert_prepared_f6(got, codes_u32: np.ndarray, scales: np.ndarray, what: str):
+    """A PreparedF6 holds the oracle's INT4 codes as bf6 (untiled from the
+    activation layout) and its scales, byte for byte; the buffer is exactly
+    clef_i4_f6_prepared_bytes long."""
+    rows, width = got.rows, got.width
+    buf = got.storage.cpu().numpy()
+    assert buf.size == clef_i4.lib().clef_i4_f6_prepared_bytes(rows, width) == \
+        clef_i4.f6_codes_bytes(rows, width) + 4 * rows, what
+    assert np.array_equal(f6_untile_numpy(buf, rows, width), f6_rows_numpy(codes_u32, width)), what
+    start = clef_i4.f6_codes_bytes(rows, width)
+    assert np.array_equal(buf[start:start + 4 * rows].view(np.uint32),
+                          np.ascontiguousarray(scales, dtype=np.float32).view(np.uint32)), what
 
 
 @pytest.mark.parametrize("width,rows", [(256, 5), (768, 37), (2048, 1000), (4096, 33), (8192, 3), (17408, 7)])
@@ -987,8 +1020,7 @@ def test_prepare_f6_matches_oracle(width, rows):
     stride = oracle.activation_stride(width)
     codes, scales, _ = oracle.prepare(x, stride)
     got = clef_i4.prepare_f6(to_dev_bf16(x))
-    assert np.array_equal(got.storage.cpu().numpy(), f6_prepared_numpy(codes, scales, width)), \
-        f"prepare_f6 width={width} rows={rows}"
+    assert_prepared_f6(got, codes, scales, f"prepare_f6 width={width} rows={rows}")
 
 
 @pytest.mark.parametrize("width", [768, 2048, 17408])
@@ -1000,8 +1032,7 @@ def test_prepare_swiglu_f6_matches_oracle(width):
     stride = oracle.activation_stride(width)
     codes, scales, _ = oracle.prepare_swiglu(g, u, stride)
     got = clef_i4.prepare_swiglu_f6(to_dev_bf16(g), to_dev_bf16(u))
-    assert np.array_equal(got.storage.cpu().numpy(), f6_prepared_numpy(codes, scales, width)), \
-        f"prepare_swiglu_f6 width={width}"
+    assert_prepared_f6(got, codes, scales, f"prepare_swiglu_f6 width={width}")
 
 
 def test_prepare_f6_equals_prepare_then_convert():
