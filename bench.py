@@ -61,7 +61,7 @@ HBM_PEAK_GBS = 8000.0
 # rocprofv3 FETCH_SIZE and WRITE_SIZE passes over `bench.py --only gemm`, each
 # scaled by the reading for a plain 512 MiB copy (x2.000 fetch, x1.000 write);
 # the runs and raw readings are in profiles/int4_gemm_m4096_k4096_n12288.txt.
-GEMM_TRAFFIC_BYTES = 336.73e6
+GEMM_TRAFFIC_BYTES = 332.66e6
 # HBM bytes moved per MoE layer call at 4096 tokens: the same two counter
 # passes over `bench.py --only moe`, summed over the layer's eight kernels
 # (read 628.1 MB + written 235.3 MB; per kernel in
