@@ -1605,6 +1605,122 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
 #endif
 }
 
+// Grouped expert GEMM for schedule tiles of a few routed rows (decode
+// batches: up to 32 tokens, where most experts hold one to three rows), on
+// the VALU as gemm_decode_kernel: v_dot8_i32_i4 multiplies the packed codes
+// as stored, and each load instruction reads 8 whole 128-byte weight rows
+// (expert_skinny_kernel's MFMA layout reads 32 rows per instruction, 32
+// bytes of each). A workgroup of NW waves owns one 32-slot tile and RW
+// output columns of its expert (GU: RW gate and the same RW up columns);
+// wave w takes k-steps w, w + NW, ...; lane l reads 16 bytes (32 k) at
+// k-segment l % 8 of weight rows l / 8 + 8 j and the same segment of each
+// slot's activation row (routed: row = route; else route / topk). The
+// tile's slots are taken MR at a time. Segment sums by DPP and wave sums
+// through LDS (exact integer adds), then expert_skinny_kernel's epilogue on
+// the same integer dots: E1 = bf16(f32(dot) * RN(as * ws)), for GU S1 on the
+// bf16 gate and up values, stored to the slots' routed rows.
+template <bool GU, int NW, int RW, int MR>
+__global__ __launch_bounds__(NW * 64) void expert_decode_kernel(
+    const uint32_t* __restrict__ a, int a_words, uint32_t a_bytes, const float* __restrict__ as,
+    const uint32_t* __restrict__ w, const float* __restrict__ ws, const uint32_t* __restrict__ w2,
+    const float* __restrict__ ws2, const float* __restrict__ groups, const int32_t* __restrict__ schedule,
+    int64_t list_stride, int topk, int kb, int n, int input_routed, uint16_t* __restrict__ out, int slices) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int NA = GU ? 2 : 1, J = RW / 8;
+  static_assert(RW % 8 == 0 && 128 % RW == 0, "decode tile");
+  __shared__ int red[NW][NA][MR][RW];
+  // Every launched item indexes inside the schedule buffer (the launch
+  // covers its largest tile count), so the entry is read with the count.
+  const int64_t item = blockIdx.x;
+  const int tile = (int)(item / slices);
+  const int c0 = (int)(item - (int64_t)tile * slices) * RW;  // first output column within the expert
+  const int tiles = schedule[0];
+  const int e = schedule[kSchedEntries + 2 * tile];
+  const int row0 = schedule[kSchedEntries + 1 + 2 * tile];
+  if (item >= (int64_t)tiles * slices || e < 0) return;  // e >= 0 in every listed tile
+  const float* list = groups + (int64_t)e * list_stride;
+  const int count = (int)list[0];
+  const int row_end = count < row0 + 32 ? count : row0 + 32;  // the tile's slots: row0 .. row_end - 1
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int seg = lane & 7, r8 = lane >> 3;
+  const int64_t nrow = (int64_t)e * n + c0;  // first weight row of the slice (RW rows in one 128-row block)
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(w + (nrow / 128) * kb * 4096, (uint32_t)(kb * 16384));
+  const __amdgpu_buffer_rsrc_t w2_rsrc = make_rsrc((GU ? w2 : w) + (nrow / 128) * kb * 4096, (uint32_t)(kb * 16384));
+  const int w_voff = (int)(nrow % 128 + r8) * 128 + 16 * seg;
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(a, a_bytes);
+  for (int r0 = row0; r0 < row_end; r0 += MR) {
+    // the pass's slots: routes (wave-uniform) and activation row offsets
+    int route[MR], a_off[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      route[m] = r0 + m < row_end ? (int)list[1 + r0 + m] : -1;
+      const int64_t xr = input_routed ? (int64_t)route[m] : (int64_t)route[m] / topk;
+      a_off[m] = route[m] >= 0 ? (int)(xr * a_words * 4) + 16 * seg : (int)0x80000000u;
+    }
+    int acc[NA][J][MR];
+#pragma unroll
+    for (int s = 0; s < NA; ++s)
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[s][j][m] = 0;
+    for (int kt = wave; kt < kb; kt += NW) {
+      v4i wv[NA][J], av[MR];
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        wv[0][j] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff + 1024 * j, kt * 16384, 0);
+        if constexpr (GU) wv[1][j] = __builtin_amdgcn_raw_buffer_load_b128(w2_rsrc, w_voff + 1024 * j, kt * 16384, 0);
+      }
+#pragma unroll
+      for (int m = 0; m < MR; ++m) av[m] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off[m], kt * 128, 0);
+#pragma unroll
+      for (int s = 0; s < NA; ++s)
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+          for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[s][j][m] = __builtin_amdgcn_sdot8(wv[s][j][c], av[m][c], acc[s][j][m], false);
+    }
+    // the 8 segments of each row: lane xor 1 and xor 2 by DPP, xor 4 by a swizzle
+#pragma unroll
+    for (int s = 0; s < NA; ++s)
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          int v = acc[s][j][m];
+          v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+          v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+          v += __builtin_amdgcn_ds_swizzle(v, 0x101F);
+          if (seg == 0) red[wave][s][m][r8 + 8 * j] = v;
+        }
+    __syncthreads();
+    for (int t = threadIdx.x; t < MR * RW; t += NW * 64) {
+      const int m = t / RW, c = t % RW;
+      const int rt = r0 + m < row_end ? (int)list[1 + r0 + m] : -1;
+      if (rt < 0) continue;
+      int dot = 0, dot_u = 0;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        dot += red[q][0][m][c];
+        if constexpr (GU) dot_u += red[q][NA - 1][m][c];
+      }
+      const float asv = as[input_routed ? (int64_t)rt : (int64_t)rt / topk];
+      float y = (float)dot * (asv * ws[nrow + c]);
+      if constexpr (GU) {
+        const float g = as_float(pack_bf16x2(0.0f, y));  // bf16(gate)
+        const float u = (float)dot_u * (asv * ws2[nrow + c]);
+        y = silu_bf16(g) * bf16_round(u);
+      }
+      out[(int64_t)rt * n + c0 + c] = (uint16_t)(pack_bf16x2(y, 0.0f) & 0xFFFFu);
+    }
+    __syncthreads();  // the partial sums are read before the next pass writes them
+  }
+#endif
+}
+
 template <bool GU>
 hipError_t launch_expert_skinny(const uint32_t* a, int a_words, int64_t a_bytes, const float* as,
                                 const uint32_t* w, const float* ws, const uint32_t* w2, const float* ws2,
@@ -1689,13 +1805,63 @@ int64_t expert_max_tiles(int64_t routes) {
   return (routes + bm - 1) / bm + (routes < 128 ? routes : 128);
 }
 
+// Routed rows up to which the grouped expert GEMMs run expert_decode_kernel
+// on the 32-slot tiles: 32 tokens at top-8. Omni MoE layer by graph replay,
+// weights in the last-level cache, against expert_skinny_kernel: 1 token
+// 17.4 against 21.5 us, 2: 22.3 / 26.3, 4: 29.1 / 34.0, 8: 38.2 / 44.7, 16:
+// 52.4 / 60.1, 32: 70.8 / 77.0; equal at 48 tokens, 96.4 against 85.5 at 64.
+constexpr int64_t kExpertDecodeRoutes = 256;
+
 namespace {
+template <bool GU, int NW, int RW, int MR>
+hipError_t launch_expert_decode_t(const uint32_t* a, int a_words, int64_t a_bytes, const float* as,
+                                  const uint32_t* w, const float* ws, const uint32_t* w2, const float* ws2,
+                                  const float* groups, const int32_t* schedule, int64_t routes, int64_t list_stride,
+                                  int topk, int k, int n, int input_routed, uint16_t* out, hipStream_t stream) {
+  if (a_bytes >= ((int64_t)1 << 31) || n % RW != 0) return hipErrorInvalidValue;
+  const int slices = n / RW;
+  const int64_t blocks = expert_max_tiles(routes) * slices;
+  expert_decode_kernel<GU, NW, RW, MR><<<(unsigned)blocks, NW * 64, 0, stream>>>(
+      a, a_words, (uint32_t)a_bytes, as, w, ws, w2, ws2, groups, schedule, list_stride, topk, k / 256, n,
+      input_routed, out, slices);
+  return hipGetLastError();
+}
+
+// MR: the slots a pass takes: one where an expert can have only one row (a
+// token's top-k names distinct experts, so at most `routes / topk` rows),
+// else two (8-slot passes were slower from 4 tokens on, 60.4 against 38.2 us
+// at 8 tokens: most experts then hold 1 to 3 rows, and a pass costs its slots
+// whether they are filled or not; experts with more rows take more passes).
+// NW: one k-step per wave where K has at most 8 of them.
+template <bool GU>
+hipError_t launch_expert_decode(const uint32_t* a, int a_words, int64_t a_bytes, const float* as,
+                                const uint32_t* w, const float* ws, const uint32_t* w2, const float* ws2,
+                                const float* groups, const int32_t* schedule, int64_t routes, int64_t list_stride,
+                                int topk, int k, int n, int input_routed, uint16_t* out, hipStream_t stream) {
+  const int64_t rows = topk > 0 ? (routes + topk - 1) / topk : routes;
+  const int kb = k / 256;
+#define CLEF_DEC(NW, RW, MR)                                                                                      \
+  return launch_expert_decode_t<GU, NW, RW, MR>(a, a_words, a_bytes, as, w, ws, w2, ws2, groups, schedule, routes, \
+                                                list_stride, topk, k, n, input_routed, out, stream)
+  constexpr int RW = GU ? 16 : 32;
+  if (kb <= 4) {
+    if (rows <= 1) CLEF_DEC(4, RW, 1);
+    CLEF_DEC(4, RW, 2);
+  }
+  if (rows <= 1) CLEF_DEC(8, RW, 1);
+  CLEF_DEC(8, RW, 2);
+#undef CLEF_DEC
+}
+
 template <bool GU>
 hipError_t launch_expert_skinny(const uint32_t* a, int a_words, int64_t a_bytes, const float* as,
                                 const uint32_t* w, const float* ws, const uint32_t* w2, const float* ws2,
                                 const float* groups, const int32_t* schedule, int64_t routes, int64_t list_stride,
                                 int topk, int k, int n, int input_routed, uint16_t* out, hipStream_t stream) {
   if (a_bytes >= ((int64_t)1 << 31) || n % 32 != 0) return hipErrorInvalidValue;
+  if (routes <= kExpertDecodeRoutes)
+    return launch_expert_decode<GU>(a, a_words, a_bytes, as, w, ws, w2, ws2, groups, schedule, routes, list_stride,
+                                    topk, k, n, input_routed, out, stream);
   const int slices = n / 32;
   const int64_t blocks = expert_max_tiles(routes) * slices;
   const int waves = k / 256 < 16 ? k / 256 : 16;  // one k-step per wave at most needs no more waves

@@ -550,12 +550,14 @@ def packed_experts(rng, n, k):
     return oracle.pack_weight(w)
 
 
-@pytest.mark.parametrize("tokens,hidden", [(3, 512), (64, 512), (300, 512), (7, 256)])
+@pytest.mark.parametrize("tokens,hidden", [(1, 512), (3, 512), (20, 768), (64, 512), (300, 512), (7, 256)])
 def test_expert_gemm_matches_oracle(tokens, hidden):
     """routed_experts_match_sparse_cpu_oracle (src/omni.rs:946-1051) and the
     OmniExpert paired check (src/benchmarking/omni.rs:328-356), bit-exact.
-    Up to 2048 routed rows the 32-slot skinny kernel runs (one wave per
-    k-step: K = 256 gives a single wave), above it the 128-slot kernel."""
+    Up to 256 routed rows the VALU decode kernel runs on the 32-slot tiles
+    (skewed routes give experts several two-slot passes; K = 256 and 768 give
+    one and three k-steps), up to 2048 the 32-slot skinny kernel (one wave
+    per k-step), above it the 128-slot kernel."""
     rng = np.random.default_rng(tokens)
     inter, topk = 256, 8
     routes = random_routes(rng, tokens, skew=2.0)
@@ -608,7 +610,8 @@ def test_expert_ungrouped_matches_oracle(tokens, input_routed):
     assert torch.equal(got.view(torch.int16), grouped.view(torch.int16))
 
 
-@pytest.mark.parametrize("tokens,wide", [(3, False), (64, False), (300, False), (300, True)])
+@pytest.mark.parametrize("tokens,wide", [(1, False), (3, False), (20, False), (20, True), (64, False), (300, False),
+                                         (300, True)])
 def test_expert_gate_up_swiglu_matches_oracle(tokens, wide):
     """Fused gate/up + SwiGLU (Engine::omni_gate_up, src/omni.rs:300-372) equals
     E1(gate), E1(up) then S1 of the oracle, bit for bit; inter = 512 gives four
@@ -724,7 +727,8 @@ def test_combine_matches_oracle(ordered, topk, width):
     assert_same_u16(bf16_host(got), want, "combine")
 
 
-@pytest.mark.parametrize("tokens,hidden,inter", [(1, 2048, 768), (5, 512, 256), (16, 512, 256), (17, 512, 256),
+@pytest.mark.parametrize("tokens,hidden,inter", [(1, 2048, 768), (2, 512, 256), (5, 512, 256), (16, 512, 256),
+                                                 (17, 512, 256), (32, 512, 256), (33, 512, 256),
                                                  (96, 2048, 768), (300, 1024, 512),
                                                  (256, 512, 256), (257, 512, 256), (4160, 512, 256)])
 def test_moe_layer_matches_oracle(tokens, hidden, inter):
