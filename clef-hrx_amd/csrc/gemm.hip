@@ -1619,16 +1619,33 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
 // through LDS (exact integer adds), then expert_skinny_kernel's epilogue on
 // the same integer dots: E1 = bf16(f32(dot) * RN(as * ws)), for GU S1 on the
 // bf16 gate and up values, stored to the slots' routed rows.
-template <bool GU, int NW, int RW, int MR>
+//
+// QH (the MoE layer's down projection): the activation is h itself, bf16
+// rows [routes][K] (K <= kDecodeQhMaxK), and each pass quantizes its slots'
+// rows into LDS with Q1's arithmetic (prepare_loop_body: the same rotation,
+// group maxima, scale and rounding, so the codes and scales are those
+// clef_i4_prepare writes) while the wave's first weight loads are in flight;
+// the layer then needs no separate quantizer launch for h.
+constexpr int kDecodeQhMaxK = 2048;
+template <bool GU, int NW, int RW, int MR, bool QH = false>
 __global__ __launch_bounds__(NW * 64) void expert_decode_kernel(
     const uint32_t* __restrict__ a, int a_words, uint32_t a_bytes, const float* __restrict__ as,
     const uint32_t* __restrict__ w, const float* __restrict__ ws, const uint32_t* __restrict__ w2,
     const float* __restrict__ ws2, const float* __restrict__ groups, const int32_t* __restrict__ schedule,
-    int64_t list_stride, int topk, int kb, int n, int input_routed, uint16_t* __restrict__ out, int slices) {
+    int64_t list_stride, int topk, int kb, int n, int input_routed, uint16_t* __restrict__ out, int slices,
+    const uint16_t* __restrict__ hq = nullptr) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int NA = GU ? 2 : 1, J = RW / 8;
   static_assert(RW % 8 == 0 && 128 % RW == 0, "decode tile");
+  static_assert(!QH || (!GU && MR * (kDecodeQhMaxK / 256) * 16 <= NW * 64), "one thread per 16 values of h");
   __shared__ int red[NW][NA][MR][RW];
+  // QH: the rotation buffers of each slot's groups (20-float rows, as the
+  // quantizer), the groups' maxima, and the slots' codes and scales
+  constexpr int QG = QH ? kDecodeQhMaxK / 256 : 1;
+  __shared__ __align__(16) float qbuf[QH ? MR * QG : 1][16 * 20];
+  __shared__ uint32_t qmax_s[QH ? MR * QG : 1];
+  __shared__ __align__(16) uint32_t qcodes[QH ? MR : 1][QH ? kDecodeQhMaxK / 8 : 4];
+  __shared__ float qscale[QH ? MR : 1][2];
   // Every launched item indexes inside the schedule buffer (the launch
   // covers its largest tile count), so the entry is read with the count.
   const int64_t item = blockIdx.x;
@@ -1665,15 +1682,112 @@ __global__ __launch_bounds__(NW * 64) void expert_decode_kernel(
       for (int j = 0; j < J; ++j)
 #pragma unroll
         for (int m = 0; m < MR; ++m) acc[s][j][m] = 0;
+    v4i wv0[J];  // QH: the wave's first k-step's weights, issued before the quantization
+    if constexpr (QH) {
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        wv0[j] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff + 1024 * j, (wave < kb ? wave : 0) * 16384, 0);
+      // Q1 of the pass's slots (bits 4): thread (m, g, L) takes values
+      // 16 L .. 16 L + 15 of group g of slot m's h row, as prepare_loop_body
+      // does for a row's groups.
+      const int G = kb;  // 256-value groups per row = k-steps
+      const int tq = threadIdx.x, m = tq / (QG * 16), g = (tq / 16) % QG, L = tq & 15;
+      int rm = -1;  // slot m's route (selects: route[] stays in registers)
+#pragma unroll
+      for (int mm = 0; mm < MR; ++mm) rm = mm == m ? route[mm] : rm;
+      const bool on = m < MR && g < G && rm >= 0;
+      float v[16];
+      if (on) {
+        const u4* src = reinterpret_cast<const u4*>(hq + (int64_t)rm * (kb * 256) + g * 256 + 16 * L);
+        const u4 x0 = src[0], x1 = src[1];
+        const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          v[2 * i] = bf16_lo(xw[i]);
+          v[2 * i + 1] = bf16_hi(xw[i]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+      }
+      float* buf = qbuf[m < MR ? m * QG + g : 0];
+      radix4x2(v);  // strides 1 and 4
+      if (m < MR) {
+        float4* wrow = reinterpret_cast<float4*>(buf + L * 20);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) wrow[c] = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+      }
+      __syncthreads();
+      if (m < MR) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = buf[k * 20 + L];
+      }
+      __syncthreads();
+      radix4x2(v);  // strides 16 and 64 (value k holds index L + 16 k)
+      uint32_t mbits = 0;
+      if (on) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const uint32_t av_ = as_uint(v[k]) & 0x7fffffffu;
+          mbits = mbits > av_ ? mbits : av_;
+        }
+      }
+      mbits = group_max16(mbits);
+      if (m < MR && L == 0) qmax_s[m * QG + g] = mbits;
+      if (m < MR) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) buf[k * 20 + L] = v[k];
+      }
+      __syncthreads();
+      if (tq < MR) {
+        // the row's scale and 1/16-scale (prepare_loop_body's steps)
+        uint32_t mx = 0;
+        for (int gg = 0; gg < G; ++gg) mx = mx > qmax_s[tq * QG + gg] ? mx : qmax_s[tq * QG + gg];
+        const float mf = mx >= 0x7f800000u ? __builtin_huge_valf() : as_float(mx);
+        const float normal = mf * 0.0625f;
+        const float safe = __builtin_fmaxf(normal, 1e-30f);
+        const float sc = safe / 7.0f;
+        qscale[tq][0] = sc;
+        qscale[tq][1] = 0.0625f / sc;
+      }
+      __syncthreads();
+      if (on) {
+        const float sc = qscale[m][0], inv = qscale[m][1];
+        const bool valid = sc < __builtin_huge_valf();
+        float nat[16];
+        const float4* rrow = reinterpret_cast<const float4*>(buf + L * 20);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float4 t4 = rrow[c];
+          nat[4 * c] = t4.x, nat[4 * c + 1] = t4.y, nat[4 * c + 2] = t4.z, nat[4 * c + 3] = t4.w;
+        }
+        qcodes[m][(g * 256 + 16 * L) / 8] = pack_codes<4>(nat, inv, valid);
+        qcodes[m][(g * 256 + 16 * L) / 8 + 1] = pack_codes<4>(nat + 8, inv, valid);
+      }
+      __syncthreads();
+    }
     for (int kt = wave; kt < kb; kt += NW) {
       v4i wv[NA][J], av[MR];
+      if (QH && kt == wave) {
 #pragma unroll
-      for (int j = 0; j < J; ++j) {
-        wv[0][j] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff + 1024 * j, kt * 16384, 0);
-        if constexpr (GU) wv[1][j] = __builtin_amdgcn_raw_buffer_load_b128(w2_rsrc, w_voff + 1024 * j, kt * 16384, 0);
+        for (int j = 0; j < J; ++j) wv[0][j] = wv0[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          wv[0][j] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff + 1024 * j, kt * 16384, 0);
+          if constexpr (GU)
+            wv[1][j] = __builtin_amdgcn_raw_buffer_load_b128(w2_rsrc, w_voff + 1024 * j, kt * 16384, 0);
+        }
       }
 #pragma unroll
-      for (int m = 0; m < MR; ++m) av[m] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off[m], kt * 128, 0);
+      for (int m = 0; m < MR; ++m) {
+        if constexpr (QH) {
+          const uint4 c4 = *reinterpret_cast<const uint4*>(&qcodes[m][kt * 32 + 4 * seg]);
+          av[m] = v4i{(int)c4.x, (int)c4.y, (int)c4.z, (int)c4.w};
+        } else {
+          av[m] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off[m], kt * 128, 0);
+        }
+      }
 #pragma unroll
       for (int s = 0; s < NA; ++s)
 #pragma unroll
@@ -1707,7 +1821,7 @@ __global__ __launch_bounds__(NW * 64) void expert_decode_kernel(
         dot += red[q][0][m][c];
         if constexpr (GU) dot_u += red[q][NA - 1][m][c];
       }
-      const float asv = as[input_routed ? (int64_t)rt : (int64_t)rt / topk];
+      const float asv = QH ? qscale[m][0] : as[input_routed ? (int64_t)rt : (int64_t)rt / topk];
       float y = (float)dot * (asv * ws[nrow + c]);
       if constexpr (GU) {
         const float g = as_float(pack_bf16x2(0.0f, y));  // bf16(gate)
@@ -1853,6 +1967,18 @@ hipError_t launch_expert_decode(const uint32_t* a, int a_words, int64_t a_bytes,
 #undef CLEF_DEC
 }
 
+template <int NW, int MR>
+hipError_t launch_expert_down_h_t(const uint16_t* h, const uint32_t* w, const float* ws, const float* groups,
+                                  const int32_t* schedule, int64_t routes, int64_t list_stride, int topk, int k, int n,
+                                  uint16_t* out, hipStream_t stream) {
+  constexpr int RW = 32;
+  const int slices = n / RW;
+  const int64_t blocks = expert_max_tiles(routes) * slices;
+  expert_decode_kernel<false, NW, RW, MR, true><<<(unsigned)blocks, NW * 64, 0, stream>>>(
+      nullptr, 0, 0u, nullptr, w, ws, w, ws, groups, schedule, list_stride, topk, k / 256, n, 1, out, slices, h);
+  return hipGetLastError();
+}
+
 template <bool GU>
 hipError_t launch_expert_skinny(const uint32_t* a, int a_words, int64_t a_bytes, const float* as,
                                 const uint32_t* w, const float* ws, const uint32_t* w2, const float* ws2,
@@ -1964,6 +2090,33 @@ hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int topk,
 hipError_t launch_expert_tasks(const float* groups, int64_t tokens, float* tasks, hipStream_t stream) {
   tile_list_kernel<float, 1><<<1, 128, 0, stream>>>(groups, tokens, 16, tasks);
   return hipGetLastError();
+}
+
+// Routed rows up to which the MoE layer's down projection quantizes its own
+// h rows (launch_expert_down_h). Every column slice of a tile repeats its
+// pass's quantization, which costs more than the quantizer launch it saves
+// once experts take several passes. Omni MoE layer by graph replay, weights
+// cached, against the separate quantizer: 1 token 15.8 against 17.7 us, 2:
+// 21.2 / 22.6, 4: 30.0 / 30.2; 8: 39.4 / 38.7, 16: 56.5 / 52.9.
+constexpr int64_t kExpertDownHRoutes = 32;
+
+bool expert_down_h_fusable(int64_t routes, int k, int n) {
+  return routes <= kExpertDownHRoutes && k % 256 == 0 && k <= kDecodeQhMaxK && n % 32 == 0;
+}
+
+hipError_t launch_expert_down_h(const uint16_t* h, const uint32_t* w, const float* ws, const float* groups,
+                                const int32_t* schedule, int64_t tokens, int topk, int k, int n, uint16_t* out,
+                                hipStream_t stream) {
+  const int64_t routes = tokens * topk;
+  if (!expert_down_h_fusable(routes, k, n) || topk < 1) return hipErrorInvalidValue;
+  const int64_t list_stride = tokens + 1;
+  const bool one_row = tokens <= 1;  // a token's top-k names distinct experts
+  if (k / 256 <= 4) {
+    if (one_row) return launch_expert_down_h_t<4, 1>(h, w, ws, groups, schedule, routes, list_stride, topk, k, n, out, stream);
+    return launch_expert_down_h_t<4, 2>(h, w, ws, groups, schedule, routes, list_stride, topk, k, n, out, stream);
+  }
+  if (one_row) return launch_expert_down_h_t<8, 1>(h, w, ws, groups, schedule, routes, list_stride, topk, k, n, out, stream);
+  return launch_expert_down_h_t<8, 2>(h, w, ws, groups, schedule, routes, list_stride, topk, k, n, out, stream);
 }
 
 hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* as, const uint32_t* w,

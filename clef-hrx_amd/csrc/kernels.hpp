@@ -111,6 +111,14 @@ hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int topk,
 // `list_stride` is the row pitch of `groups` in floats: tokens + 1 for the
 // reference's table (0 selects it), more for a table that lists every route
 // slot (ungrouped, duplicates included).
+// The MoE layer's down projection for few routed rows straight from the
+// bf16 h rows [tokens * topk][k] (quantized per pass inside the kernel, the
+// codes and scales equal to launch_prepare's): launch_prepare of h then
+// launch_expert_i4 (input_routed 1) in one launch, with the same output.
+bool expert_down_h_fusable(int64_t routes, int k, int n);
+hipError_t launch_expert_down_h(const uint16_t* h, const uint32_t* w, const float* ws, const float* groups,
+                                const int32_t* schedule, int64_t tokens, int topk, int k, int n, uint16_t* out,
+                                hipStream_t stream);
 hipError_t launch_expert_i4(const uint32_t* a, int a_words, const float* a_scales,
                             const uint32_t* w_tiled, const float* w_scales, const float* groups,
                             const int32_t* schedule, int64_t tokens, int topk, int k, int n,

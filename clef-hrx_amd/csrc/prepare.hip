@@ -195,40 +195,6 @@ struct NormSource {
   }
 };
 
-__device__ __forceinline__ uint32_t group_max16(uint32_t m) {
-  // Reduce over the 16 lanes of a group (lanes differ in the low 4 bits): a
-  // DPP row. quad_perm [1,0,3,2] and [2,3,0,1], then row_ror 4 and 8, leave
-  // the row's maximum in every lane (every lane of the wave is active here).
-  auto step = [](uint32_t v, uint32_t o) { return v > o ? v : o; };
-  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));
-  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));
-  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x124, 0xF, 0xF, false));
-  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x128, 0xF, 0xF, false));
-  return m;
-}
-
-template <int BITS>
-__device__ __forceinline__ uint32_t pack_codes(const float* v, float inv, bool valid) {
-  constexpr int per = 32 / BITS;
-  constexpr float qmax = BITS == 8 ? 127.0f : 7.0f;
-  constexpr uint32_t mask = BITS == 8 ? 0xffu : 0xfu;
-  // Round to nearest even by adding 1.5 * 2^23: when valid, |v * inv| <= qmax
-  // (times 1 + 2^-22), so the sum lies in [2^23, 2^24), where the f32 spacing is
-  // 1 and the addend is even; the add then rounds exactly as rint does, and
-  // the integer n sits two's complement in the low mantissa bits (the addend's
-  // mantissa is 0x400000). Clamping the biased value to magic +- qmax is the
-  // clamp of n.
-  constexpr float magic = 12582912.0f;
-  uint32_t word = 0;
-#pragma unroll
-  for (int p = 0; p < per; ++p) {
-    float t = v[p] * inv + magic;
-    t = __builtin_fminf(__builtin_fmaxf(t, magic - qmax), magic + qmax);
-    word |= (as_uint(t) & mask) << (p * BITS);
-  }
-  return valid ? word : 0u;
-}
-
 // The 16 codes clamp(rint(v * inv), -7, 7) of one lane as e3m2 (exact for
 // these integers), value i at bits 6i of o[0..2]: the bf6 form of the INT4
 // codes, for the bf6 projection.
