@@ -1835,6 +1835,158 @@ __global__ __launch_bounds__(NW * 64) void expert_decode_kernel(
 #endif
 }
 
+// The MoE layer's down projection and combine for a few tokens at top-8
+// (decode): workgroup (t, slice) owns token t's RW output columns. Its 8
+// waves take the token's 8 route slots in combine order (order[t][j]: the
+// slot with the j-th smallest expert id), wave j all k-steps of slot j's
+// expert: each lane reads 16 bytes (32 k) at k-segment lane % 8 of weight row
+// lane / 8 and the same segment of the slot's h row, quantized first into
+// LDS with Q1's arithmetic (as expert_decode_kernel's QH). The segment sums
+// meet by DPP; value j = E1 = bf16(f32(dot) * RN(as * ws)) of the slot goes
+// to LDS, and each column's combine runs over the 8 values in order:
+// acc = bf16(acc + bf16(v_j * p_j)) (combine_kernel's sequence), stored as
+// bf16. One launch instead of the down projection and combine.
+constexpr int kDownCombineMaxK = 1024;
+template <int RW>
+__global__ __launch_bounds__(512) void moe_down_combine_kernel(
+    const uint16_t* __restrict__ h, const uint32_t* __restrict__ w, const float* __restrict__ ws,
+    const float* __restrict__ routes, const float* __restrict__ order, int kb, int n, int slices,
+    uint16_t* __restrict__ out) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int KT = 8, QG = kDownCombineMaxK / 256, J = RW / 8;
+  static_assert(RW % 8 == 0 && 128 % RW == 0 && KT * QG * 16 == 512, "one thread per 16 values of h");
+  __shared__ __align__(16) float qbuf[KT * QG][16 * 20];
+  __shared__ uint32_t qmax_s[KT * QG];
+  __shared__ __align__(16) uint32_t qcodes[KT][kDownCombineMaxK / 8];
+  __shared__ float qscale[KT][2];
+  __shared__ float vals[KT][RW];
+  const int t = (int)(blockIdx.x / slices);
+  const int c0 = (int)(blockIdx.x - (int64_t)t * slices) * RW;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // combine position j of this wave's slot
+  const int seg = lane & 7, r8 = lane >> 3;
+  const float* rt = routes + (int64_t)t * 2 * KT;
+  // this wave's slot, its expert and weight rows
+  const int slot = (int)order[(int64_t)t * KT + wave];
+  const int e = (int)rt[slot];
+  const int64_t nrow = (int64_t)e * n + c0;
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(w + (nrow / 128) * kb * 4096, (uint32_t)(kb * 16384));
+  const int w_voff = (int)(nrow % 128 + r8) * 128 + 16 * seg;
+  v4i wv[QG][J];
+#pragma unroll
+  for (int kt = 0; kt < QG; ++kt)
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      wv[kt][j] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff + 1024 * j, (kt < kb ? kt : 0) * 16384, 0);
+  // Q1 of the token's 8 h rows (slot order): thread (m, g, L) takes values
+  // 16 L .. 16 L + 15 of group g of row t * 8 + m (prepare_loop_body's steps)
+  {
+    const int G = kb;
+    const int tq = threadIdx.x, m = tq / (QG * 16), g = (tq / 16) % QG, L = tq & 15;
+    const bool on = g < G;
+    float v[16];
+    if (on) {
+      const u4* src = reinterpret_cast<const u4*>(h + ((int64_t)t * KT + m) * (kb * 256) + g * 256 + 16 * L);
+      const u4 x0 = src[0], x1 = src[1];
+      const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v[2 * i] = bf16_lo(xw[i]);
+        v[2 * i + 1] = bf16_hi(xw[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+    }
+    float* buf = qbuf[m * QG + g];
+    radix4x2(v);  // strides 1 and 4
+    float4* wrow = reinterpret_cast<float4*>(buf + L * 20);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) wrow[c] = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = buf[k * 20 + L];
+    __syncthreads();
+    radix4x2(v);  // strides 16 and 64 (value k holds index L + 16 k)
+    uint32_t mbits = 0;
+    if (on) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const uint32_t a = as_uint(v[k]) & 0x7fffffffu;
+        mbits = mbits > a ? mbits : a;
+      }
+    }
+    mbits = group_max16(mbits);
+    if (L == 0) qmax_s[m * QG + g] = mbits;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) buf[k * 20 + L] = v[k];
+    __syncthreads();
+    if (tq < KT) {
+      uint32_t mx = 0;
+      for (int gg = 0; gg < G; ++gg) mx = mx > qmax_s[tq * QG + gg] ? mx : qmax_s[tq * QG + gg];
+      const float mf = mx >= 0x7f800000u ? __builtin_huge_valf() : as_float(mx);
+      const float normal = mf * 0.0625f;
+      const float safe = __builtin_fmaxf(normal, 1e-30f);
+      const float sc = safe / 7.0f;
+      qscale[tq][0] = sc;
+      qscale[tq][1] = 0.0625f / sc;
+    }
+    __syncthreads();
+    if (on) {
+      const float sc = qscale[m][0], inv = qscale[m][1];
+      const bool valid = sc < __builtin_huge_valf();
+      float nat[16];
+      const float4* rrow = reinterpret_cast<const float4*>(buf + L * 20);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float4 t4 = rrow[c];
+        nat[4 * c] = t4.x, nat[4 * c + 1] = t4.y, nat[4 * c + 2] = t4.z, nat[4 * c + 3] = t4.w;
+      }
+      qcodes[m][(g * 256 + 16 * L) / 8] = pack_codes<4>(nat, inv, valid);
+      qcodes[m][(g * 256 + 16 * L) / 8 + 1] = pack_codes<4>(nat + 8, inv, valid);
+    }
+    __syncthreads();
+  }
+  // the slot's dot products over every k-step (exact integer sums)
+  int acc[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) acc[j] = 0;
+#pragma unroll
+  for (int kt = 0; kt < QG; ++kt) {
+    if (kt >= kb) break;
+    const uint4 c4 = *reinterpret_cast<const uint4*>(&qcodes[slot][kt * 32 + 4 * seg]);
+    const int av[4] = {(int)c4.x, (int)c4.y, (int)c4.z, (int)c4.w};
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[j] = __builtin_amdgcn_sdot8(wv[kt][j][c], av[c], acc[j], false);
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    int v = acc[j];
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    v += __builtin_amdgcn_ds_swizzle(v, 0x101F);
+    if (seg == 0) {
+      const int col = r8 + 8 * j;
+      const float y = (float)v * (qscale[slot][0] * ws[nrow + col]);
+      vals[wave][col] = bf16_to_f32(f32_to_bf16(y));  // the slot's E1 value, bf16
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < RW) {
+    const int col = threadIdx.x;
+    float acc2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+      const float p = rt[KT + (int)order[(int64_t)t * KT + j]];
+      acc2 = bf16_round(acc2 + bf16_round(vals[j][col] * p));
+    }
+    out[(int64_t)t * n + c0 + col] = (uint16_t)f32_to_bf16(acc2);
+  }
+#endif
+}
+
 template <bool GU>
 hipError_t launch_expert_skinny(const uint32_t* a, int a_words, int64_t a_bytes, const float* as,
                                 const uint32_t* w, const float* ws, const uint32_t* w2, const float* ws2,
@@ -2102,6 +2254,30 @@ constexpr int64_t kExpertDownHRoutes = 32;
 
 bool expert_down_h_fusable(int64_t routes, int k, int n) {
   return routes <= kExpertDownHRoutes && k % 256 == 0 && k <= kDecodeQhMaxK && n % 32 == 0;
+}
+
+// Tokens up to which the MoE layer runs moe_down_combine_kernel. Each token
+// reads its 8 experts' down weights itself (experts two tokens share are read
+// twice), which the launches it saves outweigh up to here. Omni MoE layer by
+// graph replay, weights cached, against the down projection (quantizing its
+// own h rows up to 4 tokens) then combine: 1 token 14.3 against 15.8 us, 2:
+// 19.0 / 21.1, 3: 22.6 / 24.8, 4: 27.1 / 29.1, 6: 32.0 / 33.3; 8: 38.5 / 38.3.
+constexpr int64_t kDownCombineTokens = 6;
+
+bool down_combine_fusable(int64_t tokens, int topk, int k, int n) {
+  return tokens >= 1 && tokens <= kDownCombineTokens && topk == 8 && k % 256 == 0 && k <= kDownCombineMaxK &&
+         n % 8 == 0;
+}
+
+hipError_t launch_down_combine(const uint16_t* h, const uint32_t* w, const float* ws, const float* routes,
+                               const float* order, int64_t tokens, int topk, int k, int n, uint16_t* out,
+                               hipStream_t stream) {
+  if (!down_combine_fusable(tokens, topk, k, n)) return hipErrorInvalidValue;
+  constexpr int RW = 8;
+  const int slices = n / RW;
+  moe_down_combine_kernel<RW><<<(unsigned)(tokens * slices), 512, 0, stream>>>(h, w, ws, routes, order, k / 256, n,
+                                                                              slices, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_expert_down_h(const uint16_t* h, const uint32_t* w, const float* ws, const float* groups,

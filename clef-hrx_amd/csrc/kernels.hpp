@@ -116,6 +116,14 @@ hipError_t launch_expert_schedule(const float* groups, int64_t tokens, int topk,
 // codes and scales equal to launch_prepare's): launch_prepare of h then
 // launch_expert_i4 (input_routed 1) in one launch, with the same output.
 bool expert_down_h_fusable(int64_t routes, int k, int n);
+// The MoE layer's down projection and combine for a few tokens at top-8
+// (down_combine_fusable) in one launch, from the bf16 h rows [tokens * 8][k], the routes and
+// the combine order the grouping wrote: launch_prepare of h, launch_expert_i4
+// (input_routed 1) and launch_combine in one, with the same output.
+bool down_combine_fusable(int64_t tokens, int topk, int k, int n);
+hipError_t launch_down_combine(const uint16_t* h, const uint32_t* w, const float* ws, const float* routes,
+                               const float* order, int64_t tokens, int topk, int k, int n, uint16_t* out,
+                               hipStream_t stream);
 hipError_t launch_expert_down_h(const uint16_t* h, const uint32_t* w, const float* ws, const float* groups,
                                 const int32_t* schedule, int64_t tokens, int topk, int k, int n, uint16_t* out,
                                 hipStream_t stream);

@@ -728,14 +728,15 @@ def test_combine_matches_oracle(ordered, topk, width):
 
 
 @pytest.mark.parametrize("tokens,hidden,inter", [(1, 2048, 768), (2, 512, 256), (4, 2048, 768), (5, 512, 256),
-                                                 (3, 512, 2048), (16, 512, 256),
+                                                 (6, 512, 1024), (7, 512, 256), (3, 512, 2048), (16, 512, 256),
                                                  (17, 512, 256), (32, 512, 256), (33, 512, 256),
                                                  (96, 2048, 768), (300, 1024, 512),
                                                  (256, 512, 256), (257, 512, 256), (4160, 512, 256)])
 def test_moe_layer_matches_oracle(tokens, hidden, inter):
     """Whole Omni INT4 MoE block (src/omni.rs:762-857) bit-exact vs the oracle.
-    Up to 4 tokens the down projection quantizes its own h rows (inter 768
-    with four waves, 2048 with eight), 5 does not; 32 and 33 tokens sit on
+    Up to 6 tokens the down projection, its quantizer and combine run as one
+    kernel (inter up to 1024; 7 tokens do not); with inter 2048 up to 4
+    tokens the down projection quantizes its own h rows; 32 and 33 tokens sit on
     either side of the VALU decode expert kernels' limit, 256 and 257 tokens
     (2048 and 2056 routed rows) on either side of the switch from 32-slot to
     128-slot expert tiles; 4160 tokens (65 blocks of 64) take the grouping
