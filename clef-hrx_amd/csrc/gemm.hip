@@ -17,6 +17,7 @@
 #include "expert_persist.hpp"
 #include "kernels.hpp"
 #include "launch.hpp"
+#include "route.hpp"
 
 namespace clef {
 
@@ -1605,6 +1606,92 @@ __global__ __launch_bounds__(1024) void expert_skinny_kernel(
 #endif
 }
 
+// Q1 (bits 4) of up to MR bf16 rows of G 256-value groups (G <= QG) into
+// LDS, with prepare_loop_body's arithmetic (the same rotation, group maxima,
+// scale and rounding, so the codes and scales are those clef_i4_prepare
+// writes): row m's codes as packed words in qcodes[m] (32 words per group),
+// its scale in qscale[m][0]. Thread (m, g, L) = (tid / (QG * 16),
+// tid / 16 % QG, tid % 16), for tid < MR * QG * 16, takes values 16 L ..
+// 16 L + 15 of group g of row m; row(m) gives the row's first element, or
+// nullptr for a slot without a row. Every thread of the workgroup calls it
+// (it holds barriers); the lanes of each 16-lane group stay together.
+template <int MR, int QG, class RowFn>
+__device__ __forceinline__ void q1_rows_lds(RowFn row, int G, float (*qbuf)[16 * 20], uint32_t* qmax_s,
+                                            uint32_t (*qcodes)[QG * 32], float (*qscale)[2]) {
+  const int tq = threadIdx.x, m = tq / (QG * 16), g = (tq / 16) % QG, L = tq & 15;
+  const uint16_t* src = m < MR ? row(m) : nullptr;
+  const bool on = m < MR && g < G && src != nullptr;
+  float v[16];
+  if (on) {
+    const u4* p = reinterpret_cast<const u4*>(src + g * 256 + 16 * L);
+    const u4 x0 = p[0], x1 = p[1];
+    const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[2 * i] = bf16_lo(xw[i]);
+      v[2 * i + 1] = bf16_hi(xw[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+  }
+  float* buf = qbuf[m < MR ? m * QG + g : 0];
+  radix4x2(v);  // strides 1 and 4
+  if (m < MR) {
+    float4* wrow = reinterpret_cast<float4*>(buf + L * 20);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) wrow[c] = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+  }
+  __syncthreads();
+  if (m < MR) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = buf[k * 20 + L];
+  }
+  __syncthreads();
+  radix4x2(v);  // strides 16 and 64 (value k holds index L + 16 k)
+  uint32_t mbits = 0;
+  if (on) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const uint32_t a = as_uint(v[k]) & 0x7fffffffu;
+      mbits = mbits > a ? mbits : a;
+    }
+  }
+  mbits = group_max16(mbits);
+  if (m < MR && L == 0) qmax_s[m * QG + g] = mbits;
+  if (m < MR) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) buf[k * 20 + L] = v[k];
+  }
+  __syncthreads();
+  if (tq < MR) {
+    // the row's scale and 1/16-scale (prepare_loop_body's steps)
+    uint32_t mx = 0;
+    for (int gg = 0; gg < G; ++gg) mx = mx > qmax_s[tq * QG + gg] ? mx : qmax_s[tq * QG + gg];
+    const float mf = mx >= 0x7f800000u ? __builtin_huge_valf() : as_float(mx);
+    const float normal = mf * 0.0625f;
+    const float safe = __builtin_fmaxf(normal, 1e-30f);
+    const float sc = safe / 7.0f;
+    qscale[tq][0] = sc;
+    qscale[tq][1] = 0.0625f / sc;
+  }
+  __syncthreads();
+  if (on) {
+    const float sc = qscale[m][0], inv = qscale[m][1];
+    const bool valid = sc < __builtin_huge_valf();
+    float nat[16];
+    const float4* rrow = reinterpret_cast<const float4*>(buf + L * 20);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4 t4 = rrow[c];
+      nat[4 * c] = t4.x, nat[4 * c + 1] = t4.y, nat[4 * c + 2] = t4.z, nat[4 * c + 3] = t4.w;
+    }
+    qcodes[m][(g * 256 + 16 * L) / 8] = pack_codes<4>(nat, inv, valid);
+    qcodes[m][(g * 256 + 16 * L) / 8 + 1] = pack_codes<4>(nat + 8, inv, valid);
+  }
+  __syncthreads();
+}
+
 // Grouped expert GEMM for schedule tiles of a few routed rows (decode
 // batches: up to 32 tokens, where most experts hold one to three rows), on
 // the VALU as gemm_decode_kernel: v_dot8_i32_i4 multiplies the packed codes
@@ -1644,7 +1731,7 @@ __global__ __launch_bounds__(NW * 64) void expert_decode_kernel(
   constexpr int QG = QH ? kDecodeQhMaxK / 256 : 1;
   __shared__ __align__(16) float qbuf[QH ? MR * QG : 1][16 * 20];
   __shared__ uint32_t qmax_s[QH ? MR * QG : 1];
-  __shared__ __align__(16) uint32_t qcodes[QH ? MR : 1][QH ? kDecodeQhMaxK / 8 : 4];
+  __shared__ __align__(16) uint32_t qcodes[QH ? MR : 1][QG * 32];
   __shared__ float qscale[QH ? MR : 1][2];
   // Every launched item indexes inside the schedule buffer (the launch
   // covers its largest tile count), so the entry is read with the count.
@@ -1687,84 +1774,15 @@ __global__ __launch_bounds__(NW * 64) void expert_decode_kernel(
 #pragma unroll
       for (int j = 0; j < J; ++j)
         wv0[j] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff + 1024 * j, (wave < kb ? wave : 0) * 16384, 0);
-      // Q1 of the pass's slots (bits 4): thread (m, g, L) takes values
-      // 16 L .. 16 L + 15 of group g of slot m's h row, as prepare_loop_body
-      // does for a row's groups.
-      const int G = kb;  // 256-value groups per row = k-steps
-      const int tq = threadIdx.x, m = tq / (QG * 16), g = (tq / 16) % QG, L = tq & 15;
-      int rm = -1;  // slot m's route (selects: route[] stays in registers)
+      // Q1 of the pass's slots' h rows
+      q1_rows_lds<MR, QG>(
+          [&](int m) -> const uint16_t* {
+            int rm = -1;  // slot m's route (selects: route[] stays in registers)
 #pragma unroll
-      for (int mm = 0; mm < MR; ++mm) rm = mm == m ? route[mm] : rm;
-      const bool on = m < MR && g < G && rm >= 0;
-      float v[16];
-      if (on) {
-        const u4* src = reinterpret_cast<const u4*>(hq + (int64_t)rm * (kb * 256) + g * 256 + 16 * L);
-        const u4 x0 = src[0], x1 = src[1];
-        const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          v[2 * i] = bf16_lo(xw[i]);
-          v[2 * i + 1] = bf16_hi(xw[i]);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = 0.0f;
-      }
-      float* buf = qbuf[m < MR ? m * QG + g : 0];
-      radix4x2(v);  // strides 1 and 4
-      if (m < MR) {
-        float4* wrow = reinterpret_cast<float4*>(buf + L * 20);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) wrow[c] = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
-      }
-      __syncthreads();
-      if (m < MR) {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = buf[k * 20 + L];
-      }
-      __syncthreads();
-      radix4x2(v);  // strides 16 and 64 (value k holds index L + 16 k)
-      uint32_t mbits = 0;
-      if (on) {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          const uint32_t av_ = as_uint(v[k]) & 0x7fffffffu;
-          mbits = mbits > av_ ? mbits : av_;
-        }
-      }
-      mbits = group_max16(mbits);
-      if (m < MR && L == 0) qmax_s[m * QG + g] = mbits;
-      if (m < MR) {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) buf[k * 20 + L] = v[k];
-      }
-      __syncthreads();
-      if (tq < MR) {
-        // the row's scale and 1/16-scale (prepare_loop_body's steps)
-        uint32_t mx = 0;
-        for (int gg = 0; gg < G; ++gg) mx = mx > qmax_s[tq * QG + gg] ? mx : qmax_s[tq * QG + gg];
-        const float mf = mx >= 0x7f800000u ? __builtin_huge_valf() : as_float(mx);
-        const float normal = mf * 0.0625f;
-        const float safe = __builtin_fmaxf(normal, 1e-30f);
-        const float sc = safe / 7.0f;
-        qscale[tq][0] = sc;
-        qscale[tq][1] = 0.0625f / sc;
-      }
-      __syncthreads();
-      if (on) {
-        const float sc = qscale[m][0], inv = qscale[m][1];
-        const bool valid = sc < __builtin_huge_valf();
-        float nat[16];
-        const float4* rrow = reinterpret_cast<const float4*>(buf + L * 20);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float4 t4 = rrow[c];
-          nat[4 * c] = t4.x, nat[4 * c + 1] = t4.y, nat[4 * c + 2] = t4.z, nat[4 * c + 3] = t4.w;
-        }
-        qcodes[m][(g * 256 + 16 * L) / 8] = pack_codes<4>(nat, inv, valid);
-        qcodes[m][(g * 256 + 16 * L) / 8 + 1] = pack_codes<4>(nat + 8, inv, valid);
-      }
-      __syncthreads();
+            for (int mm = 0; mm < MR; ++mm) rm = mm == m ? route[mm] : rm;
+            return rm >= 0 ? hq + (int64_t)rm * (kb * 256) : nullptr;
+          },
+          kb, qbuf, qmax_s, qcodes, qscale);
     }
     for (int kt = wave; kt < kb; kt += NW) {
       v4i wv[NA][J], av[MR];
@@ -1835,6 +1853,120 @@ __global__ __launch_bounds__(NW * 64) void expert_decode_kernel(
 #endif
 }
 
+// The MoE layer's router, Q1(x) and fused gate/up + SwiGLU for a few tokens
+// at top-8 over 128 experts (decode), one launch: workgroup (t, r, slice)
+// owns route slot r of token t and RW columns of h. Every workgroup routes
+// the tokens itself (route_body16, the router's own code: the same ids;
+// workgroup 0 also writes the routes and the combine order, order[t][j] =
+// the slot with the j-th smallest expert id, as the grouping does), quantizes
+// token t's x row into LDS (q1_rows_lds: the codes and scale
+// clef_i4_prepare writes), and multiplies it with its expert's RW gate and
+// RW up rows as expert_decode_kernel does (v_dot8_i32_i4, whole weight rows
+// per load, k-steps split over the waves), then writes h = S1(E1(gate),
+// E1(up)) for the slot's routed row. The redundant routing and Q1 cost less
+// than the two launches and the grouping they replace up to a dozen tokens.
+constexpr int kRouteGateUpMaxK = 2048;
+template <int NW, int RW>
+__global__ __launch_bounds__(NW * 64) void moe_route_gate_up_kernel(
+    const void* __restrict__ logits, int dtype, int tokens, const uint16_t* __restrict__ x,
+    const uint32_t* __restrict__ gw, const float* __restrict__ gs, const uint32_t* __restrict__ uw,
+    const float* __restrict__ us, int kb, int n, int slices, float* __restrict__ routes,
+    float* __restrict__ order, uint16_t* __restrict__ h) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int KT = 8, QG = kRouteGateUpMaxK / 256, J = RW / 8;
+  static_assert(RW % 8 == 0 && 128 % RW == 0 && NW * 64 >= 256 && QG * 16 <= NW * 64, "decode tile");
+  __shared__ int ids[16 * KT];
+  __shared__ int red[NW][2][RW];
+  __shared__ __align__(16) float qbuf[QG][16 * 20];
+  __shared__ uint32_t qmax_s[QG];
+  __shared__ __align__(16) uint32_t qcodes[1][QG * 32];
+  __shared__ float qscale[1][2];
+  const int per_token = KT * slices;
+  const int t = (int)(blockIdx.x / per_token);
+  const int rs = (int)(blockIdx.x - (int64_t)t * per_token);
+  const int r = rs / slices, c0 = (rs - r * slices) * RW;
+  // every thread takes part in the routing's row reductions (tokens <= 16)
+  route_impl::route_body16(logits, dtype, tokens, 128, KT, routes, 0, ids, blockIdx.x == 0);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int seg = lane & 7, r8 = lane >> 3;
+  if (blockIdx.x == 0 && threadIdx.x < tokens * KT) {
+    const int tt = threadIdx.x / KT, e = ids[threadIdx.x];
+    int less = 0;
+#pragma unroll
+    for (int q = 0; q < KT; ++q) less += ids[tt * KT + q] < e ? 1 : 0;
+    order[tt * KT + less] = (float)(threadIdx.x % KT);
+  }
+  const int e = ids[t * KT + r];
+  const int64_t nrow = (int64_t)e * n + c0;
+  const __amdgpu_buffer_rsrc_t g_rsrc = make_rsrc(gw + (nrow / 128) * kb * 4096, (uint32_t)(kb * 16384));
+  const __amdgpu_buffer_rsrc_t u_rsrc = make_rsrc(uw + (nrow / 128) * kb * 4096, (uint32_t)(kb * 16384));
+  const int w_voff = (int)(nrow % 128 + r8) * 128 + 16 * seg;
+  // the wave's first k-step's gate and up rows go out before the quantization
+  v4i wv0[2][J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    wv0[0][j] = __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, w_voff + 1024 * j, (wave < kb ? wave : 0) * 16384, 0);
+    wv0[1][j] = __builtin_amdgcn_raw_buffer_load_b128(u_rsrc, w_voff + 1024 * j, (wave < kb ? wave : 0) * 16384, 0);
+  }
+  q1_rows_lds<1, QG>([&](int) -> const uint16_t* { return x + (int64_t)t * (kb * 256); }, kb, qbuf, qmax_s, qcodes,
+                     qscale);
+  int acc[2][J];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+    for (int j = 0; j < J; ++j) acc[s2][j] = 0;
+  for (int kt = wave; kt < kb; kt += NW) {
+    v4i wv[2][J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      if (kt == wave) {
+        wv[0][j] = wv0[0][j];
+        wv[1][j] = wv0[1][j];
+      } else {
+        wv[0][j] = __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, w_voff + 1024 * j, kt * 16384, 0);
+        wv[1][j] = __builtin_amdgcn_raw_buffer_load_b128(u_rsrc, w_voff + 1024 * j, kt * 16384, 0);
+      }
+    }
+    const uint4 c4 = *reinterpret_cast<const uint4*>(&qcodes[0][kt * 32 + 4 * seg]);
+    const int av[4] = {(int)c4.x, (int)c4.y, (int)c4.z, (int)c4.w};
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[s2][j] = __builtin_amdgcn_sdot8(wv[s2][j][c], av[c], acc[s2][j], false);
+  }
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      int v = acc[s2][j];
+      v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+      v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+      v += __builtin_amdgcn_ds_swizzle(v, 0x101F);
+      if (seg == 0) red[wave][s2][r8 + 8 * j] = v;
+    }
+  __syncthreads();
+  if (threadIdx.x < RW) {
+    const int c = threadIdx.x;
+    int dg = 0, du = 0;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      dg += red[q][0][c];
+      du += red[q][1][c];
+    }
+    const float asv = qscale[0][0];
+    const float y = (float)dg * (asv * gs[nrow + c]);
+    const float g = as_float(pack_bf16x2(0.0f, y));  // bf16(gate)
+    const float u = (float)du * (asv * us[nrow + c]);
+    const float hv = silu_bf16(g) * bf16_round(u);
+    h[((int64_t)t * KT + r) * n + c0 + c] = (uint16_t)(pack_bf16x2(hv, 0.0f) & 0xFFFFu);
+  }
+#endif
+}
+
 // The MoE layer's down projection and combine for a few tokens at top-8
 // (decode): workgroup (t, slice) owns token t's RW output columns. Its 8
 // waves take the token's 8 route slots in combine order (order[t][j]: the
@@ -1857,7 +1989,7 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
   static_assert(RW % 8 == 0 && 128 % RW == 0 && KT * QG * 16 == 512, "one thread per 16 values of h");
   __shared__ __align__(16) float qbuf[KT * QG][16 * 20];
   __shared__ uint32_t qmax_s[KT * QG];
-  __shared__ __align__(16) uint32_t qcodes[KT][kDownCombineMaxK / 8];
+  __shared__ __align__(16) uint32_t qcodes[KT][QG * 32];
   __shared__ float qscale[KT][2];
   __shared__ float vals[KT][RW];
   const int t = (int)(blockIdx.x / slices);
@@ -1878,75 +2010,9 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
 #pragma unroll
     for (int j = 0; j < J; ++j)
       wv[kt][j] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_voff + 1024 * j, (kt < kb ? kt : 0) * 16384, 0);
-  // Q1 of the token's 8 h rows (slot order): thread (m, g, L) takes values
-  // 16 L .. 16 L + 15 of group g of row t * 8 + m (prepare_loop_body's steps)
-  {
-    const int G = kb;
-    const int tq = threadIdx.x, m = tq / (QG * 16), g = (tq / 16) % QG, L = tq & 15;
-    const bool on = g < G;
-    float v[16];
-    if (on) {
-      const u4* src = reinterpret_cast<const u4*>(h + ((int64_t)t * KT + m) * (kb * 256) + g * 256 + 16 * L);
-      const u4 x0 = src[0], x1 = src[1];
-      const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        v[2 * i] = bf16_lo(xw[i]);
-        v[2 * i + 1] = bf16_hi(xw[i]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = 0.0f;
-    }
-    float* buf = qbuf[m * QG + g];
-    radix4x2(v);  // strides 1 and 4
-    float4* wrow = reinterpret_cast<float4*>(buf + L * 20);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) wrow[c] = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = buf[k * 20 + L];
-    __syncthreads();
-    radix4x2(v);  // strides 16 and 64 (value k holds index L + 16 k)
-    uint32_t mbits = 0;
-    if (on) {
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const uint32_t a = as_uint(v[k]) & 0x7fffffffu;
-        mbits = mbits > a ? mbits : a;
-      }
-    }
-    mbits = group_max16(mbits);
-    if (L == 0) qmax_s[m * QG + g] = mbits;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) buf[k * 20 + L] = v[k];
-    __syncthreads();
-    if (tq < KT) {
-      uint32_t mx = 0;
-      for (int gg = 0; gg < G; ++gg) mx = mx > qmax_s[tq * QG + gg] ? mx : qmax_s[tq * QG + gg];
-      const float mf = mx >= 0x7f800000u ? __builtin_huge_valf() : as_float(mx);
-      const float normal = mf * 0.0625f;
-      const float safe = __builtin_fmaxf(normal, 1e-30f);
-      const float sc = safe / 7.0f;
-      qscale[tq][0] = sc;
-      qscale[tq][1] = 0.0625f / sc;
-    }
-    __syncthreads();
-    if (on) {
-      const float sc = qscale[m][0], inv = qscale[m][1];
-      const bool valid = sc < __builtin_huge_valf();
-      float nat[16];
-      const float4* rrow = reinterpret_cast<const float4*>(buf + L * 20);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float4 t4 = rrow[c];
-        nat[4 * c] = t4.x, nat[4 * c + 1] = t4.y, nat[4 * c + 2] = t4.z, nat[4 * c + 3] = t4.w;
-      }
-      qcodes[m][(g * 256 + 16 * L) / 8] = pack_codes<4>(nat, inv, valid);
-      qcodes[m][(g * 256 + 16 * L) / 8 + 1] = pack_codes<4>(nat + 8, inv, valid);
-    }
-    __syncthreads();
-  }
+  // Q1 of the token's 8 h rows (slot order)
+  q1_rows_lds<KT, QG>([&](int m) -> const uint16_t* { return h + ((int64_t)t * KT + m) * (kb * 256); }, kb, qbuf,
+                      qmax_s, qcodes, qscale);
   // the slot's dot products over every k-step (exact integer sums)
   int acc[J];
 #pragma unroll
@@ -2256,27 +2322,65 @@ bool expert_down_h_fusable(int64_t routes, int k, int n) {
   return routes <= kExpertDownHRoutes && k % 256 == 0 && k <= kDecodeQhMaxK && n % 32 == 0;
 }
 
-// Tokens up to which the MoE layer runs moe_down_combine_kernel. Each token
-// reads its 8 experts' down weights itself (experts two tokens share are read
-// twice), which the launches it saves outweigh up to here. Omni MoE layer by
-// graph replay, weights cached, against the down projection (quantizing its
-// own h rows up to 4 tokens) then combine: 1 token 14.3 against 15.8 us, 2:
-// 19.0 / 21.1, 3: 22.6 / 24.8, 4: 27.1 / 29.1, 6: 32.0 / 33.3; 8: 38.5 / 38.3.
+// Tokens up to which the MoE layer runs moe_down_combine_kernel after the
+// separate router and grouping. Each token reads its 8 experts' down weights
+// itself (experts two tokens share are read twice), which the launches it
+// saves outweigh up to here. Omni MoE layer by graph replay, weights cached,
+// against the down projection (quantizing its own h rows up to 4 tokens) then
+// combine: 1 token 14.3 against 15.8 us, 2: 19.0 / 21.1, 3: 22.6 / 24.8,
+// 4: 27.1 / 29.1, 6: 32.0 / 33.3; 8: 38.5 / 38.3.
 constexpr int64_t kDownCombineTokens = 6;
+// Tokens up to which the layer is moe_route_gate_up_kernel then
+// moe_down_combine_kernel (top-8 of 128 experts). Omni MoE layer (hidden
+// 2048, inter 768) by graph replay, weights cached, against the router and
+// grouping, expert_decode_kernel and moe_down_combine_kernel (up to 6 tokens)
+// or the expert kernels then combine: 1 token 11.5 against 14.1 us, 4: 20.0 /
+// 27.8, 6: 25.0 / 32.4, 7: 29.1 / 37.3, 8: 30.8 / 38.5, 10: 36.4 / 43.8,
+// 12: 40.1 / 46.2; 16: 52.0 / 51.9.
+constexpr int64_t kRouteGateUpTokens = 12;
+
+bool down_combine_shape(int topk, int k, int n) {
+  return topk == 8 && k % 256 == 0 && k <= kDownCombineMaxK && n % 8 == 0;
+}
 
 bool down_combine_fusable(int64_t tokens, int topk, int k, int n) {
-  return tokens >= 1 && tokens <= kDownCombineTokens && topk == 8 && k % 256 == 0 && k <= kDownCombineMaxK &&
-         n % 8 == 0;
+  return tokens >= 1 && tokens <= kDownCombineTokens && down_combine_shape(topk, k, n);
+}
+
+bool route_gate_up_fusable(int64_t tokens, int topk, int experts, int k, int n) {
+  return tokens >= 1 && tokens <= kRouteGateUpTokens && topk == 8 && experts == 128 && k % 256 == 0 &&
+         k <= kRouteGateUpMaxK && n % 32 == 0 && down_combine_shape(topk, n, k);
+}
+
+hipError_t launch_route_gate_up(const void* logits, int dtype, int64_t tokens, const uint16_t* x,
+                                const uint32_t* gate_w, const float* gate_s, const uint32_t* up_w,
+                                const float* up_s, int k, int n, float* routes, float* order, uint16_t* h,
+                                hipStream_t stream) {
+  if (!route_gate_up_fusable(tokens, 8, 128, k, n)) return hipErrorInvalidValue;
+  // 4 waves, 32 columns (graph replay of the layer at hidden 2048, inter 768,
+  // 1-6 tokens: 11.4-25.3 us against 13.3-37.9 with 8 waves and 16 columns;
+  // 64 columns or 2 waves within a microsecond either way)
+  constexpr int NW = 4, RW = 32;
+  const int slices = n / RW;
+  moe_route_gate_up_kernel<NW, RW><<<(unsigned)(tokens * 8 * slices), NW * 64, 0, stream>>>(
+      logits, dtype, (int)tokens, x, gate_w, gate_s, up_w, up_s, k / 256, n, slices, routes, order, h);
+  return hipGetLastError();
 }
 
 hipError_t launch_down_combine(const uint16_t* h, const uint32_t* w, const float* ws, const float* routes,
                                const float* order, int64_t tokens, int topk, int k, int n, uint16_t* out,
                                hipStream_t stream) {
-  if (!down_combine_fusable(tokens, topk, k, n)) return hipErrorInvalidValue;
-  constexpr int RW = 8;
-  const int slices = n / RW;
-  moe_down_combine_kernel<RW><<<(unsigned)(tokens * slices), 512, 0, stream>>>(h, w, ws, routes, order, k / 256, n,
-                                                                              slices, out);
+  if (tokens < 1 || tokens > kRouteGateUpTokens || !down_combine_shape(topk, k, n)) return hipErrorInvalidValue;
+  // 16 columns per workgroup where they divide n (1-6 tokens: 0.5-2.5 us
+  // less per layer than 8; 32 within half a microsecond of 16)
+  auto go = [&](auto kernel, int width) {
+    const int slices = n / width;
+    kernel<<<(unsigned)(tokens * slices), 512, 0, stream>>>(h, w, ws, routes, order, k / 256, n, slices, out);
+  };
+  if (n % 16 == 0)
+    go(moe_down_combine_kernel<16>, 16);
+  else
+    go(moe_down_combine_kernel<8>, 8);
   return hipGetLastError();
 }
 

@@ -121,6 +121,17 @@ bool expert_down_h_fusable(int64_t routes, int k, int n);
 // the combine order the grouping wrote: launch_prepare of h, launch_expert_i4
 // (input_routed 1) and launch_combine in one, with the same output.
 bool down_combine_fusable(int64_t tokens, int topk, int k, int n);
+// The MoE layer's router, Q1(x) and fused gate/up + SwiGLU for as many tokens
+// (top-8 of 128 experts) in one launch: the routes and the combine order as
+// launch_route and the grouping write them, and h [tokens * 8][n] as
+// launch_expert_gate_up writes it. route_gate_up_fusable (k = hidden, n =
+// inter) holds when the whole layer runs as this launch then
+// launch_down_combine, which accepts these token counts too.
+bool route_gate_up_fusable(int64_t tokens, int topk, int experts, int k, int n);
+hipError_t launch_route_gate_up(const void* logits, int dtype, int64_t tokens, const uint16_t* x,
+                                const uint32_t* gate_w, const float* gate_s, const uint32_t* up_w,
+                                const float* up_s, int k, int n, float* routes, float* order, uint16_t* h,
+                                hipStream_t stream);
 hipError_t launch_down_combine(const uint16_t* h, const uint32_t* w, const float* ws, const float* routes,
                                const float* order, int64_t tokens, int topk, int k, int n, uint16_t* out,
                                hipStream_t stream);

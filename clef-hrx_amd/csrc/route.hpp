@@ -144,7 +144,7 @@ constexpr int kRouteTokens16 = 16;
 // the block) + rank] (topk <= 8).
 __device__ __forceinline__ void route_body16(const void* __restrict__ logits, int dtype, int64_t tokens,
                                              int experts, int topk, float* __restrict__ routes, int64_t block,
-                                             int* ids = nullptr) {
+                                             int* ids = nullptr, bool write_routes = true) {
   const int lane = threadIdx.x & 63, li = lane & 15;
   const int64_t t = block * kRouteTokens16 + (threadIdx.x >> 4);
   const bool live = t < tokens;  // every lane stays on for the row reductions
@@ -211,9 +211,11 @@ __device__ __forceinline__ void route_body16(const void* __restrict__ logits, in
   float sum = 0.0f;
   for (int r = 0; r < topk; ++r) sum = sum + __shfl(p, row0 + r, 64);
   if (live && li < topk) {
-    float* out = routes + t * 2 * topk;
-    out[li] = (float)rid;
-    out[topk + li] = bf16_round(p / sum);
+    if (write_routes) {
+      float* out = routes + t * 2 * topk;
+      out[li] = (float)rid;
+      out[topk + li] = bf16_round(p / sum);
+    }
     if (ids != nullptr) ids[8 * (threadIdx.x >> 4) + li] = rid;
   }
 }

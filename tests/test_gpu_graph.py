@@ -17,11 +17,13 @@ def randn(shape, std, seed):
     return (torch.randn(shape, generator=g, device="cuda") * std).to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("t,pm,pn", [(256, 256, 1024), (512, 2048, 6144)])
+@pytest.mark.parametrize("t,pm,pn", [(4, 4, 1024), (256, 256, 1024), (512, 2048, 6144)])
 def test_graph_replays_match_eager(t, pm, pn):
-    """256 tokens and a 256 x 1024 projection take the few-rows kernels (32-slot
-    expert tiles, the K-split GEMM); 512 tokens and a 2048 x 6144 projection
-    take the 128-slot expert kernels and the persistent GEMM."""
+    """4 tokens and a 4 x 1024 projection take the decode kernels (the MoE
+    block as two kernels, the dot-product GEMM); 256 tokens and a 256 x 1024
+    projection the few-rows kernels (32-slot expert tiles, the K-split GEMM);
+    512 tokens and a 2048 x 6144 projection the 128-slot expert kernels and
+    the persistent GEMM."""
     d, inter = 512, 256
     gate = clef_i4.load_quantized_weight(randn((128 * inter, d), 0.02, 1))
     up = clef_i4.load_quantized_weight(randn((128 * inter, d), 0.02, 2))

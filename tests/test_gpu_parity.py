@@ -728,15 +728,17 @@ def test_combine_matches_oracle(ordered, topk, width):
 
 
 @pytest.mark.parametrize("tokens,hidden,inter", [(1, 2048, 768), (2, 512, 256), (4, 2048, 768), (5, 512, 256),
-                                                 (6, 512, 1024), (7, 512, 256), (3, 512, 2048), (16, 512, 256),
+                                                 (6, 512, 1024), (7, 512, 256), (12, 2048, 768), (13, 2048, 768),
+                                                 (3, 512, 2048), (16, 512, 256),
                                                  (17, 512, 256), (32, 512, 256), (33, 512, 256),
                                                  (96, 2048, 768), (300, 1024, 512),
                                                  (256, 512, 256), (257, 512, 256), (4160, 512, 256)])
 def test_moe_layer_matches_oracle(tokens, hidden, inter):
     """Whole Omni INT4 MoE block (src/omni.rs:762-857) bit-exact vs the oracle.
-    Up to 6 tokens the down projection, its quantizer and combine run as one
-    kernel (inter up to 1024; 7 tokens do not); with inter 2048 up to 4
-    tokens the down projection quantizes its own h rows; 32 and 33 tokens sit on
+    Up to 12 tokens (inter up to 1024) the block is two kernels: the router,
+    Q1(x) and gate/up + SwiGLU, then the down projection, its quantizer and
+    combine; 13 tokens take the separate router and grouping; with inter 2048
+    up to 4 tokens the down projection quantizes its own h rows; 32 and 33 tokens sit on
     either side of the VALU decode expert kernels' limit, 256 and 257 tokens
     (2048 and 2056 routed rows) on either side of the switch from 32-slot to
     128-slot expert tiles; 4160 tokens (65 blocks of 64) take the grouping
@@ -760,14 +762,16 @@ def test_moe_layer_matches_oracle(tokens, hidden, inter):
 
 @pytest.mark.parametrize("tokens,hidden,inter,topk", [
     (12, 512, 256, 4), (300, 512, 256, 6), (700, 512, 256, 2), (40, 512, 256, 16), (20, 512, 256, 24),
-    (64, 5120, 256, 8), (300, 4352, 256, 8), (9, 6144, 256, 4)])
+    (64, 5120, 256, 8), (300, 4352, 256, 8), (9, 6144, 256, 4), (3, 4352, 256, 8), (5, 3072, 512, 8)])
 def test_moe_layer_other_topk_and_wide_hidden(tokens, hidden, inter, topk):
     """The MoE block off the Omni shape, bit-exact against the oracle.
     topk other than 8 runs the generic grouping and combine kernels (the
     routing workgroup groups only top-8 routes); topk above 16 takes the
     wave-per-token router. hidden above 4096 (16 groups of 256) runs the
     router, the grouping and the quantizer of x as three launches instead of
-    the router beside the quantizer."""
+    the router beside the quantizer; above hidden 2048, up to 6 tokens run
+    the router (with the grouping up to hidden 4096), the gate/up kernel and
+    one kernel for the down projection, its quantizer and combine."""
     rng = np.random.default_rng(tokens * 31 + hidden + topk)
     x = randn_bf16(rng, (tokens, hidden))
     logits = BF(rng.standard_normal((tokens, 128)).astype(np.float32))
