@@ -29,12 +29,13 @@ hipError_t launch_prepare(const uint16_t* x, int64_t rows, int width, int stride
 bool route_prepare_fusable(int width);
 // With `groups` non-NULL (route_group_fusable) the routing workgroup also
 // writes the grouping tables and tile schedule (tiles of `bm` slots), as
-// launch_group_routes would.
+// launch_group_routes would. With `counts16` non-NULL (top-8) it writes the
+// per-16-token expert counts launch_group_counted reads.
 bool route_group_fusable(int64_t tokens, int topk);
 hipError_t launch_route_prepare(const void* logits, int dtype, int64_t tokens, int experts, int topk,
                                 float* routes, const uint16_t* x, int width, int stride, uint32_t* out,
                                 hipStream_t stream, float* groups = nullptr, float* order = nullptr,
-                                int32_t* schedule = nullptr, int bm = 0);
+                                int32_t* schedule = nullptr, int bm = 0, int* counts16 = nullptr);
 hipError_t launch_prepare_swiglu(const uint16_t* gate, const uint16_t* up, int64_t rows, int width,
                                  int stride, int bits, uint32_t* out, hipStream_t stream);
 hipError_t launch_prepare_attention_gate(const uint16_t* x, const uint16_t* q_gate, int64_t rows, int width,
@@ -84,6 +85,14 @@ hipError_t launch_router_gate(const uint16_t* x, const uint16_t* w, int64_t toke
 hipError_t launch_route(const void* logits, int dtype, int64_t tokens, int experts, int topk,
                         float* routes, hipStream_t stream);
 size_t group_workspace_bytes(int64_t tokens);
+// The grouping of top-8 routes from the per-16-token expert counts that
+// launch_route_prepare wrote (counts16 [ceil(tokens / 16)][128] int32,
+// group_counted_bytes): the scan and the scatter in one launch, with the same
+// outputs as launch_group_routes. For group_counted_fusable token counts.
+bool group_counted_fusable(int64_t tokens, int topk);
+size_t group_counted_bytes(int64_t tokens);
+hipError_t launch_group_counted(const float* routes, int64_t tokens, const int* counts16, float* groups,
+                                float* order, int32_t* schedule, int schedule_bm, hipStream_t stream);
 // With `schedule` non-NULL the scan also writes the grouped expert GEMM's tile
 // schedule (as launch_expert_schedule, tiles of schedule_bm slots).
 hipError_t launch_group_routes(const float* routes, int64_t tokens, int topk, float* groups,

@@ -301,6 +301,104 @@ __global__ __launch_bounds__(64) void group_scatter_kernel(const float* __restri
   }
 }
 
+// The scan and the scatter of top-8 routes in one launch, from counts16
+// [rows16][128] (tokens of 16-token block r routed to expert e, written by
+// the router): workgroup b (1024 threads) handles the 64-token block b.
+// Its 32 row groups of 32 threads each read every 16-token count row with
+// 16-byte loads (thread q of a group four experts), keeping the sum of the
+// rows of earlier tokens (r < 4b: the list offsets of this block) and of
+// all rows (the experts' counts); the 32 partial sums meet in LDS. Wave 0
+// then lists the block's tokens as group_scatter_kernel<8> does (masks of
+// 64 tokens, rank = offset + popcount below), every workgroup writes its
+// share of the tile schedule from the counts, and workgroup 0 writes
+// groups[e][0]. Same outputs as the count, scan and scatter launches.
+__global__ __launch_bounds__(1024) void group_scatter_scan_kernel(const float* __restrict__ routes, int64_t tokens,
+                                                                  const int* __restrict__ counts16, int64_t rows16,
+                                                                  float* __restrict__ groups, float* __restrict__ order,
+                                                                  int bm, int32_t* __restrict__ schedule) {
+  constexpr int KT = 8, RG = 32, U = 8;
+  __shared__ int part[2][RG][128];
+  __shared__ unsigned long long masks[128];
+  __shared__ int offs[128];
+  __shared__ int first[129];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t t = (int64_t)blockIdx.x * kGroupBlock + lane;
+  const bool live = tid < 64 && t < tokens;
+  float id[KT];
+#pragma unroll
+  for (int r = 0; r < KT; ++r) id[r] = live ? routes[t * 2 * KT + r] : -1.0f;
+  if (tid < 128) masks[tid] = 0ull;
+  {
+    const int g = tid / 32, q = tid % 32;
+    const int64_t split = (int64_t)blockIdx.x * (kGroupBlock / 16);
+    int pre[4] = {0, 0, 0, 0}, tot[4] = {0, 0, 0, 0};
+    for (int64_t r0 = g; r0 < rows16; r0 += RG * U) {
+      int4 c[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t r = r0 + (int64_t)RG * u;
+        c[u] = r < rows16 ? *reinterpret_cast<const int4*>(counts16 + r * 128 + 4 * q) : make_int4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool early = r0 + (int64_t)RG * u < split;
+        tot[0] += c[u].x, tot[1] += c[u].y, tot[2] += c[u].z, tot[3] += c[u].w;
+        if (early) pre[0] += c[u].x, pre[1] += c[u].y, pre[2] += c[u].z, pre[3] += c[u].w;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      part[0][g][4 * q + i] = pre[i];
+      part[1][g][4 * q + i] = tot[i];
+    }
+  }
+  __syncthreads();
+  // threads 0..127: expert tid's count (tile_prefix's holders); 128..255:
+  // the list offset of this block for expert tid - 128
+  int count = 0;
+  if (tid < 256) {
+    const int e = tid & 127;
+    int sum = 0;
+#pragma unroll
+    for (int g = 0; g < RG; ++g) sum += part[tid < 128 ? 1 : 0][g][e];
+    if (tid < 128)
+      count = sum;
+    else
+      offs[e] = sum;
+  }
+  if (blockIdx.x == 0 && tid < 128) groups[(int64_t)tid * (tokens + 1)] = (float)count;
+  tile_prefix(count, tid < 128, tid & 127, bm, first);
+  if (blockIdx.x == 0 && tid == 0) schedule[0] = first[128];
+  if (blockIdx.x == 0 && tid < kSchedEntries - kSchedClaims) schedule[kSchedClaims + tid] = 0;
+  tile_entries(first, bm, (int)(blockIdx.x * 1024 + tid), (int)(gridDim.x * 1024), schedule);
+  if (tid >= 64) return;
+  int ex[KT];
+#pragma unroll
+  for (int r = 0; r < KT; ++r) {
+    ex[r] = route_expert(id[r]);
+    if (ex[r] >= 0) atomicOr(&masks[ex[r]], 1ull << lane);
+  }
+  // one wave: its LDS operations complete in order
+  if (!live) return;
+  const unsigned long long below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int r = 0; r < KT; ++r) {
+    const int e = ex[r];
+    bool last = e >= 0;
+#pragma unroll
+    for (int q = r + 1; q < KT; ++q) last = last && ex[q] != e;
+    if (!last) continue;
+    const int rank = offs[e] + __popcll(masks[e] & below);
+    groups[(int64_t)e * (tokens + 1) + 1 + rank] = (float)(t * KT + r);
+    if (order) {
+      int less = 0;
+#pragma unroll
+      for (int q = 0; q < KT; ++q) less += id[q] < (float)e ? 1 : 0;
+      order[t * KT + less] = (float)r;
+    }
+  }
+}
+
 // The three passes in one workgroup of 16 waves for up to 512 tokens at
 // top-8: one launch instead of three, where each pass is a few microseconds
 // of latency. (Beyond that the scattered list writes of a single CU cost more
@@ -600,10 +698,22 @@ hipError_t launch_route(const void* logits, int dtype, int64_t tokens, int exper
   return hipGetLastError();
 }
 
+// Tokens up to which the MoE layer groups from the router's per-16-token
+// counts (route_prepare_kernel, then group_scatter_scan_kernel) instead of
+// the count, scan and scatter launches. Every workgroup of the second
+// launch reads all ceil(tokens / 16) count rows (512 bytes each).
+constexpr int64_t kGroupCountedTokens = 8192;
+
+bool group_counted_fusable(int64_t tokens, int topk) {
+  return topk == 8 && tokens > kGroupCountScanBlocks * kGroupBlock && tokens <= kGroupCountedTokens;
+}
+
 size_t group_workspace_bytes(int64_t tokens) {
   const int64_t blocks = (tokens + kGroupBlock - 1) / kGroupBlock;
   return (size_t)blocks * 128 * sizeof(int);
 }
+
+size_t group_counted_bytes(int64_t tokens) { return (size_t)((tokens + 15) / 16) * 128 * sizeof(int); }
 
 namespace {
 __global__ __launch_bounds__(256) void route_slots_kernel(const float* __restrict__ routes, int64_t slots_n,
@@ -655,6 +765,15 @@ hipError_t launch_group_routes(const float* routes, int64_t tokens, int topk, fl
   else
     group_scatter_kernel<0><<<(unsigned)blocks, 64, 0, stream>>>(routes, tokens, topk, counts, groups, order,
                                                                  schedule_bm, scatter_schedule);
+  return hipGetLastError();
+}
+
+hipError_t launch_group_counted(const float* routes, int64_t tokens, const int* counts16, float* groups,
+                                float* order, int32_t* schedule, int schedule_bm, hipStream_t stream) {
+  if (!group_counted_fusable(tokens, 8) || schedule == nullptr) return hipErrorInvalidValue;
+  const int64_t blocks = (tokens + kGroupBlock - 1) / kGroupBlock;
+  group_scatter_scan_kernel<<<(unsigned)blocks, 1024, 0, stream>>>(routes, tokens, counts16, (tokens + 15) / 16,
+                                                                   groups, order, schedule_bm, schedule);
   return hipGetLastError();
 }
 

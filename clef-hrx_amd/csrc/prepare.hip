@@ -520,18 +520,38 @@ __global__ __launch_bounds__(256) void prepare_loop_kernel(Src src, int64_t rows
 // GPU instead of running one after the other.
 // With `groups` non-NULL (at most 16 tokens at top-8: one routing
 // workgroup) that workgroup also groups the routes it wrote (group_small).
+// With `counts16` non-NULL (top-8) routing workgroup b also writes
+// counts16[b][e], the number of its 16 tokens routed to expert e, for
+// group_scatter_scan_kernel.
 __global__ __launch_bounds__(256) void route_prepare_kernel(const void* __restrict__ logits, int dtype,
                                                             int64_t tokens, int experts, int topk,
                                                             float* __restrict__ routes, int64_t route_blocks,
                                                             PlainSource src, int width, int out_words,
                                                             uint32_t* __restrict__ out, float* groups, float* order,
-                                                            int32_t* schedule, int bm) {
+                                                            int32_t* schedule, int bm, int* counts16) {
   if ((int64_t)blockIdx.x < route_blocks) {
     if (groups != nullptr) {  // topk 8, one routing workgroup: route_body16
       __shared__ int ids[128];
       route_impl::route_body16(logits, dtype, tokens, experts, topk, routes, 0, ids);
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // ids written; the route stores may drain
       group_small(ids, (int)tokens, groups, order, schedule, bm);
+      return;
+    }
+    if (counts16 != nullptr) {  // topk 8: the block's expert counts from its ids
+      __shared__ int ids[128];
+      __shared__ uint32_t masks16[128];  // bit i: token i of the block names the expert
+      const int tid = threadIdx.x;
+      if (tid < 128) masks16[tid] = 0u;
+      route_impl::route_body16(logits, dtype, tokens, experts, topk, routes, blockIdx.x, ids);
+      __syncthreads();
+      const int64_t left = tokens - (int64_t)blockIdx.x * route_impl::kRouteTokens16;
+      const int n = 8 * (int)(left < route_impl::kRouteTokens16 ? left : route_impl::kRouteTokens16);
+      if (tid < n) {
+        const int e = ids[tid];
+        if (e >= 0 && e < 128) atomicOr(&masks16[e], 1u << (tid >> 3));
+      }
+      __syncthreads();
+      if (tid < 128) counts16[(int64_t)blockIdx.x * 128 + tid] = __popc(masks16[tid]);
       return;
     }
     route_impl::route_block(logits, dtype, tokens, experts, topk, routes, blockIdx.x);
@@ -647,9 +667,11 @@ bool route_group_fusable(int64_t tokens, int topk) { return topk == 8 && tokens 
 
 hipError_t launch_route_prepare(const void* logits, int dtype, int64_t tokens, int experts, int topk,
                                 float* routes, const uint16_t* x, int width, int stride, uint32_t* out,
-                                hipStream_t stream, float* groups, float* order, int32_t* schedule, int bm) {
+                                hipStream_t stream, float* groups, float* order, int32_t* schedule, int bm,
+                                int* counts16) {
   if (!route_prepare_fusable(width)) return hipErrorInvalidValue;
   if (groups != nullptr && !route_group_fusable(tokens, topk)) return hipErrorInvalidValue;
+  if (counts16 != nullptr && (groups != nullptr || topk != 8)) return hipErrorInvalidValue;
   const int per_block = 16 / (width / 256);
   const int64_t blocks = (tokens + per_block - 1) / per_block;
   const int64_t prep = blocks < 2048 ? blocks : 2048;
@@ -657,7 +679,7 @@ hipError_t launch_route_prepare(const void* logits, int dtype, int64_t tokens, i
   const int64_t route_blocks = (tokens + per - 1) / per;
   route_prepare_kernel<<<(unsigned)(route_blocks + prep), 256, 0, stream>>>(
       logits, dtype, tokens, experts, topk, routes, route_blocks, PlainSource{x}, width, stride / 8, out, groups, order,
-      schedule, bm);
+      schedule, bm, counts16);
   return hipGetLastError();
 }
 

@@ -732,7 +732,8 @@ def test_combine_matches_oracle(ordered, topk, width):
                                                  (3, 512, 2048), (16, 512, 256),
                                                  (17, 512, 256), (32, 512, 256), (33, 512, 256),
                                                  (96, 2048, 768), (300, 1024, 512),
-                                                 (256, 512, 256), (257, 512, 256), (4160, 512, 256)])
+                                                 (256, 512, 256), (257, 512, 256), (1100, 512, 256),
+                                                 (4160, 512, 256)])
 def test_moe_layer_matches_oracle(tokens, hidden, inter):
     """Whole Omni INT4 MoE block (src/omni.rs:762-857) bit-exact vs the oracle.
     Up to 12 tokens (inter up to 1024) the block is two kernels: the router,
@@ -741,8 +742,8 @@ def test_moe_layer_matches_oracle(tokens, hidden, inter):
     up to 4 tokens the down projection quantizes its own h rows; 32 and 33 tokens sit on
     either side of the VALU decode expert kernels' limit, 256 and 257 tokens
     (2048 and 2056 routed rows) on either side of the switch from 32-slot to
-    128-slot expert tiles; 4160 tokens (65 blocks of 64) take the grouping
-    scan with one workgroup per expert."""
+    128-slot expert tiles; 1100 and 4160 tokens group from the router's
+    per-16-token expert counts (partial last blocks of 16 and 64 tokens)."""
     rng = np.random.default_rng(tokens + hidden)
     x = randn_bf16(rng, (tokens, hidden))
     logits = BF(rng.standard_normal((tokens, 128)).astype(np.float32))
