@@ -15,6 +15,7 @@
 #include "gemm_dma.hpp"
 #include "gemm_dmah.hpp"
 #include "expert_persist.hpp"
+#include "group.hpp"
 #include "kernels.hpp"
 #include "launch.hpp"
 #include "route.hpp"
@@ -1898,7 +1899,8 @@ __global__ __launch_bounds__(NW * 64) void moe_route_gate_up_kernel(
     for (int q = 0; q < KT; ++q) less += ids[tt * KT + q] < e ? 1 : 0;
     order[tt * KT + less] = (float)(threadIdx.x % KT);
   }
-  const int e = ids[t * KT + r];
+  // an invalid id (a logit row of NaN) names no expert: any in-range weights
+  const int e = ids[t * KT + r] >= 0 && ids[t * KT + r] < 128 ? ids[t * KT + r] : 0;
   const int64_t nrow = (int64_t)e * n + c0;
   const __amdgpu_buffer_rsrc_t g_rsrc = make_rsrc(gw + (nrow / 128) * kb * 4096, (uint32_t)(kb * 16384));
   const __amdgpu_buffer_rsrc_t u_rsrc = make_rsrc(uw + (nrow / 128) * kb * 4096, (uint32_t)(kb * 16384));
@@ -1999,8 +2001,9 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
   const int seg = lane & 7, r8 = lane >> 3;
   const float* rt = routes + (int64_t)t * 2 * KT;
   // this wave's slot, its expert and weight rows
-  const int slot = (int)order[(int64_t)t * KT + wave];
-  const int e = (int)rt[slot];
+  const int slot = order_slot(order[(int64_t)t * KT + wave], KT);
+  const int e_id = route_expert(rt[slot]);
+  const int e = e_id >= 0 ? e_id : 0;  // a slot naming no expert: any in-range weights (unspecified output)
   const int64_t nrow = (int64_t)e * n + c0;
   const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(w + (nrow / 128) * kb * 4096, (uint32_t)(kb * 16384));
   const int w_voff = (int)(nrow % 128 + r8) * 128 + 16 * seg;
@@ -2045,7 +2048,7 @@ __global__ __launch_bounds__(512) void moe_down_combine_kernel(
     float acc2 = 0.0f;
 #pragma unroll
     for (int j = 0; j < KT; ++j) {
-      const float p = rt[KT + (int)order[(int64_t)t * KT + j]];
+      const float p = rt[KT + order_slot(order[(int64_t)t * KT + j], KT)];
       acc2 = bf16_round(acc2 + bf16_round(vals[j][col] * p));
     }
     out[(int64_t)t * n + c0 + col] = (uint16_t)f32_to_bf16(acc2);

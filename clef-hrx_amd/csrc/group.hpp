@@ -17,6 +17,14 @@ __device__ __forceinline__ int route_expert(float id) {
   return (id > -1.0f && id < 128.0f) ? (int)id : -1;
 }
 
+// Slot named by combine-order entry `o` of a token with `topk` slots. The
+// grouping writes an entry for each expert a token names, so a token naming
+// an expert twice or naming none (logit rows with NaN, or with fewer than
+// topk values above -FLT_MAX) leaves entries unwritten; an entry outside
+// [0, topk) then reads slot 0, never memory past the token's rows. Such a
+// token's output is unspecified, as in the reference.
+__device__ __forceinline__ int order_slot(float o, int topk) { return o >= 0.0f && o < (float)topk ? (int)o : 0; }
+
 // The expert GEMM's tile list from the experts' counts: tiles of bm slots,
 // schedule = [total] then (expert, first slot) per tile, experts ascending.
 //

@@ -563,7 +563,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     int rank[KT];
     if (order) {
 #pragma unroll
-      for (int j = 0; j < KT; ++j) rank[j] = (int)order[t * KT + j];
+      for (int j = 0; j < KT; ++j) rank[j] = order_slot(order[t * KT + j], KT);
     } else {
       float ids[KT];
 #pragma unroll
@@ -611,7 +611,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   for (int j = 0; j < topk; ++j) {
     int rank;
     if (order) {
-      rank = (int)order[t * topk + j];
+      rank = order_slot(order[t * topk + j], topk);
     } else {
       // j-th smallest expert id (kernels/omni_combine.loom:50-77).
       float best = 1000000.0f;

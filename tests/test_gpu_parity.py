@@ -788,6 +788,52 @@ def test_moe_layer_other_topk_and_wide_hidden(tokens, hidden, inter, topk):
     assert_same_u16(bf16_host(got), want, f"moe layer tokens={tokens} hidden={hidden} topk={topk}")
 
 
+@pytest.mark.parametrize("tokens", [5, 20, 300, 1100])
+def test_moe_layer_degenerate_logit_rows(tokens):
+    """Logit rows that make a token name an expert twice (three finite
+    logits, the rest -inf: once those three are taken the reset -FLT_MAX
+    slots win again) or no expert (all NaN) leave combine-order entries
+    unwritten. With the workspace filled with 0xFF bytes first (so unwritten
+    entries hold NaN), the layer must keep every access in range, route
+    every token as the oracle's router does, and give the other tokens'
+    outputs bit for bit: every stage is token-local, so the oracle runs on
+    the other tokens alone. The degenerate tokens' outputs are unspecified
+    (as in the reference) and not compared. 5 tokens take the two-kernel
+    layer, 20 the decode kernels, 300 and 1100 the grouped paths."""
+    hidden, inter = 512, 256
+    rng = np.random.default_rng(tokens + 77)
+    x = randn_bf16(rng, (tokens, hidden))
+    lg = rng.standard_normal((tokens, 128)).astype(np.float32)
+    bad = np.zeros(tokens, dtype=bool)
+    bad[1::4] = True
+    for i in np.nonzero(bad)[0]:
+        if i % 8 == 1:
+            lg[i] = np.nan
+        else:
+            lg[i] = -np.inf
+            lg[i, rng.choice(128, 3, replace=False)] = rng.standard_normal(3)
+    logits = BF(lg)
+    gate = packed_experts(rng, inter, hidden)
+    up = packed_experts(rng, inter, hidden)
+    down = packed_experts(rng, hidden, inter)
+    layer = clef_i4.MoeLayer(dev_weight(*gate, 128 * inter, hidden), dev_weight(*up, 128 * inter, hidden),
+                             dev_weight(*down, 128 * hidden, inter))
+    layer.workspace(tokens, DEV).fill_(0xFF)
+    routes = torch.empty((tokens, 16), dtype=torch.float32, device=DEV)
+    got = bf16_host(layer(to_dev_bf16(x), to_dev_bf16(logits), routes_out=routes))
+    want_routes = oracle.route(logits, 8)
+    got_routes = routes.cpu().numpy()
+    assert np.array_equal(got_routes[:, :8], want_routes[:, :8]), "route ids"
+    nan_rows = np.isnan(lg).all(axis=1)  # their probabilities are NaN, whose bits are not part of the contract
+    assert np.isnan(got_routes[nan_rows, 8:]).all()
+    assert np.array_equal(got_routes[~nan_rows].view(np.uint32), want_routes[~nan_rows].view(np.uint32)), "routes"
+    ids = want_routes[:, :8]
+    assert all(len(set(ids[i].tolist())) < 8 for i in np.nonzero(bad)[0]), "every degenerate row repeats or lacks ids"
+    good = ~bad
+    want, _ = oracle.moe_layer(x[good], logits[good], gate, up, down)
+    assert_same_u16(got[good], want, f"moe layer tokens={tokens}, the well-formed tokens")
+
+
 def test_moe_layer_closed_form():
     """The MoE block on constant rows (every code +-7, silu(g) = g for the
     gates >= 17 these inputs give) against the closed form of
