@@ -323,7 +323,9 @@ size_t clef_moe_expert_workspace_bytes(int64_t tokens, int32_t topk);
  * route grouping shape"; k % 256 == 0 && n % 256 == 0 && k, n >= 256 &&
  * stride >= k && stride % 32 == 0 -> "unsupported Omni expert tile shape";
  * the packed codes of `a` (rows * stride / 2 bytes) below 2 GiB -> "expert
- * activation operand of 2 GiB or more ...". */
+ * activation operand of 2 GiB or more ...". `groups` must hold lists as
+ * clef_moe_group_routes writes them (counts <= tokens, route ordinals below
+ * tokens * topk): the ordinals address output rows and are not checked. */
 int clef_moe_expert_i4(const uint32_t* a, int32_t stride, const float* a_scales,
                        const uint32_t* w_tiled, const float* w_scales, const float* groups,
                        int64_t tokens, int32_t topk, int32_t k, int32_t n, int32_t input_routed,
@@ -381,7 +383,10 @@ int clef_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h
  * routes). Replaces Engine::omni_combine / omni_combine_ordered
  * (src/omni.rs:246-278, 535-556) and kernels/omni_combine.loom,
  * omni_combine_ordered.loom. Preconditions: width % 8 == 0, 1 <= topk <=
- * 128, tokens >= 1 -> "unsupported ordered Omni accumulation". */
+ * 128, tokens >= 1 -> "unsupported ordered Omni accumulation". An order
+ * entry outside [0, topk) (the grouping leaves entries unwritten for a
+ * token that names an expert twice or none) reads slot 0; such a token's
+ * output is unspecified. */
 int clef_moe_combine(const uint16_t* values, const float* routes, const float* order,
                      int64_t tokens, int32_t width, int32_t topk, uint16_t* out,
                      clef_stream_t stream);
