@@ -162,6 +162,13 @@ __device__ __forceinline__ void radix4x2(float* v) {
   for (int q = 0; q < 4; ++q) radix4(v[q], v[q + 4], v[q + 8], v[q + 12]);
 }
 
+// Between the writes and the reads of a 16x16 transpose that one 16-lane
+// group makes in its own LDS rows. The group's lanes are in one wave, and the
+// LDS executes one wave's operations in issue order, so its reads see its
+// writes (and its later writes follow its reads) without a workgroup barrier;
+// this only keeps the compiler from moving memory operations across it.
+__device__ __forceinline__ void group_lds_order() { asm volatile("" ::: "memory"); }
+
 __device__ __forceinline__ uint32_t group_max16(uint32_t m) {
   // Reduce over the 16 lanes of a group (lanes differ in the low 4 bits): a
   // DPP row. quad_perm [1,0,3,2] and [2,3,0,1], then row_ror 4 and 8, leave

@@ -343,10 +343,10 @@ __global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       wrow[c] = make_float4(v[p][4 * c], v[p][4 * c + 1], v[p][4 * c + 2], v[p][4 * c + 3]);
-    __syncthreads();
+    group_lds_order();
 #pragma unroll
     for (int k = 0; k < 16; ++k) v[p][k] = buf[k * kPitch + L];
-    __syncthreads();
+    group_lds_order();
     radix4x2(v[p]);  // strides 16 and 64 (value k holds index L + 16k)
     if (on) {
 #pragma unroll
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int
     const bool on = active && grp < G;
 #pragma unroll
     for (int k = 0; k < 16; ++k) buf[k * kPitch + L] = v[p][k];
-    __syncthreads();
+    group_lds_order();
     float nat[16];
     const float4* rrow = reinterpret_cast<const float4*>(buf + L * kPitch);
 #pragma unroll
@@ -395,7 +395,7 @@ __global__ __launch_bounds__(256) void prepare_kernel(Src src, int64_t rows, int
       nat[4 * c + 2] = t.z;
       nat[4 * c + 3] = t.w;
     }
-    __syncthreads();
+    group_lds_order();
     if (on) store_group<BITS>(out, out + row * out_words, row, grp * 256 + 16 * L, width, nat, inv, valid);
   }
   if (active && grp0 == 0 && L == 0) scales_of<BITS>(out, rows, width, out_words)[row] = scale;
@@ -449,10 +449,10 @@ __device__ __forceinline__ void prepare_loop_body(Src src, int64_t rows, int wid
     float4* wrow = reinterpret_cast<float4*>(buf + L * kPitch);
 #pragma unroll
     for (int c = 0; c < 4; ++c) wrow[c] = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
-    __syncthreads();
+    group_lds_order();
 #pragma unroll
     for (int k = 0; k < 16; ++k) v[k] = buf[k * kPitch + L];
-    __syncthreads();
+    group_lds_order();
     radix4x2(v);  // strides 16 and 64 (value k holds index L + 16k)
     uint32_t mbits = 0;
     if (on) {
@@ -500,7 +500,11 @@ __device__ __forceinline__ void prepare_loop_body(Src src, int64_t rows, int wid
       nat[4 * c + 2] = t.z;
       nat[4 * c + 3] = t.w;
     }
-    __syncthreads();
+    // The next iteration's first LDS writes (this group's rows, then gmax
+    // after every wave has passed the barriers below) need no barrier here:
+    // the scale slots are rewritten only after the next gmax barrier, which
+    // every wave reaches after reading this iteration's scale.
+    group_lds_order();
     if (on) {
       store_group<BITS>(out, out + out_off, row, col, width, nat, inv, valid);
       if (grp == 0 && L == 0) scales_of<BITS>(out, rows, width, out_words)[row] = scale;
