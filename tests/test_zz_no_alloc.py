@@ -36,8 +36,9 @@ def test_static_scratch_layer_matches_workspace_layer():
     layer = clef_i4.MoeLayer(_weight(gen, 128 * inter, d), _weight(gen, 128 * inter, d),
                              _weight(gen, 128 * d, inter), topk=topk)
     # 600 tokens: 4800 routed rows on the 128-slot expert tiles; 97 tokens:
-    # 776 routed rows on the 32-slot tiles.
-    for tokens in (600, 97):
+    # 776 routed rows on the 32-slot tiles; 5 tokens: the two-kernel layer
+    # (each call smaller than the last, the scratch holding its contents).
+    for tokens in (600, 97, 5):
         print(f"static MoE layer tokens={tokens}", flush=True)
         need = clef_i4.lib().clef_moe_layer_workspace_bytes(tokens, d, inter, topk)
         assert need <= SCRATCH_BYTES, need
